@@ -1,0 +1,226 @@
+"""Benchmark: one Mamba2 SSD layer forward at the nemotron-h-8b shape on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu-baseline]
+
+A step is one call of mamba2_jax.kernels.mamba_chunk_scan_combined_fwd (the five
+stage kernels: chunk_cumsum, chunk_state, state_passing, bmm_chunk, chunk_scan)
+on synthetic inputs already resident in HBM, returning the output and the final
+states.  Prints ONE JSON line (rank 0): tokens/s, ms per layer, the roofline
+fraction of the dominant kernel (per-stage durations come from HIP events
+recorded on the launch stream between the stages, inside the timed region),
+the per-stage table, a decode-step measurement (c4: 256 in-place
+selective_state_update steps) and the CPU baseline (the oracle's NumPy
+restatement of the reference's naive path, timed on a bounded head sample on
+this host's cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mamba2-jax-pallas_amd"))
+
+METRIC = "SSD layer fwd ms + tokens/sec and % MFMA/HBM roofline, nemotron-h-8b shape"
+PEAK_HBM_GBS = 8000.0            # MI355X HBM3E, GB/s
+PEAK_MFMA_TFLOPS = {"bf16": 2500.0, "f32": 157.3}   # dense
+STAGES = ["chunk_cumsum", "chunk_state", "state_passing", "bmm_chunk", "chunk_scan"]
+
+
+def stage_work(cfg, with_init=False, with_z=False):
+    """Algorithmic (compulsory) HBM bytes and flops per launch of each stage, as
+    the combined path runs them (CB and the carried states in the input dtype)."""
+    s = 2 if cfg.dtype == "bf16" else 4
+    b, L, H, G, P, N, Q = (cfg.batch, cfg.seqlen, cfg.nheads, cfg.ngroups, cfg.headdim,
+                           cfg.dstate, cfg.chunk_size)
+    nc = math.ceil(L / Q)
+    S = b * nc * H * P * N
+    cq = b * H * nc * Q
+    w = {}
+    w["chunk_cumsum"] = (b * L * H * s + 8 * cq + 8 * H, 5 * b * L * H)
+    w["chunk_state"] = (b * L * H * P * s + b * L * G * N * s + 8 * cq + 4 * S,
+                        2 * b * L * H * P * N)
+    w["state_passing"] = (4 * S + 4 * b * H * nc + (4 * b * H * P * N if with_init else 0)
+                          + s * S + 4 * b * H * P * N, 2 * S)
+    w["bmm_chunk"] = (2 * b * L * G * N * s + s * b * nc * G * Q * Q, 2 * b * nc * G * Q * Q * N)
+    w["chunk_scan"] = (s * b * nc * G * Q * Q + b * L * H * P * s + 8 * cq + b * L * G * N * s
+                       + s * S + 4 * H + (b * L * H * P * s if with_z else 0) + 4 * b * L * H * P,
+                       b * nc * H * P * Q * (Q + 1) + 2 * b * L * H * N * P)
+    return w
+
+
+def cpu_baseline(cfg, heads, min_seconds=10.0, max_reps=20):
+    """The oracle's NumPy restatement of the reference naive path (float32), on
+    the first `heads` heads (whole groups) of the workload, scaled to all heads."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    from mamba2_jax import configs
+    from oracle import ssd_oracle as O
+    import dataclasses
+    hpg = cfg.nheads // cfg.ngroups
+    heads = max(hpg, (heads // hpg) * hpg)
+    sub = dataclasses.replace(cfg, nheads=heads, ngroups=heads // hpg)
+    d = configs.make_ssd_inputs(sub)
+    kw = dict(chunk_size=sub.chunk_size, dt_softplus=True, return_final_states=True,
+              io_dtype=sub.dtype, acc=np.float32)
+    O.ssd_combined(**d, **kw)                     # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < min_seconds and len(times) < max_reps):
+        t0 = time.perf_counter()
+        O.ssd_combined(**d, **kw)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times)) * cfg.nheads / heads
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    return {
+        "value": cfg.tokens / t, "unit": "tokens/s", "cores": threads, "kind": "port",
+        "ms_per_layer": t * 1e3,
+        "sample": (f"oracle NumPy float32 restatement of ssd_naive, {heads} of {cfg.nheads} heads "
+                   f"(whole groups), full L={cfg.seqlen}; median of {len(times)} runs "
+                   f"x {cfg.nheads / heads:g} (linear in heads); host affinity "
+                   f"{len(os.sched_getaffinity(0))} cpus, BLAS threads {threads}"),
+    }
+
+
+def bench_decode(steps=256, warmup=16):
+    """c4: `steps` consecutive in-place decode steps (batch 64, H 128, G 8, P 64, N 128)."""
+    import torch
+    from mamba2_jax import configs
+    from mamba2_jax.ops import selective_state_update
+    cfg = configs.DECODE
+    d = configs.make_decode_inputs(cfg, steps=steps)
+    dev = torch.device("cuda")
+    bf = lambda a: torch.from_numpy(a).to(dev).to(torch.bfloat16)
+    f = lambda a: torch.from_numpy(a).to(dev)
+    state = f(d["state"])
+    xs, zs, Bs, Cs, dts = bf(d["x"]), bf(d["z"]), bf(d["B"]), bf(d["C"]), f(d["dt"])
+    A, D, bias = f(d["A"]), f(d["D"]), f(d["dt_bias"])
+    for t in range(warmup):
+        selective_state_update(state, xs[t], dts[t], A, Bs[t], Cs[t], D=D, z=zs[t],
+                               dt_bias=bias, dt_softplus=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for t in range(steps):
+        selective_state_update(state, xs[t], dts[t], A, Bs[t], Cs[t], D=D, z=zs[t],
+                               dt_bias=bias, dt_softplus=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    b, H, G, P, N = cfg.batch, cfg.nheads, cfg.ngroups, cfg.headdim, cfg.dstate
+    by = 8 * b * H * P * N + b * H * P * (2 + 2 + 4) + b * H * 4 + 2 * b * G * N * 2 + 12 * H
+    return {"workload": "selective_state_update, batch 64, H 128, G 8, P 64, N 128, "
+                        "fp32 state in place, bf16 x/z/B/C, 256 consecutive steps",
+            "ms_per_step": ms, "tokens_per_s": b / (ms * 1e-3),
+            "hbm_gbs": by / (ms * 1e-3) / 1e9, "hbm_frac": by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "bytes_per_step": by}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=32)
+    args = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): "
+              "this build has no multi-GPU path; the SSD forward shards by head groups with no "
+              "communication, so per-GPU throughput is the one-GPU figure.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    from mamba2_jax import configs
+    from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
+
+    cfg = configs.CONFIGS[args.config]
+    dev = torch.device("cuda")
+    d = configs.make_ssd_inputs(cfg)
+    T = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
+    t = lambda a, dt=None: None if a is None else torch.from_numpy(a).to(dev).to(dt or torch.float32)
+    kw = dict(x=t(d["x"], T), dt=t(d["dt"], T), A=t(d["A"]), B=t(d["B"], T), C=t(d["C"], T),
+              D=t(d["D"]), dt_bias=t(d["dt_bias"]), initial_states=t(d["initial_states"]),
+              seq_idx=None if d["seq_idx"] is None else torch.from_numpy(d["seq_idx"]).to(dev),
+              cu_seqlens=None if d["cu_seqlens"] is None else torch.from_numpy(d["cu_seqlens"]).to(dev),
+              chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
+              return_varlen_states=d["cu_seqlens"] is not None)
+
+    for _ in range(args.warmup):
+        mamba_chunk_scan_combined_fwd(**kw)
+    K = args.steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(K)]
+    for e in evs:                                   # create the events outside the timed region
+        for x in e:
+            x.record()
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    g0.record()
+    for i in range(K):
+        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[i])
+    g1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms = g0.elapsed_time(g1) / K
+    stage_ms = {s: float(np.mean([evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(K)]))
+                for j, s in enumerate(STAGES)}
+
+    work = stage_work(cfg, with_init=d["initial_states"] is not None)
+    peak_mfma = PEAK_MFMA_TFLOPS[cfg.dtype]
+    stages = {}
+    for s in STAGES:
+        by, fl = work[s]
+        sec = stage_ms[s] * 1e-3
+        stages[s] = {"ms": stage_ms[s], "bytes": by, "gflop": fl / 1e9,
+                     "hbm_gbs": by / sec / 1e9, "hbm_frac": by / sec / 1e9 / PEAK_HBM_GBS,
+                     "mfma_tflops": fl / sec / 1e12, "mfma_frac": fl / sec / 1e12 / peak_mfma}
+    dom = max(STAGES, key=lambda s: stage_ms[s])
+    by, fl = work[dom]
+    ridge = peak_mfma * 1e12 / (PEAK_HBM_GBS * 1e9)
+    bound = "mfma" if fl / by > ridge else "hbm"
+    if bound == "hbm":
+        roof = {"bound": "hbm", "achieved": stages[dom]["hbm_gbs"], "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": stages[dom]["hbm_frac"]}
+    else:
+        roof = {"bound": "mfma", "achieved": stages[dom]["mfma_tflops"], "peak": peak_mfma,
+                "unit": "TFLOP/s", "frac": stages[dom]["mfma_frac"]}
+    roof.update({"kernel": dom, "algorithmic_bytes": by, "algorithmic_flop": fl,
+                 "avg_launch_ms": stage_ms[dom], "traffic": None})
+    tot_by = sum(w[0] for w in work.values())
+    res = {
+        "metric": METRIC, "value": cfg.tokens / (ms * 1e-3), "unit": "tokens/s",
+        "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": cfg.dtype, "data": "synthetic",
+        "config": {"workload": f"{cfg.name} SSD layer forward ({args.config})",
+                   "batch": cfg.batch, "seq_len": cfg.seqlen, "nheads": cfg.nheads,
+                   "ngroups": cfg.ngroups, "headdim": cfg.headdim, "dstate": cfg.dstate,
+                   "chunk_size": cfg.chunk_size, "parallelism": "single-gpu"},
+        "ms_per_layer": ms, "wall_ms_per_step": wall / K * 1e3,
+        "layer_hbm_frac": tot_by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "roofline": roof, "stages": stages,
+        "reference_published": {"hardware": "H100", "dtype": "fp32", "pallas_ms": 0.94,
+                                "triton_ms": 0.69, "source": "reference README.md:35"},
+    }
+    if not args.no_decode:
+        res["decode"] = bench_decode()
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(cfg, args.cpu_heads)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

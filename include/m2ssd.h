@@ -1,0 +1,237 @@
+/*
+ * m2ssd.h -- C ABI of libm2ssd.so: the Mamba2 SSD chunked-scan forward and the
+ * selective-state-update decode step, as hand-written HIP kernels for MI355X
+ * (gfx950).
+ *
+ * Every entry point takes one argument struct of plain device pointers, sizes
+ * and flags, plus a stream (a hipStream_t passed as void*; NULL = the default
+ * stream).  Nothing here allocates device memory: outputs and workspace are
+ * owned by the caller.  Calls only enqueue work on the stream and never
+ * synchronise.  Entry points are re-entrant; errors are reported through the
+ * return code and a thread-local message (m2_last_error).
+ *
+ * Tensor layouts are the reference's (row-major, contiguous):
+ *   b = batch, L = seqlen, H = nheads, G = ngroups, P = headdim, N = dstate,
+ *   Q = chunk_size, nc = ceil(L / Q).
+ * Element types: M2_F32 or M2_BF16 as named per field.  A, D, dt_bias and all
+ * state / cumsum / output tensors not marked otherwise are float32.
+ */
+#ifndef M2SSD_H
+#define M2SSD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define M2SSD_ABI_VERSION 1
+
+/* return codes */
+#define M2_OK               0
+#define M2_ERR_INVALID     -1   /* bad shape, size, pointer or flag */
+#define M2_ERR_UNSUPPORTED -2   /* dtype / size this build does not handle */
+#define M2_ERR_LAUNCH      -3   /* HIP launch / runtime error */
+#define M2_ERR_WORKSPACE   -4   /* workspace missing or too small */
+
+/* element types */
+#define M2_F32  0
+#define M2_BF16 1
+
+/* ---------------------------------------------------------------------------
+ * chunk_cumsum: dt' = clip(softplus?(dt + dt_bias), dt_min, dt_max) (0 past
+ * the end of the sequence); dA_cumsum = inclusive cumsum over each chunk of
+ * dt' * A.
+ * Replaces chunk_cumsum_fwd (reference kernels/chunk_cumsum_fwd.py:288-302,
+ * :194-235; naive ops/ssd_naive.py:26-70).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void*  dt;          /* [b, L, H], dt_dtype                     */
+    const float* A;           /* [H]                                     */
+    const float* dt_bias;     /* [H] or NULL                             */
+    float*       dA_cumsum;   /* out [b, H, nc, Q]                       */
+    float*       dt_out;      /* out [b, H, nc, Q]                       */
+    int64_t batch, seqlen, nheads, chunk_size;
+    int32_t dt_dtype;
+    int32_t dt_softplus;      /* 0 / 1                                   */
+    float   dt_min, dt_max;   /* dt_limit                                */
+} m2_chunk_cumsum_args;
+int m2_chunk_cumsum(const m2_chunk_cumsum_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * chunk_state: states[b,c,h] = sum_q exp(min(dA[Q-1]-dA[q],0)) dt[q] x[q]^T B[q]
+ * (P x N per chunk and head; B shared by the heads of a group).  With seq_idx,
+ * positions whose sequence differs from the one at the chunk's last valid
+ * position (or where that id is negative) are left out.
+ * Replaces chunk_state_fwd (reference kernels/chunk_state_fwd.py:424-441,
+ * :194-304; naive ops/ssd_naive.py:77-128).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void*    x;          /* [b, L, H, P], dtype                    */
+    const void*    B;          /* [b, L, G, N], dtype                    */
+    const float*   dt;         /* [b, H, nc, Q]                          */
+    const float*   dA_cumsum;  /* [b, H, nc, Q]                          */
+    const int32_t* seq_idx;    /* [b, L] or NULL                         */
+    float*         states;     /* out [b, nc, H, P, N]                   */
+    int64_t batch, seqlen, nheads, headdim, ngroups, dstate, chunk_size;
+    int32_t dtype;             /* of x and B                             */
+} m2_chunk_state_args;
+int m2_chunk_state(const m2_chunk_state_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * state_passing: out[:, 0] = initial (or 0); out[:, c+1] = exp(dA[c]) out[:, c]
+ * + states[:, c]; final = the value after the last chunk.  With seq_idx the
+ * carried state is dropped at chunk c when seq_idx at the end of chunk c
+ * differs from seq_idx at the end of chunk c-1 (taken as 0 for c = 0).
+ * dA_chunk_cumsum may be a strided view (e.g. dA_cumsum[..., -1]).
+ * Replaces state_passing_fwd (reference kernels/state_passing_fwd.py:348-363,
+ * :158-341; naive ops/ssd_naive.py:135-182).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const float*   states;           /* [b, nc, H, D]                    */
+    const float*   dA_chunk_cumsum;  /* [b, H, nc] at the strides below  */
+    int64_t        dA_stride_batch, dA_stride_head, dA_stride_chunk;
+    const float*   initial_states;   /* [b, H, D] or NULL                */
+    const int32_t* seq_idx;          /* [b, seqlen] or NULL              */
+    void*          out;              /* out [b, nc, H, D], out_dtype     */
+    float*         final_states;     /* out [b, H, D]                    */
+    int64_t batch, nchunks, nheads, dim, seqlen, chunk_size;
+    int32_t out_dtype;
+} m2_state_passing_args;
+int m2_state_passing(const m2_state_passing_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * bmm_chunk: out[b,c,g] = a_c @ b_c^T over each chunk (Q x Q, contraction K),
+ * then optionally zeroed above the diagonal (causal) and where seq_idx[i] !=
+ * seq_idx[j].
+ * Replaces bmm_chunk_fwd (reference kernels/bmm_chunk_fwd.py:381-400,
+ * :293-374; naive ops/ssd_naive.py:189-216).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void*    a;          /* [b, L, G, K], dtype                    */
+    const void*    b;          /* [b, L, G, K], dtype                    */
+    const int32_t* seq_idx;    /* [b, L] or NULL                         */
+    void*          out;        /* out [b, nc, G, Q, Q], out_dtype        */
+    int64_t batch, seqlen, ngroups, k, chunk_size;
+    int32_t dtype, out_dtype;
+    int32_t causal;
+} m2_bmm_chunk_args;
+int m2_bmm_chunk(const m2_bmm_chunk_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * chunk_scan: out[m] = sum_{k<=m} cb[m,k] exp(dA[m]-dA[k]) dt[k] x[k]
+ *                    + exp(dA[m]) C[m] @ states^T + D x[m]; out *= silu(z).
+ * states are rounded to x's dtype before use.  out_x (optional) receives the
+ * output before the z gate.  With seq_idx, rows whose sequence differs from
+ * the one at the previous chunk's last position (0 for chunk 0) get no
+ * inter-chunk term; cb is used as given (mask it with bmm_chunk).
+ * Replaces chunk_scan_fwd (reference kernels/chunk_scan_fwd.py:579-600,
+ * :482-572; naive ops/ssd_naive.py:223-318).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void*    cb;         /* [b, nc, G, Q, Q], cb_dtype             */
+    const void*    x;          /* [b, L, H, P], dtype                    */
+    const float*   dt;         /* [b, H, nc, Q]                          */
+    const float*   dA_cumsum;  /* [b, H, nc, Q]                          */
+    const void*    C;          /* [b, L, G, N], dtype                    */
+    const void*    states;     /* [b, nc, H, P, N], states_dtype         */
+    const float*   D;          /* [H] or [H, P] or NULL                  */
+    const void*    z;          /* [b, L, H, P], dtype, or NULL           */
+    const int32_t* seq_idx;    /* [b, L] or NULL                         */
+    float*         out;        /* out [b, L, H, P]                       */
+    float*         out_x;      /* out [b, L, H, P] or NULL               */
+    int64_t batch, seqlen, nheads, headdim, ngroups, dstate, chunk_size;
+    int32_t dtype, cb_dtype, states_dtype;
+    int32_t D_has_hdim;        /* 1 if D is [H, P]                       */
+} m2_chunk_scan_args;
+int m2_chunk_scan(const m2_chunk_scan_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * chunk_state_varlen: final state of each packed sequence s (batch 1):
+ * the decay-weighted x^T B over its positions in its last chunk, plus
+ * exp(dA at its last position) * chunk_states[last chunk] when it started in
+ * an earlier chunk.  cu_seqlens is read on the device.
+ * Replaces chunk_state_varlen_mosaic (reference kernels/chunk_state_fwd.py:448-597).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void*    B;            /* [L, G, N], dtype                     */
+    const void*    x;            /* [L, H, P], dtype                     */
+    const float*   dt;           /* [H, nc, Q]                           */
+    const float*   dA_cumsum;    /* [H, nc, Q]                           */
+    const int32_t* cu_seqlens;   /* [nseq + 1]                           */
+    const void*    chunk_states; /* [nc, H, P, N], states_dtype          */
+    float*         out;          /* out [nseq, H, P, N]                  */
+    int64_t seqlen, nseq, nheads, headdim, ngroups, dstate, nchunks, chunk_size;
+    int32_t dtype, states_dtype;
+} m2_chunk_state_varlen_args;
+int m2_chunk_state_varlen(const m2_chunk_state_varlen_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * ssd_combined: the whole forward (cumsum -> chunk_state -> state_passing ->
+ * bmm_chunk -> chunk_scan [-> varlen states]) on one stream, intermediates in
+ * the caller's workspace (size from m2_ssd_combined_workspace_size).
+ * states_passed is kept in x's dtype; out and the final states are float32.
+ * Replaces mamba_chunk_scan_combined_fwd (reference kernels/ssd_combined.py:46-203).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void*    x;               /* [b, L, H, P], dtype               */
+    const void*    dt;              /* [b, L, H], dt_dtype               */
+    const float*   A;               /* [H]                               */
+    const void*    B;               /* [b, L, G, N], dtype               */
+    const void*    C;               /* [b, L, G, N], dtype               */
+    const float*   D;               /* [H] / [H, P] / NULL               */
+    const void*    z;               /* [b, L, H, P], dtype, or NULL      */
+    const float*   dt_bias;         /* [H] or NULL                       */
+    const float*   initial_states;  /* [b, H, P, N] or NULL              */
+    const int32_t* seq_idx;         /* [b, L] or NULL                    */
+    const int32_t* cu_seqlens;      /* [nseq + 1] or NULL (needs b == 1) */
+    float*         out;             /* out [b, L, H, P]                  */
+    float*         final_states;    /* out [b, H, P, N] or NULL          */
+    float*         varlen_states;   /* out [nseq, H, P, N] or NULL       */
+    void*          workspace;
+    size_t         workspace_bytes;
+    int64_t batch, seqlen, nheads, headdim, ngroups, dstate, chunk_size, nseq;
+    int32_t dtype, dt_dtype;
+    int32_t D_has_hdim, dt_softplus;
+    float   dt_min, dt_max;
+    void**         stage_events;    /* optional profiling hook: NULL, or 6
+                                       hipEvent_t recorded before stage 1 and
+                                       after each of the 5 stages           */
+} m2_ssd_combined_args;
+size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a);
+int m2_ssd_combined(const m2_ssd_combined_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * selective_state_update (one decode token, state updated IN PLACE):
+ * dt' = softplus?(dt + dt_bias); state = state * exp(dt' A) + dt' x B^T;
+ * out = state @ C + D x; out *= silu(z).
+ * Replaces selective_state_update (reference ops/selective_state_update.py:22-123).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    float*       state;        /* [b, H, P, N], updated in place         */
+    const void*  x;            /* [b, H, P], dtype                       */
+    const void*  dt;           /* [b, H] or [b, H, P], dt_dtype          */
+    const float* A;            /* [H] or [H, P, N]                       */
+    const void*  B;            /* [b, G, N], dtype                       */
+    const void*  C;            /* [b, G, N], dtype                       */
+    const float* D;            /* [H] / [H, P] / NULL                    */
+    const void*  z;            /* [b, H, P], dtype, or NULL              */
+    const float* dt_bias;      /* [H] / [H, P] / NULL                    */
+    float*       out;          /* out [b, H, P]                          */
+    int64_t batch, nheads, headdim, ngroups, dstate;
+    int32_t dtype, dt_dtype;
+    int32_t dt_has_hdim, A_full, D_has_hdim, dt_bias_has_hdim;
+    int32_t dt_softplus;
+} m2_ssu_args;
+int m2_selective_state_update(const m2_ssu_args* a, void* stream);
+
+/* thread-local message for the last non-zero return code of this thread */
+const char* m2_last_error(void);
+/* M2SSD_ABI_VERSION of the loaded library */
+int m2_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* M2SSD_H */

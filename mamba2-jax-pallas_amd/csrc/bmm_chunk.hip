@@ -1,0 +1,134 @@
+// bmm_chunk: CB[b,c,g] = a_c @ b_c^T for every chunk c and group g
+// (Q x Q output, contraction over K = dstate).
+//
+// Both operands are K-contiguous in HBM ([.., L, G, K] rows), which is exactly
+// the per-lane layout MFMA wants, so every fragment is one 16-byte global load
+// (bf16) straight into VGPRs -- no LDS round trip.  A workgroup owns 64 rows of
+// one (b, c, g) block; each of its 4 wavefronts owns one 16-row tile and all
+// Q/16 column tiles.  Causal and seq_idx masks are applied in the epilogue.
+//
+// Follows reference kernels/bmm_chunk_fwd.py:87-154 (product), :348-372
+// (masks; positions past the end carry seq id -1) and ops/ssd_naive.py:189-216.
+#include "m2_internal.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+
+template <typename T, typename TO, int CT>
+__global__ void __launch_bounds__(THREADS)
+k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
+            const int32_t* __restrict__ seq_idx, TO* __restrict__ out, int L, int G,
+            int K, int Q, int nc, int causal, int rowblocks, int nblocks) {
+    typedef MF<T> M;
+    const int work = xcd_remap(blockIdx.x, nblocks);
+    const int rb = work % rowblocks;
+    int rest = work / rowblocks;
+    const int g = rest % G;
+    rest /= G;
+    const int c = rest % nc;
+    const int bi = rest / nc;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int r0 = rb * 64 + w * 16;
+    if (r0 >= Q) return;
+    const int ln = lane & 15, kg = lane >> 4;
+
+    const int arow = r0 + ln;
+    const int64_t tbase = (int64_t)bi * L + (int64_t)c * Q;
+    const bool arow_ok = (c * Q + arow) < L;
+    const T* ap = a + ((tbase + arow) * G + g) * K + kg * M::KPL;
+    const T* bp[CT];
+    bool bok[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        const int col = ct * 16 + ln;
+        bok[ct] = (c * Q + col) < L && col < Q;
+        bp[ct] = b + ((tbase + col) * G + g) * K + kg * M::KPL;
+    }
+    f32x4 acc[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) acc[ct] = zero4();
+
+    typename M::frag zf;
+#pragma unroll
+    for (int j = 0; j < M::KPL; ++j) M::set(zf, j, 0.f);
+
+    for (int k0 = 0; k0 < K; k0 += M::K) {
+        const typename M::frag af = arow_ok ? load_frag(ap + k0) : zf;
+        typename M::frag bf[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) bf[ct] = bok[ct] ? load_frag(bp[ct] + k0) : zf;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct] = M::mma(af, bf[ct], acc[ct]);
+    }
+
+    TO* op = out + ((((int64_t)bi * nc + c) * G + g) * Q) * Q;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        const int col = ct * 16 + ln;
+        if (col >= Q) continue;
+        int scol = 0;
+        if (seq_idx) scol = (c * Q + col) < L ? seq_idx[tbase + col] : -1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = r0 + kg * 4 + i;
+            float v = acc[ct][i];
+            if (causal && col > row) v = 0.f;
+            if (seq_idx) {
+                const int srow = (c * Q + row) < L ? seq_idx[tbase + row] : -1;
+                if (srow != scol) v = 0.f;
+            }
+            op[(int64_t)row * Q + col] = from_f32<TO>(v);
+        }
+    }
+}
+
+template <typename T, typename TO>
+int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
+    const int Q = (int)a.chunk_size;
+    const int nc = (int)((a.seqlen + Q - 1) / Q);
+    const int rowblocks = (Q + 63) / 64;
+    const int64_t nblocks = a.batch * nc * a.ngroups * rowblocks;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "bmm_chunk: too many blocks");
+    const int ct = Q / 16;
+#define M2_BMM_CASE(CTV)                                                                  \
+    case CTV:                                                                             \
+        k_bmm_chunk<T, TO, CTV><<<(unsigned)nblocks, THREADS, 0, s>>>(                     \
+            (const T*)a.a, (const T*)a.b, a.seq_idx, (TO*)a.out, (int)a.seqlen,           \
+            (int)a.ngroups, (int)a.k, Q, nc, a.causal, rowblocks, (int)nblocks);          \
+        break;
+    switch (ct) {
+        M2_BMM_CASE(1) M2_BMM_CASE(2) M2_BMM_CASE(3) M2_BMM_CASE(4) M2_BMM_CASE(5)
+        M2_BMM_CASE(6) M2_BMM_CASE(7) M2_BMM_CASE(8) M2_BMM_CASE(9) M2_BMM_CASE(10)
+        M2_BMM_CASE(11) M2_BMM_CASE(12) M2_BMM_CASE(13) M2_BMM_CASE(14) M2_BMM_CASE(15)
+        M2_BMM_CASE(16)
+        default: return m2::set_error(M2_ERR_UNSUPPORTED, "bmm_chunk: chunk_size %d", Q);
+    }
+#undef M2_BMM_CASE
+    return m2::check_launch("bmm_chunk");
+}
+
+}  // namespace
+
+namespace m2 {
+
+int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t s) {
+    M2_REQUIRE(a.a && a.b && a.out, M2_ERR_INVALID, "bmm_chunk: a, b and out are required");
+    M2_REQUIRE(a.batch > 0 && a.seqlen > 0 && a.ngroups > 0 && a.k > 0 && a.chunk_size > 0,
+               M2_ERR_INVALID, "bmm_chunk: sizes must be positive");
+    M2_REQUIRE(a.chunk_size % 16 == 0 && a.chunk_size <= 256, M2_ERR_UNSUPPORTED,
+               "bmm_chunk: chunk_size must be a multiple of 16 and <= 256 (got %lld)",
+               (long long)a.chunk_size);
+    if (a.dtype == M2_BF16) {
+        M2_REQUIRE(a.k % 32 == 0, M2_ERR_UNSUPPORTED, "bmm_chunk: bf16 needs k %% 32 == 0");
+        if (a.out_dtype == M2_F32) return launch_typed<bf16, float>(a, s);
+        if (a.out_dtype == M2_BF16) return launch_typed<bf16, bf16>(a, s);
+    } else if (a.dtype == M2_F32) {
+        M2_REQUIRE(a.k % 4 == 0, M2_ERR_UNSUPPORTED, "bmm_chunk: f32 needs k %% 4 == 0");
+        if (a.out_dtype == M2_F32) return launch_typed<float, float>(a, s);
+        if (a.out_dtype == M2_BF16) return launch_typed<float, bf16>(a, s);
+    }
+    return set_error(M2_ERR_UNSUPPORTED, "bmm_chunk: dtype %d -> %d", a.dtype, a.out_dtype);
+}
+
+}  // namespace m2

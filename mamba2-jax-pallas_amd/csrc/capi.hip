@@ -1,0 +1,163 @@
+// C-ABI plumbing: thread-local error messages, version, the per-stage entry
+// points, and m2_ssd_combined (the whole forward over a caller workspace).
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "m2_internal.h"
+
+namespace m2 {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(M2_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+    return M2_OK;
+}
+
+}  // namespace m2
+
+extern "C" const char* m2_last_error(void) { return m2::g_err; }
+extern "C" int m2_abi_version(void) { return M2SSD_ABI_VERSION; }
+
+#define M2_ENTRY(name, T, launcher)                                  \
+    extern "C" int name(const T* a, void* stream) {                  \
+        if (!a) return m2::set_error(M2_ERR_INVALID, #name ": NULL args"); \
+        return m2::launcher(*a, (hipStream_t)stream);                \
+    }
+
+M2_ENTRY(m2_chunk_cumsum, m2_chunk_cumsum_args, launch_chunk_cumsum)
+M2_ENTRY(m2_chunk_state, m2_chunk_state_args, launch_chunk_state)
+M2_ENTRY(m2_state_passing, m2_state_passing_args, launch_state_passing)
+M2_ENTRY(m2_bmm_chunk, m2_bmm_chunk_args, launch_bmm_chunk)
+M2_ENTRY(m2_chunk_scan, m2_chunk_scan_args, launch_chunk_scan)
+M2_ENTRY(m2_chunk_state_varlen, m2_chunk_state_varlen_args, launch_chunk_state_varlen)
+M2_ENTRY(m2_selective_state_update, m2_ssu_args, launch_ssu)
+
+// ---------------------------------------------------------------------------
+// combined forward
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Layout {
+    size_t dA, dt, states, passed, cb, total;
+};
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+Layout layout_of(const m2_ssd_combined_args& a) {
+    Layout l{};
+    const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
+    const size_t es = m2_dtype_size(a.dtype);
+    const size_t bhcq = (size_t)a.batch * a.nheads * nc * a.chunk_size;
+    const size_t S = (size_t)a.batch * nc * a.nheads * a.headdim * a.dstate;
+    size_t off = 0;
+    l.dA = off;     off += align256(bhcq * 4);
+    l.dt = off;     off += align256(bhcq * 4);
+    l.states = off; off += align256(S * 4);
+    l.passed = off; off += align256(S * es);
+    l.cb = off;     off += align256((size_t)a.batch * nc * a.ngroups * a.chunk_size * a.chunk_size * es);
+    l.total = off;
+    return l;
+}
+
+int record(void** ev, int i, hipStream_t s) {
+    if (!ev) return M2_OK;
+    if (hipEventRecord((hipEvent_t)ev[i], s) != hipSuccess)
+        return m2::set_error(M2_ERR_LAUNCH, "m2_ssd_combined: hipEventRecord failed");
+    return M2_OK;
+}
+
+}  // namespace
+
+extern "C" size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a) {
+    if (!a || a->chunk_size <= 0 || !m2_dtype_size(a->dtype)) return 0;
+    return layout_of(*a).total;
+}
+
+extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
+    if (!ap) return m2::set_error(M2_ERR_INVALID, "m2_ssd_combined: NULL args");
+    const m2_ssd_combined_args& a = *ap;
+    hipStream_t s = (hipStream_t)stream_;
+    M2_REQUIRE(a.chunk_size > 0 && a.batch > 0 && a.seqlen > 0, M2_ERR_INVALID,
+               "m2_ssd_combined: batch, seqlen and chunk_size must be positive");
+    M2_REQUIRE(m2_dtype_size(a.dtype) != 0, M2_ERR_UNSUPPORTED, "m2_ssd_combined: dtype %d", a.dtype);
+    M2_REQUIRE(a.x && a.dt && a.A && a.B && a.C && a.out, M2_ERR_INVALID,
+               "m2_ssd_combined: x, dt, A, B, C and out are required");
+    M2_REQUIRE(!a.varlen_states || (a.cu_seqlens && a.batch == 1 && a.nseq > 0), M2_ERR_INVALID,
+               "m2_ssd_combined: varlen states need cu_seqlens, nseq > 0 and batch == 1");
+    const Layout l = layout_of(a);
+    M2_REQUIRE(a.workspace && a.workspace_bytes >= l.total, M2_ERR_WORKSPACE,
+               "m2_ssd_combined: workspace of %zu bytes needed, %zu given", l.total,
+               a.workspace_bytes);
+    char* ws = (char*)a.workspace;
+    float* dA = (float*)(ws + l.dA);
+    float* dto = (float*)(ws + l.dt);
+    float* states = (float*)(ws + l.states);
+    void* passed = ws + l.passed;
+    void* cb = ws + l.cb;
+    const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
+    int rc;
+    if ((rc = record(a.stage_events, 0, s))) return rc;
+
+    m2_chunk_cumsum_args c1{};
+    c1.dt = a.dt; c1.A = a.A; c1.dt_bias = a.dt_bias; c1.dA_cumsum = dA; c1.dt_out = dto;
+    c1.batch = a.batch; c1.seqlen = a.seqlen; c1.nheads = a.nheads; c1.chunk_size = a.chunk_size;
+    c1.dt_dtype = a.dt_dtype; c1.dt_softplus = a.dt_softplus; c1.dt_min = a.dt_min; c1.dt_max = a.dt_max;
+    if ((rc = m2::launch_chunk_cumsum(c1, s))) return rc;
+    if ((rc = record(a.stage_events, 1, s))) return rc;
+
+    m2_chunk_state_args c2{};
+    c2.x = a.x; c2.B = a.B; c2.dt = dto; c2.dA_cumsum = dA; c2.seq_idx = a.seq_idx; c2.states = states;
+    c2.batch = a.batch; c2.seqlen = a.seqlen; c2.nheads = a.nheads; c2.headdim = a.headdim;
+    c2.ngroups = a.ngroups; c2.dstate = a.dstate; c2.chunk_size = a.chunk_size; c2.dtype = a.dtype;
+    if ((rc = m2::launch_chunk_state(c2, s))) return rc;
+    if ((rc = record(a.stage_events, 2, s))) return rc;
+
+    m2_state_passing_args c3{};
+    c3.states = states; c3.dA_chunk_cumsum = dA + (a.chunk_size - 1);
+    c3.dA_stride_batch = a.nheads * nc * a.chunk_size; c3.dA_stride_head = nc * a.chunk_size;
+    c3.dA_stride_chunk = a.chunk_size;
+    c3.initial_states = a.initial_states; c3.seq_idx = a.seq_idx; c3.out = passed;
+    c3.final_states = a.final_states;
+    c3.batch = a.batch; c3.nchunks = nc; c3.nheads = a.nheads; c3.dim = a.headdim * a.dstate;
+    c3.seqlen = a.seqlen; c3.chunk_size = a.chunk_size; c3.out_dtype = a.dtype;
+    if ((rc = m2::launch_state_passing(c3, s))) return rc;
+    if ((rc = record(a.stage_events, 3, s))) return rc;
+
+    m2_bmm_chunk_args c4{};
+    c4.a = a.C; c4.b = a.B; c4.seq_idx = a.seq_idx; c4.out = cb;
+    c4.batch = a.batch; c4.seqlen = a.seqlen; c4.ngroups = a.ngroups; c4.k = a.dstate;
+    c4.chunk_size = a.chunk_size; c4.dtype = a.dtype; c4.out_dtype = a.dtype; c4.causal = 0;
+    if ((rc = m2::launch_bmm_chunk(c4, s))) return rc;
+    if ((rc = record(a.stage_events, 4, s))) return rc;
+
+    m2_chunk_scan_args c5{};
+    c5.cb = cb; c5.x = a.x; c5.dt = dto; c5.dA_cumsum = dA; c5.C = a.C; c5.states = passed;
+    c5.D = a.D; c5.z = a.z; c5.seq_idx = a.seq_idx; c5.out = a.out; c5.out_x = nullptr;
+    c5.batch = a.batch; c5.seqlen = a.seqlen; c5.nheads = a.nheads; c5.headdim = a.headdim;
+    c5.ngroups = a.ngroups; c5.dstate = a.dstate; c5.chunk_size = a.chunk_size;
+    c5.dtype = a.dtype; c5.cb_dtype = a.dtype; c5.states_dtype = a.dtype; c5.D_has_hdim = a.D_has_hdim;
+    if ((rc = m2::launch_chunk_scan(c5, s))) return rc;
+    if ((rc = record(a.stage_events, 5, s))) return rc;
+
+    if (a.varlen_states) {
+        m2_chunk_state_varlen_args c6{};
+        c6.B = a.B; c6.x = a.x; c6.dt = dto; c6.dA_cumsum = dA; c6.cu_seqlens = a.cu_seqlens;
+        c6.chunk_states = passed; c6.out = a.varlen_states;
+        c6.seqlen = a.seqlen; c6.nseq = a.nseq; c6.nheads = a.nheads; c6.headdim = a.headdim;
+        c6.ngroups = a.ngroups; c6.dstate = a.dstate; c6.nchunks = nc; c6.chunk_size = a.chunk_size;
+        c6.dtype = a.dtype; c6.states_dtype = a.dtype;
+        if ((rc = m2::launch_chunk_state_varlen(c6, s))) return rc;
+    }
+    return M2_OK;
+}

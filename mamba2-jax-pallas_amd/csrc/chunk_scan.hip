@@ -1,0 +1,292 @@
+// chunk_scan: the SSD output of one chunk and head
+//   y[m,:] = sum_{k<=m} cb[m,k] exp(dA[m]-dA[k]) dt[k] x[k,:]      (intra-chunk)
+//          + exp(dA[m]) * C[m,:] @ states^T                        (carried state)
+//          + D x[m,:],   then y *= silu(z[m,:])
+//
+// One workgroup per (b, c, h), 4 wavefronts; the chunk's x rows [Q x P] and
+// the carried state [P x N] are staged in LDS (16-byte coalesced loads; the
+// state is rounded to x's dtype on the way in).  Each wavefront takes 16-row
+// tiles of the output in a snake order so that the causal (triangular) work
+// is balanced, and for each tile accumulates
+//   1. C-rows (16-byte loads straight into VGPRs) x state  -> scaled by exp(dA[m])
+//   2. decay-weighted CB-rows x x-tile, for k-tiles up to the diagonal only.
+// The decay exp(dA[m]-dA[k]) is evaluated per element in registers while the
+// CB fragment is built -- never factored into exp(dA[m]) * exp(-dA[k]), which
+// overflows once |dA| inside a chunk exceeds ~88.  The D skip and z gate are
+// fused into the store.
+//
+// Follows reference ops/ssd_naive.py:223-318 (math), kernels/chunk_scan_fwd.py
+// :294-322 (seq_idx rule for the carried-state term) and :545-570 (epilogue).
+#include "m2_internal.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+
+template <typename T> struct ScanPad;
+template <> struct ScanPad<bf16> { static constexpr int x = 2; static constexpr int s = 8; };
+template <> struct ScanPad<float> { static constexpr int x = 16; static constexpr int s = 4; };
+
+struct ScanArgs {
+    const void* cb;
+    const void* x;
+    const float* dt;
+    const float* dA;
+    const void* C;
+    const void* states;
+    const float* D;
+    const void* z;
+    const int32_t* seq_idx;
+    float* out;
+    float* out_x;
+    int states_same;      // states dtype == x dtype
+    int states_bf16;      // states dtype is bf16
+    int D_has_hdim;
+    int L, H, G, P, N, Q, nc, nblocks;
+};
+
+// KPL consecutive cb values of one row, as float
+template <int KPL> M2_DEV void load_cb(const float* p, float* v) {
+    if constexpr (KPL == 8) {
+        const float4 a = reinterpret_cast<const float4*>(p)[0];
+        const float4 b = reinterpret_cast<const float4*>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) v[j] = p[j];
+    }
+}
+template <int KPL> M2_DEV void load_cb(const bf16* p, float* v) {
+    if constexpr (KPL == 8) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (float)a[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < KPL; ++j) v[j] = (float)p[j];
+    }
+}
+
+template <typename T, typename TCB, int PT>
+__global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
+    typedef MF<T> M;
+    constexpr int KPL = M::KPL;
+    extern __shared__ __align__(16) char smem[];
+    const int P = PT * 16;
+    const int Q = a.Q, L = a.L, H = a.H, N = a.N, nc = a.nc;
+    const int SX = P + ScanPad<T>::x, SS = N + ScanPad<T>::s;
+    T* xs = reinterpret_cast<T*>(smem);                  // [Q][SX]
+    T* ss = xs + Q * SX;                                  // [P][SS]
+    float* dAs = reinterpret_cast<float*>(ss + P * SS);   // [Q]
+    float* dts = dAs + Q;                                 // [Q]
+    int* seqs = reinterpret_cast<int*>(dts + Q);          // [Q] (seq_idx only)
+
+    const int work = xcd_remap(blockIdx.x, a.nblocks);
+    const int h = work % H;
+    const int rest = work / H;
+    const int c = rest % nc;
+    const int bi = rest / nc;
+    const int g = h / (H / a.G);
+    const int valid = min(Q, L - c * Q);
+    const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
+
+    // --- stage dA, dt, seq_idx, x rows and the carried state ----------------
+    const int64_t cq = (((int64_t)bi * H + h) * nc + c) * Q;
+    int seq_prev = 0;
+    if (a.seq_idx && c > 0) seq_prev = a.seq_idx[tok0 - 1];
+    for (int q = threadIdx.x; q < Q; q += THREADS) {
+        dAs[q] = a.dA[cq + q];
+        dts[q] = a.dt[cq + q];
+        if (a.seq_idx) seqs[q] = q < valid ? a.seq_idx[tok0 + q] : -1;
+    }
+    {
+        constexpr int VE = 16 / sizeof(T);
+        const T* xsrc = reinterpret_cast<const T*>(a.x) + (tok0 * H + h) * P;
+        const int vpr = P / VE, total = Q * vpr;
+        for (int idx = threadIdx.x; idx < total; idx += THREADS) {
+            const int r = idx / vpr, cv = idx % vpr;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (r < valid) v = *reinterpret_cast<const uint4*>(xsrc + (int64_t)r * H * P + cv * VE);
+            uint32_t* d = reinterpret_cast<uint32_t*>(xs + r * SX + cv * VE);
+            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        }
+    }
+    {
+        const int64_t soff = (((int64_t)bi * nc + c) * H + h) * (int64_t)P * N;
+        if (a.states_same) {
+            constexpr int VE = 16 / sizeof(T);
+            const T* src = reinterpret_cast<const T*>(a.states) + soff;
+            const int vpr = N / VE, total = P * vpr;
+            for (int idx = threadIdx.x; idx < total; idx += THREADS) {
+                const int r = idx / vpr, cv = idx % vpr;
+                *reinterpret_cast<uint4*>(ss + r * SS + cv * VE) =
+                    *reinterpret_cast<const uint4*>(src + (int64_t)r * N + cv * VE);
+            }
+        } else {
+            for (int idx = threadIdx.x; idx < P * N; idx += THREADS) {
+                const int r = idx / N, cl = idx % N;
+                const float v = a.states_bf16
+                                    ? (float)reinterpret_cast<const bf16*>(a.states)[soff + idx]
+                                    : reinterpret_cast<const float*>(a.states)[soff + idx];
+                ss[r * SS + cl] = from_f32<T>(v);
+            }
+        }
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int ln = lane & 15, kg = lane >> 4;
+    const T* Cbase = reinterpret_cast<const T*>(a.C) + (tok0 * a.G + g) * N;
+    const TCB* cbbase = reinterpret_cast<const TCB*>(a.cb) +
+                        (((int64_t)bi * nc + c) * a.G + g) * (int64_t)Q * Q;
+    typename M::frag zf;
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) M::set(zf, j, 0.f);
+
+    const int ntiles = Q / 16;
+    for (int r = 0;; ++r) {
+        const int t = r * 4 + ((r & 1) ? (3 - w) : w);
+        if (t >= ntiles) break;
+        const int m0 = t * 16;
+        f32x4 acc[PT];
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt) acc[pt] = zero4();
+
+        // 1. carried state: C[m, :] @ state^T
+        {
+            const int m = m0 + ln;
+            const bool mok = m < valid;
+            const T* crow = Cbase + (int64_t)m * a.G * N + kg * KPL;
+            for (int k0 = 0; k0 < N; k0 += M::K) {
+                const typename M::frag af = mok ? load_frag(crow + k0) : zf;
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) {
+                    const typename M::frag bfr =
+                        load_frag(ss + (pt * 16 + ln) * SS + k0 + kg * KPL);
+                    acc[pt] = M::mma(af, bfr, acc[pt]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int mr = m0 + kg * 4 + i;
+                float f = expf(dAs[mr]);
+                if (a.seq_idx && seqs[mr] != seq_prev) f = 0.f;
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) acc[pt][i] *= f;
+            }
+        }
+
+        // 2. intra-chunk: (cb o decay o dt)[m, k<=m] @ x[k, :]
+        {
+            const int m = m0 + ln;
+            const float dAm = dAs[m];
+            const TCB* cbrow = cbbase + (int64_t)m * Q;
+            const int kend = m0 + 16;
+            for (int k0 = 0; k0 < kend; k0 += M::K) {
+                const int kb = k0 + kg * KPL;
+                float cbv[KPL];
+                if (kb < Q) load_cb<KPL>(cbrow + kb, cbv);
+                typename M::frag af;
+#pragma unroll
+                for (int j = 0; j < KPL; ++j) {
+                    const int k = kb + j;
+                    float v = 0.f;
+                    if (k <= m && k < Q) v = cbv[j] * expf(dAm - dAs[k]) * dts[k];
+                    M::set(af, j, v);
+                }
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) {
+                    typename M::frag bfr;
+#pragma unroll
+                    for (int j = 0; j < KPL; ++j) {
+                        const int k = kb + j;
+                        M::set_raw(bfr, j, k < Q ? xs[k * SX + pt * 16 + ln] : T(0.f));
+                    }
+                    acc[pt] = M::mma(af, bfr, acc[pt]);
+                }
+            }
+        }
+
+        // 3. epilogue: + D x, out_x, z gate, store
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt) {
+            const int p = pt * 16 + ln;
+            const float dv = a.D ? (a.D_has_hdim ? a.D[h * P + p] : a.D[h]) : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int mr = m0 + kg * 4 + i;
+                if (mr >= valid) continue;
+                float v = acc[pt][i];
+                if (a.D) v += dv * to_f32(xs[mr * SX + p]);
+                const int64_t o = ((tok0 + mr) * H + h) * (int64_t)P + p;
+                if (a.out_x) a.out_x[o] = v;
+                if (a.z) v *= silu_f(to_f32(reinterpret_cast<const T*>(a.z)[o]));
+                a.out[o] = v;
+            }
+        }
+    }
+}
+
+template <typename T, typename TCB>
+int launch_typed(const ScanArgs& sa, hipStream_t s) {
+    const size_t shm = (size_t)sa.Q * (sa.P + ScanPad<T>::x) * sizeof(T) +
+                       (size_t)sa.P * (sa.N + ScanPad<T>::s) * sizeof(T) +
+                       (size_t)sa.Q * 3 * sizeof(float);
+    void (*kern)(ScanArgs) = nullptr;
+    switch (sa.P) {
+        case 32: kern = k_chunk_scan<T, TCB, 2>; break;
+        case 64: kern = k_chunk_scan<T, TCB, 4>; break;
+        case 128: kern = k_chunk_scan<T, TCB, 8>; break;
+        default:
+            return m2::set_error(M2_ERR_UNSUPPORTED,
+                                 "chunk_scan: headdim %d not supported (32, 64, 128)", sa.P);
+    }
+    if (shm > 160 * 1024)
+        return m2::set_error(M2_ERR_UNSUPPORTED, "chunk_scan: %zu B of LDS needed", shm);
+    if (shm > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return m2::set_error(M2_ERR_LAUNCH, "chunk_scan: cannot reserve %zu B of LDS", shm);
+    kern<<<(unsigned)sa.nblocks, THREADS, shm, s>>>(sa);
+    return m2::check_launch("chunk_scan");
+}
+
+}  // namespace
+
+namespace m2 {
+
+int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t s) {
+    M2_REQUIRE(a.cb && a.x && a.dt && a.dA_cumsum && a.C && a.states && a.out, M2_ERR_INVALID,
+               "chunk_scan: cb, x, dt, dA_cumsum, C, states and out are required");
+    M2_REQUIRE(a.batch > 0 && a.seqlen > 0 && a.nheads > 0 && a.ngroups > 0 &&
+                   a.nheads % a.ngroups == 0 && a.chunk_size > 0,
+               M2_ERR_INVALID, "chunk_scan: bad sizes (nheads must be a multiple of ngroups)");
+    M2_REQUIRE(a.chunk_size % 16 == 0 && a.chunk_size <= 256, M2_ERR_UNSUPPORTED,
+               "chunk_scan: chunk_size must be a multiple of 16 and <= 256");
+    M2_REQUIRE(a.states_dtype == M2_F32 || a.states_dtype == M2_BF16, M2_ERR_UNSUPPORTED,
+               "chunk_scan: states dtype %d", a.states_dtype);
+    ScanArgs sa{};
+    sa.cb = a.cb; sa.x = a.x; sa.dt = a.dt; sa.dA = a.dA_cumsum; sa.C = a.C; sa.states = a.states;
+    sa.D = a.D; sa.z = a.z; sa.seq_idx = a.seq_idx; sa.out = a.out; sa.out_x = a.out_x;
+    sa.states_same = a.states_dtype == a.dtype; sa.states_bf16 = a.states_dtype == M2_BF16;
+    sa.D_has_hdim = a.D_has_hdim;
+    sa.L = (int)a.seqlen; sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.P = (int)a.headdim;
+    sa.N = (int)a.dstate; sa.Q = (int)a.chunk_size;
+    sa.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
+    const int64_t nblocks = a.batch * sa.nc * a.nheads;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_scan: too many blocks");
+    sa.nblocks = (int)nblocks;
+    if (a.dtype == M2_BF16) {
+        M2_REQUIRE(a.dstate % 32 == 0, M2_ERR_UNSUPPORTED, "chunk_scan: bf16 needs dstate %% 32 == 0");
+        if (a.cb_dtype == M2_F32) return launch_typed<bf16, float>(sa, s);
+        if (a.cb_dtype == M2_BF16) return launch_typed<bf16, bf16>(sa, s);
+    } else if (a.dtype == M2_F32) {
+        M2_REQUIRE(a.dstate % 4 == 0, M2_ERR_UNSUPPORTED, "chunk_scan: f32 needs dstate %% 4 == 0");
+        if (a.cb_dtype == M2_F32) return launch_typed<float, float>(sa, s);
+        if (a.cb_dtype == M2_BF16) return launch_typed<float, bf16>(sa, s);
+    }
+    return set_error(M2_ERR_UNSUPPORTED, "chunk_scan: dtype %d / cb dtype %d", a.dtype, a.cb_dtype);
+}
+
+}  // namespace m2

@@ -1,0 +1,278 @@
+// chunk_state: per-chunk SSM states
+//   states[b,c,h][p,n] = sum_q w[q] x[q,p] B[q,n],  w[q] = exp(min(dA[last]-dA[q],0)) dt[q]
+// and its variable-length twin (the final state of each packed sequence).
+//
+// One workgroup per (b, c, h) (per (sequence, h) for varlen), 4 wavefronts.
+// The contraction runs over chunk positions q, the outer (row) dimension of
+// both x [.., L, H, P] and B [.., L, G, N] in HBM, so x and B rows are staged
+// through LDS with coalesced 16-byte loads and the MFMA fragments (8
+// consecutive positions per lane for bf16) are gathered from LDS; the decay
+// weight w[q] is applied to the x operand as it is gathered.  Positions are
+// processed in blocks of KB rows to bound LDS.  Wavefront w owns all P/16 row
+// tiles and N/64 column tiles: [P x N] fp32 accumulators live in VGPRs and
+// are written once.
+//
+// Follows reference kernels/chunk_state_fwd.py:104-187 (product), :239-269
+// (scale and seq_idx rule), :448-597 (varlen) and ops/ssd_naive.py:77-128.
+#include "m2_internal.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+
+// LDS row padding (elements) so that the 4 k-groups of a fragment gather hit
+// different banks.
+template <typename T> struct Pad;
+template <> struct Pad<bf16> { static constexpr int v = 2; static constexpr int KB = 128; };
+template <> struct Pad<float> { static constexpr int v = 16; static constexpr int KB = 64; };
+
+// Copy `nrows` rows of W elements (row r at src + r * stride) into LDS rows of
+// stride S; rows >= valid are zero.  16-byte global loads, 4-byte LDS stores.
+template <typename T>
+M2_DEV void stage_rows(T* __restrict__ dst, int S, const T* __restrict__ src,
+                       int64_t stride, int nrows, int valid, int W) {
+    constexpr int VE = 16 / sizeof(T);
+    const int vpr = W / VE;
+    const int total = nrows * vpr;
+    for (int base = threadIdx.x; base < total; base += 4 * THREADS) {
+        uint4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = base + u * THREADS;
+            const int r = idx / vpr, cv = idx % vpr;
+            v[u] = make_uint4(0, 0, 0, 0);
+            if (idx < total && r < valid)
+                v[u] = *reinterpret_cast<const uint4*>(src + r * stride + cv * VE);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = base + u * THREADS;
+            if (idx < total) {
+                const int r = idx / vpr, cv = idx % vpr;
+                uint32_t* d = reinterpret_cast<uint32_t*>(dst + r * S + cv * VE);
+                d[0] = v[u].x; d[1] = v[u].y; d[2] = v[u].z; d[3] = v[u].w;
+            }
+        }
+    }
+}
+
+struct StateArgs {
+    const void* x;
+    const void* B;
+    const float* dt;
+    const float* dA;
+    const int32_t* seq_idx;
+    const int32_t* cu_seqlens;   // varlen only
+    const void* chunk_states;    // varlen only
+    int states_bf16;             // varlen only: dtype of chunk_states
+    float* out;
+    int L, H, G, P, N, Q, nc, nblocks;
+};
+
+template <typename T, int PT, int CTW, bool VARLEN>
+__global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
+    typedef MF<T> M;
+    constexpr int PAD = Pad<T>::v;
+    extern __shared__ __align__(16) char smem[];
+    const int P = PT * 16, N = CTW * 64;
+    const int Q = a.Q, L = a.L, H = a.H, nc = a.nc;
+    const int KB = min(Pad<T>::KB, Q);
+    const int SX = P + PAD, SB = N + PAD;
+    T* xs = reinterpret_cast<T*>(smem);               // [KB][SX]
+    T* bs = xs + KB * SX;                              // [KB][SB]
+    float* wq = reinterpret_cast<float*>(bs + KB * SB); // [Q]
+
+    const int work = xcd_remap(blockIdx.x, a.nblocks);
+    const int h = work % H;
+    const int g = h / (H / a.G);
+    int bi = 0, c, s = 0, qlo = 0, qhi, start = 0;
+    if (!VARLEN) {
+        const int rest = work / H;
+        c = rest % nc;
+        bi = rest / nc;
+        qhi = min(Q, L - c * Q);
+    } else {
+        s = work / H;
+        // clamp malformed boundaries into [0, L] so every access stays in bounds
+        const int end = min(max(a.cu_seqlens[s + 1], 0), L);
+        start = min(max(a.cu_seqlens[s], 0), end);
+        if (end <= start) {          // empty sequence: zero state
+            float* op = a.out + ((int64_t)s * H + h) * a.P * a.N;
+            for (int i = threadIdx.x; i < a.P * a.N; i += THREADS) op[i] = 0.f;
+            return;
+        }
+        c = (end - 1) / Q;
+        qlo = max(start - c * Q, 0);
+        qhi = end - c * Q;
+    }
+    const float* dAp = a.dA + (((int64_t)bi * H + h) * nc + c) * Q;
+    const float* dtp = a.dt + (((int64_t)bi * H + h) * nc + c) * Q;
+    const float dA_ref = dAp[qhi - 1];
+    int se = 0;
+    if (!VARLEN && a.seq_idx) se = a.seq_idx[(int64_t)bi * L + c * Q + qhi - 1];
+    for (int q = threadIdx.x; q < Q; q += THREADS) {
+        float v = 0.f;
+        if (q >= qlo && q < qhi) {
+            v = expf(fminf(dA_ref - dAp[q], 0.f)) * dtp[q];
+            if (!VARLEN && a.seq_idx &&
+                (se < 0 || a.seq_idx[(int64_t)bi * L + c * Q + q] != se))
+                v = 0.f;
+        }
+        wq[q] = v;
+    }
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int ln = lane & 15, kg = lane >> 4;
+    const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;   // token of position 0
+    const int valid = min(Q, L - c * Q);
+    const T* xsrc = reinterpret_cast<const T*>(a.x) + (tok0 * H + h) * P;
+    const T* bsrc = reinterpret_cast<const T*>(a.B) + (tok0 * a.G + g) * N;
+
+    f32x4 acc[PT][CTW];
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+        for (int j = 0; j < CTW; ++j) acc[pt][j] = zero4();
+
+    for (int kb = 0; kb < Q; kb += KB) {
+        if (kb) __syncthreads();
+        stage_rows<T>(xs, SX, xsrc + (int64_t)kb * H * P, (int64_t)H * P, KB, valid - kb, P);
+        stage_rows<T>(bs, SB, bsrc + (int64_t)kb * a.G * N, (int64_t)a.G * N, KB, valid - kb, N);
+        __syncthreads();
+        for (int k0 = 0; k0 < KB; k0 += M::K) {
+            typename M::frag af[PT], bfr[CTW];
+#pragma unroll
+            for (int j = 0; j < M::KPL; ++j) {
+                const int kl = k0 + kg * M::KPL + j;      // position within the block
+                const bool kok = kl < KB && kb + kl < Q;
+                const float wk = kok ? wq[kb + kl] : 0.f;
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) {
+                    const float xv = kok ? to_f32(xs[kl * SX + pt * 16 + ln]) : 0.f;
+                    M::set(af[pt], j, xv * wk);
+                }
+#pragma unroll
+                for (int jj = 0; jj < CTW; ++jj) {
+                    const int n = (w * CTW + jj) * 16 + ln;
+                    M::set_raw(bfr[jj], j, kok ? bs[kl * SB + n] : T(0.f));
+                }
+            }
+#pragma unroll
+            for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+                for (int jj = 0; jj < CTW; ++jj) acc[pt][jj] = M::mma(af[pt], bfr[jj], acc[pt][jj]);
+        }
+    }
+
+    float* op;
+    float carry_scale = 0.f;
+    const bf16* cs16 = nullptr;
+    const float* cs32 = nullptr;
+    if (!VARLEN) {
+        op = a.out + ((((int64_t)bi * nc + c) * H + h) * P) * N;
+    } else {
+        op = a.out + (((int64_t)s * H + h) * P) * N;
+        if (start < c * Q) {
+            carry_scale = expf(dA_ref);
+            const int64_t off = (((int64_t)c * H + h) * P) * N;
+            if (a.states_bf16) cs16 = reinterpret_cast<const bf16*>(a.chunk_states) + off;
+            else cs32 = reinterpret_cast<const float*>(a.chunk_states) + off;
+        }
+    }
+#pragma unroll
+    for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+        for (int jj = 0; jj < CTW; ++jj) {
+            const int n = (w * CTW + jj) * 16 + ln;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int p = pt * 16 + kg * 4 + i;
+                float v = acc[pt][jj][i];
+                if (VARLEN) {
+                    if (cs16) v += carry_scale * to_f32(cs16[p * N + n]);
+                    else if (cs32) v += carry_scale * cs32[p * N + n];
+                }
+                op[p * N + n] = v;
+            }
+        }
+}
+
+template <typename T, bool VARLEN>
+int launch_typed(const StateArgs& sa, int64_t nblocks, hipStream_t s) {
+    const int KB = Pad<T>::KB < sa.Q ? Pad<T>::KB : sa.Q;
+    const size_t shm = (size_t)KB * ((sa.P + Pad<T>::v) + (sa.N + Pad<T>::v)) * sizeof(T) +
+                       (size_t)sa.Q * sizeof(float);
+    const void* fn = nullptr;
+    void (*kern)(StateArgs) = nullptr;
+#define M2_CS_CASE(PTV, CTWV)                                       \
+    if (sa.P == PTV * 16 && sa.N == CTWV * 64) kern = k_chunk_state<T, PTV, CTWV, VARLEN>;
+    M2_CS_CASE(2, 1) M2_CS_CASE(2, 2) M2_CS_CASE(2, 4)
+    M2_CS_CASE(4, 1) M2_CS_CASE(4, 2) M2_CS_CASE(4, 4)
+    M2_CS_CASE(8, 1) M2_CS_CASE(8, 2) M2_CS_CASE(8, 4)
+#undef M2_CS_CASE
+    if (!kern)
+        return m2::set_error(M2_ERR_UNSUPPORTED,
+                             "chunk_state: headdim %d / dstate %d not supported "
+                             "(headdim in {32, 64, 128}, dstate in {64, 128, 256})",
+                             sa.P, sa.N);
+    fn = reinterpret_cast<const void*>(kern);
+    if (shm > 65536) {
+        if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) !=
+            hipSuccess)
+            return m2::set_error(M2_ERR_LAUNCH, "chunk_state: cannot reserve %zu B of LDS", shm);
+    }
+    kern<<<(unsigned)nblocks, THREADS, shm, s>>>(sa);
+    return m2::check_launch(VARLEN ? "chunk_state_varlen" : "chunk_state");
+}
+
+}  // namespace
+
+namespace m2 {
+
+int launch_chunk_state(const m2_chunk_state_args& a, hipStream_t s) {
+    M2_REQUIRE(a.x && a.B && a.dt && a.dA_cumsum && a.states, M2_ERR_INVALID,
+               "chunk_state: x, B, dt, dA_cumsum and states are required");
+    M2_REQUIRE(a.batch > 0 && a.seqlen > 0 && a.nheads > 0 && a.ngroups > 0 &&
+                   a.nheads % a.ngroups == 0 && a.chunk_size > 0,
+               M2_ERR_INVALID, "chunk_state: bad sizes (nheads must be a multiple of ngroups)");
+    M2_REQUIRE(a.chunk_size % 16 == 0 && a.chunk_size <= 256, M2_ERR_UNSUPPORTED,
+               "chunk_state: chunk_size must be a multiple of 16 and <= 256");
+    StateArgs sa{};
+    sa.x = a.x; sa.B = a.B; sa.dt = a.dt; sa.dA = a.dA_cumsum; sa.seq_idx = a.seq_idx;
+    sa.out = a.states;
+    sa.L = (int)a.seqlen; sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.P = (int)a.headdim;
+    sa.N = (int)a.dstate; sa.Q = (int)a.chunk_size;
+    sa.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
+    const int64_t nblocks = a.batch * sa.nc * a.nheads;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_state: too many blocks");
+    sa.nblocks = (int)nblocks;
+    if (a.dtype == M2_BF16) return launch_typed<bf16, false>(sa, nblocks, s);
+    if (a.dtype == M2_F32) return launch_typed<float, false>(sa, nblocks, s);
+    return set_error(M2_ERR_UNSUPPORTED, "chunk_state: dtype %d", a.dtype);
+}
+
+int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t s) {
+    M2_REQUIRE(a.x && a.B && a.dt && a.dA_cumsum && a.cu_seqlens && a.chunk_states && a.out,
+               M2_ERR_INVALID, "chunk_state_varlen: all pointers are required");
+    M2_REQUIRE(a.seqlen > 0 && a.nseq > 0 && a.nheads > 0 && a.ngroups > 0 &&
+                   a.nheads % a.ngroups == 0 && a.chunk_size > 0 &&
+                   a.nchunks == (a.seqlen + a.chunk_size - 1) / a.chunk_size,
+               M2_ERR_INVALID, "chunk_state_varlen: bad sizes");
+    M2_REQUIRE(a.chunk_size % 16 == 0 && a.chunk_size <= 256, M2_ERR_UNSUPPORTED,
+               "chunk_state_varlen: chunk_size must be a multiple of 16 and <= 256");
+    M2_REQUIRE(a.states_dtype == M2_F32 || a.states_dtype == M2_BF16, M2_ERR_UNSUPPORTED,
+               "chunk_state_varlen: states dtype %d", a.states_dtype);
+    StateArgs sa{};
+    sa.x = a.x; sa.B = a.B; sa.dt = a.dt; sa.dA = a.dA_cumsum; sa.cu_seqlens = a.cu_seqlens;
+    sa.chunk_states = a.chunk_states; sa.states_bf16 = a.states_dtype == M2_BF16; sa.out = a.out;
+    sa.L = (int)a.seqlen; sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.P = (int)a.headdim;
+    sa.N = (int)a.dstate; sa.Q = (int)a.chunk_size; sa.nc = (int)a.nchunks;
+    const int64_t nblocks = a.nseq * a.nheads;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_state_varlen: too many blocks");
+    sa.nblocks = (int)nblocks;
+    if (a.dtype == M2_BF16) return launch_typed<bf16, true>(sa, nblocks, s);
+    if (a.dtype == M2_F32) return launch_typed<float, true>(sa, nblocks, s);
+    return set_error(M2_ERR_UNSUPPORTED, "chunk_state_varlen: dtype %d", a.dtype);
+}
+
+}  // namespace m2

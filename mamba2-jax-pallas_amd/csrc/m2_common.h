@@ -1,0 +1,98 @@
+// Shared device helpers for the gfx950 SSD kernels: element types, MFMA
+// fragment traits, workgroup->XCD mapping and the error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "m2ssd.h"
+
+typedef __bf16 bf16;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+
+#define M2_DEV __device__ __forceinline__
+
+// ---------------------------------------------------------------------------
+// element conversion
+// ---------------------------------------------------------------------------
+M2_DEV float to_f32(float v) { return v; }
+M2_DEV float to_f32(bf16 v) { return (float)v; }
+
+template <typename T> M2_DEV T from_f32(float v);
+template <> M2_DEV float from_f32<float>(float v) { return v; }
+template <> M2_DEV bf16 from_f32<bf16>(float v) { return (bf16)v; }  // RNE
+
+// softplus(v) = log(1 + exp(v)), stable for all v
+M2_DEV float softplus_f(float v) { return fmaxf(v, 0.f) + log1pf(expf(-fabsf(v))); }
+M2_DEV float silu_f(float v) { return v / (1.f + expf(-v)); }
+
+// ---------------------------------------------------------------------------
+// MFMA 16x16 traits.  One instruction computes D(16x16) += A(16xK) B(Kx16).
+//   A operand: lane l holds row (l & 15), k = (l >> 4) * KPL + j, j < KPL
+//   B operand: lane l holds col (l & 15), same k
+//   D:         lane l holds col (l & 15), rows 4 * (l >> 4) + i, i < 4
+// bf16 inputs use v_mfma_f32_16x16x32_bf16 (K = 32), fp32 inputs use
+// v_mfma_f32_16x16x4_f32 (K = 4) so that fp32 callers keep fp32 operands.
+// ---------------------------------------------------------------------------
+template <typename T> struct MF;
+
+template <> struct MF<bf16> {
+    static constexpr int KPL = 8;
+    static constexpr int K = 32;
+    typedef bf16x8 frag;
+    static M2_DEV f32x4 mma(const frag& a, const frag& b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static M2_DEV void set(frag& f, int j, float v) { f[j] = (bf16)v; }
+    static M2_DEV void set_raw(frag& f, int j, bf16 v) { f[j] = v; }
+};
+
+template <> struct MF<float> {
+    static constexpr int KPL = 1;
+    static constexpr int K = 4;
+    typedef float frag;
+    static M2_DEV f32x4 mma(frag a, frag b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+    static M2_DEV void set(frag& f, int, float v) { f = v; }
+    static M2_DEV void set_raw(frag& f, int, float v) { f = v; }
+};
+
+// Load KPL consecutive elements (16 B for bf16, 4 B for fp32) as a fragment.
+M2_DEV bf16x8 load_frag(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+M2_DEV float load_frag(const float* p) { return *p; }
+
+M2_DEV f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
+
+// ---------------------------------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+// L2).  Remap the hardware block id so that each XCD receives a contiguous
+// range of work ids: neighbouring work items (heads of one group, which share
+// B / C / CB tiles) then share an L2.
+// ---------------------------------------------------------------------------
+M2_DEV int xcd_remap(int bid, int nblocks) {
+    const int nx = 8;
+    int per = nblocks / nx, rem = nblocks % nx;
+    int xcd = bid % nx, local = bid / nx;
+    return xcd * per + (xcd < rem ? xcd : rem) + local;
+}
+
+// ---------------------------------------------------------------------------
+// error plumbing (host side)
+// ---------------------------------------------------------------------------
+namespace m2 {
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+}  // namespace m2
+
+#define M2_REQUIRE(cond, code, ...)                              \
+    do {                                                         \
+        if (!(cond)) return ::m2::set_error((code), __VA_ARGS__); \
+    } while (0)
+
+// element size of an M2_* dtype code (0 if unknown)
+static inline size_t m2_dtype_size(int32_t dt) {
+    return dt == M2_F32 ? 4 : dt == M2_BF16 ? 2 : 0;
+}

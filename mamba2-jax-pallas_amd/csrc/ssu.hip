@@ -1,0 +1,151 @@
+// selective_state_update: one decode token, fp32 state updated in place
+//   dt' = softplus?(dt + dt_bias)
+//   state[p,n] = state[p,n] * exp(dt' A) + dt' x[p] B[n]
+//   y[p] = sum_n state[p,n] C[n] + D x[p];   y *= silu(z[p])
+//
+// HBM-bound: the state (b*H*P*N fp32) is read and written exactly once.  One
+// workgroup per (batch, head); each thread owns 4 consecutive n (16-byte
+// accesses) of RPT rows p, issuing all RPT state loads before any arithmetic
+// so that RPT x 16 B stay in flight per thread.  The readout over n is a
+// butterfly reduction across the N/4 lanes that share a row.
+//
+// Follows reference ops/selective_state_update.py:68-123.
+#include "m2_internal.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+
+struct SsuArgs {
+    float* state;
+    const void* x;
+    const void* dt;
+    const float* A;
+    const void* B;
+    const void* C;
+    const float* D;
+    const void* z;
+    const float* dt_bias;
+    float* out;
+    int H, G, P, N;
+    int dt_bf16, dt_has_hdim, A_full, D_has_hdim, bias_has_hdim, softplus;
+};
+
+template <typename T> M2_DEV float ld(const void* p, int64_t i) {
+    return to_f32(reinterpret_cast<const T*>(p)[i]);
+}
+
+// TPR = threads per row (N / 4), RPT = rows per thread
+template <typename T, int TPR, int RPT>
+__global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
+    constexpr int ROWS_PER_PASS = THREADS / TPR;
+    const int bh = blockIdx.x;
+    const int bi = bh / a.H, h = bh % a.H;
+    const int g = h / (a.H / a.G);
+    const int P = a.P, N = a.N;
+    const int tr = threadIdx.x / TPR;           // row within a pass
+    const int n0 = (threadIdx.x % TPR) * 4;
+    float* st = a.state + (int64_t)bh * P * N;
+
+    float Bv[4], Cv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        Bv[j] = ld<T>(a.B, ((int64_t)bi * a.G + g) * N + n0 + j);
+        Cv[j] = ld<T>(a.C, ((int64_t)bi * a.G + g) * N + n0 + j);
+    }
+    float4 s[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        const int p = r * ROWS_PER_PASS + tr;
+        if (p < P) s[r] = *reinterpret_cast<const float4*>(st + (int64_t)p * N + n0);
+    }
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        const int p = r * ROWS_PER_PASS + tr;
+        if (p >= P) continue;
+        const int64_t hp = (int64_t)bh * P + p;       // (batch, head, p) index
+        float d = a.dt_has_hdim ? (a.dt_bf16 ? ld<bf16>(a.dt, hp) : ld<float>(a.dt, hp))
+                                : (a.dt_bf16 ? ld<bf16>(a.dt, bh) : ld<float>(a.dt, bh));
+        if (a.dt_bias) d += a.bias_has_hdim ? a.dt_bias[h * P + p] : a.dt_bias[h];
+        if (a.softplus) d = softplus_f(d);
+        const float xv = ld<T>(a.x, hp);
+        const float dx = d * xv;
+        float v[4] = {s[r].x, s[r].y, s[r].z, s[r].w};
+        float part = 0.f;
+        if (a.A_full) {
+            const float* Ar = a.A + ((int64_t)h * P + p) * N + n0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j] = v[j] * expf(d * Ar[j]) + dx * Bv[j];
+                part += v[j] * Cv[j];
+            }
+        } else {
+            const float dA = expf(d * a.A[h]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[j] = v[j] * dA + dx * Bv[j];
+                part += v[j] * Cv[j];
+            }
+        }
+        *reinterpret_cast<float4*>(st + (int64_t)p * N + n0) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int off = TPR / 2; off > 0; off >>= 1) part += __shfl_xor(part, off, TPR);
+        if (threadIdx.x % TPR == 0) {
+            float y = part;
+            if (a.D) y += (a.D_has_hdim ? a.D[h * P + p] : a.D[h]) * xv;
+            if (a.z) y *= silu_f(ld<T>(a.z, hp));
+            a.out[hp] = y;
+        }
+    }
+}
+
+template <typename T>
+int launch_typed(const SsuArgs& sa, int64_t nblocks, hipStream_t s) {
+    void (*kern)(SsuArgs) = nullptr;
+    const int tpr = sa.N / 4;
+    const int rows_per_pass = THREADS / tpr;
+    const int rpt = (sa.P + rows_per_pass - 1) / rows_per_pass;
+#define M2_SSU_CASE(TPRV, RPTV) \
+    if (tpr == TPRV && rpt <= RPTV && !kern) kern = k_ssu<T, TPRV, RPTV>;
+    M2_SSU_CASE(8, 2) M2_SSU_CASE(8, 4)                       // N = 32
+    M2_SSU_CASE(16, 4) M2_SSU_CASE(16, 8)                     // N = 64
+    M2_SSU_CASE(32, 4) M2_SSU_CASE(32, 8) M2_SSU_CASE(32, 16) // N = 128
+    M2_SSU_CASE(64, 8) M2_SSU_CASE(64, 16) M2_SSU_CASE(64, 32) // N = 256
+#undef M2_SSU_CASE
+    if (!kern)
+        return m2::set_error(M2_ERR_UNSUPPORTED,
+                             "selective_state_update: dstate %d / headdim %d not supported", sa.N,
+                             sa.P);
+    kern<<<(unsigned)nblocks, THREADS, 0, s>>>(sa);
+    return m2::check_launch("selective_state_update");
+}
+
+}  // namespace
+
+namespace m2 {
+
+int launch_ssu(const m2_ssu_args& a, hipStream_t s) {
+    M2_REQUIRE(a.state && a.x && a.dt && a.A && a.B && a.C && a.out, M2_ERR_INVALID,
+               "selective_state_update: state, x, dt, A, B, C and out are required");
+    M2_REQUIRE(a.batch > 0 && a.nheads > 0 && a.ngroups > 0 && a.nheads % a.ngroups == 0 &&
+                   a.headdim > 0 && a.dstate > 0,
+               M2_ERR_INVALID, "selective_state_update: bad sizes");
+    M2_REQUIRE(a.dstate % 4 == 0, M2_ERR_UNSUPPORTED,
+               "selective_state_update: dstate must be a multiple of 4 (got %lld)",
+               (long long)a.dstate);
+    M2_REQUIRE(a.dt_dtype == M2_F32 || a.dt_dtype == M2_BF16, M2_ERR_UNSUPPORTED,
+               "selective_state_update: dt dtype %d", a.dt_dtype);
+    const int64_t nblocks = a.batch * a.nheads;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "selective_state_update: too many blocks");
+    SsuArgs sa{};
+    sa.state = a.state; sa.x = a.x; sa.dt = a.dt; sa.A = a.A; sa.B = a.B; sa.C = a.C; sa.D = a.D;
+    sa.z = a.z; sa.dt_bias = a.dt_bias; sa.out = a.out;
+    sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.P = (int)a.headdim; sa.N = (int)a.dstate;
+    sa.dt_bf16 = a.dt_dtype == M2_BF16; sa.dt_has_hdim = a.dt_has_hdim; sa.A_full = a.A_full;
+    sa.D_has_hdim = a.D_has_hdim; sa.bias_has_hdim = a.dt_bias_has_hdim; sa.softplus = a.dt_softplus;
+    if (a.dtype == M2_BF16) return launch_typed<bf16>(sa, nblocks, s);
+    if (a.dtype == M2_F32) return launch_typed<float>(sa, nblocks, s);
+    return set_error(M2_ERR_UNSUPPORTED, "selective_state_update: dtype %d", a.dtype);
+}
+
+}  // namespace m2

@@ -1,0 +1,136 @@
+// state_passing: the sequential inter-chunk recurrence
+//   out[c] = s_c,  s_{c+1} = exp(dA_last[c]) * s_c + states[c],  final = s_nc
+// over b * H independent rows of D = P * N float32 values.
+//
+// HBM-bound streaming kernel.  Each thread owns VW consecutive elements of one
+// (batch, head) row and walks the chunks in order, keeping its running state
+// in registers; chunk c+DEPTH is loaded while chunk c is combined so that
+// DEPTH 16-byte loads per thread stay in flight.  Loads and stores are 16 B
+// per lane (8 B for bf16 output) and contiguous across the workgroup.  The
+// per-chunk decay and the seq_idx reset are wave-uniform scalars.
+//
+// Follows reference kernels/state_passing_fwd.py:108-151 (recurrence),
+// :208-225 (seq_idx reset: end-of-chunk id differs from the previous chunk's,
+// previous id of chunk 0 is 0) and ops/ssd_naive.py:135-182.
+#include "m2_internal.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int DEPTH = 4;
+
+template <int VW> struct Vec;
+template <> struct Vec<4> {
+    float v[4];
+    M2_DEV void load(const float* p) {
+        float4 t = *reinterpret_cast<const float4*>(p);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
+    M2_DEV void store(float* p) const {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    M2_DEV void store(bf16* p) const {
+        typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+        bf16x4 t = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+        *reinterpret_cast<bf16x4*>(p) = t;
+    }
+};
+template <> struct Vec<1> {
+    float v[1];
+    M2_DEV void load(const float* p) { v[0] = *p; }
+    M2_DEV void store(float* p) const { *p = v[0]; }
+    M2_DEV void store(bf16* p) const { *p = (bf16)v[0]; }
+};
+
+template <typename TO, int VW>
+__global__ void __launch_bounds__(THREADS)
+k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
+                int64_t sb, int64_t sh, int64_t sc, const float* __restrict__ init,
+                const int32_t* __restrict__ seq_idx, TO* __restrict__ out,
+                float* __restrict__ fin, int nc, int H, int64_t D, int L, int Q,
+                int blocks_per_row) {
+    const int row = blockIdx.x / blocks_per_row;          // (batch, head)
+    const int blk = blockIdx.x % blocks_per_row;
+    const int bi = row / H, h = row % H;
+    const int64_t d0 = ((int64_t)blk * THREADS + threadIdx.x) * VW;
+    if (d0 >= D) return;
+    const int64_t cstride = (int64_t)H * D;                // between chunks
+    const float* src = states + ((int64_t)bi * nc * H + h) * D + d0;
+    TO* dst = out + ((int64_t)bi * nc * H + h) * D + d0;
+    const float* dA = dAc + (int64_t)bi * sb + (int64_t)h * sh;
+
+    Vec<VW> run;
+    if (init) {
+        run.load(init + ((int64_t)bi * H + h) * D + d0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) run.v[j] = 0.f;
+    }
+    Vec<VW> buf[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH; ++i)
+        if (i < nc) buf[i].load(src + i * cstride);
+    int prev_seq = 0;
+    for (int c0 = 0; c0 < nc; c0 += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            const int c = c0 + i;
+            if (c < nc) {
+                run.store(dst + c * cstride);
+                float scale = expf(dA[(int64_t)c * sc]);
+                if (seq_idx) {
+                    const int end = min((c + 1) * Q, L) - 1;
+                    const int cur = seq_idx[(int64_t)bi * L + end];
+                    if (cur != prev_seq) scale = 0.f;
+                    prev_seq = cur;
+                }
+                const Vec<VW> st = buf[i];
+                if (c + DEPTH < nc) buf[i].load(src + (int64_t)(c + DEPTH) * cstride);
+#pragma unroll
+                for (int j = 0; j < VW; ++j) run.v[j] = fmaf(scale, run.v[j], st.v[j]);
+            }
+        }
+    }
+    if (fin) run.store(fin + ((int64_t)bi * H + h) * D + d0);
+}
+
+template <typename TO>
+int launch_typed(const m2_state_passing_args& a, hipStream_t s) {
+    const int vw = (a.dim % 4 == 0) ? 4 : 1;
+    const int64_t per_block = (int64_t)THREADS * vw;
+    const int bpr = (int)((a.dim + per_block - 1) / per_block);
+    const int64_t nblocks = a.batch * a.nheads * bpr;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "state_passing: too many blocks");
+    if (vw == 4)
+        k_state_passing<TO, 4><<<(unsigned)nblocks, THREADS, 0, s>>>(
+            a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
+            a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
+            (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
+    else
+        k_state_passing<TO, 1><<<(unsigned)nblocks, THREADS, 0, s>>>(
+            a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
+            a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
+            (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
+    return m2::check_launch("state_passing");
+}
+
+}  // namespace
+
+namespace m2 {
+
+int launch_state_passing(const m2_state_passing_args& a, hipStream_t s) {
+    M2_REQUIRE(a.states && a.dA_chunk_cumsum && a.out, M2_ERR_INVALID,
+               "state_passing: states, dA_chunk_cumsum and out are required");
+    M2_REQUIRE(a.batch > 0 && a.nchunks > 0 && a.nheads > 0 && a.dim > 0, M2_ERR_INVALID,
+               "state_passing: sizes must be positive");
+    M2_REQUIRE(!a.seq_idx || (a.chunk_size > 0 && a.seqlen > 0 &&
+                              a.seqlen > (a.nchunks - 1) * a.chunk_size &&
+                              a.seqlen <= a.nchunks * a.chunk_size),
+               M2_ERR_INVALID, "state_passing: seq_idx needs chunk_size and a seqlen that "
+               "spans nchunks chunks");
+    if (a.out_dtype == M2_F32) return launch_typed<float>(a, s);
+    if (a.out_dtype == M2_BF16) return launch_typed<bf16>(a, s);
+    return set_error(M2_ERR_UNSUPPORTED, "state_passing: out dtype %d", a.out_dtype);
+}
+
+}  // namespace m2

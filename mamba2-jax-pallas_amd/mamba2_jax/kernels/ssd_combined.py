@@ -1,0 +1,128 @@
+"""mamba_chunk_scan_combined_fwd on MI355X: the whole SSD layer forward.
+
+Drop-in for reference kernels/ssd_combined.py:46-203.  One call into
+libm2ssd.so (m2_ssd_combined) enqueues the five stage kernels
+(chunk_cumsum -> chunk_state -> state_passing -> bmm_chunk -> chunk_scan, plus
+chunk_state_varlen when varlen states are requested) on the current stream;
+the intermediates live in a workspace drawn from torch's caching allocator.
+As in the reference, the state entering each chunk is kept in x's dtype,
+while the output and the final states are float32.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib as L
+from .chunk_state_fwd import _io_dtype, _seq_idx
+
+
+def _events_array(events):
+    """Raw hipEvent_t handles of 6 torch.cuda.Event objects (created on first record)."""
+    import ctypes
+    if events is None:
+        return None, None
+    if len(events) != 6:
+        raise ValueError("_stage_events needs 6 events")
+    for e in events:
+        if not e.cuda_event:
+            e.record()          # forces creation of the underlying event
+    arr = (ctypes.c_void_p * 6)(*[e.cuda_event for e in events])
+    return arr, ctypes.cast(arr, ctypes.c_void_p).value
+
+
+def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
+                                  initial_states=None, seq_idx=None, cu_seqlens=None,
+                                  dt_softplus=False, dt_limit=(0.0, float("inf")),
+                                  return_final_states=False, return_varlen_states=False,
+                                  *, _stage_events=None):
+    """SSD chunked-scan forward.
+
+    x (batch, seqlen, nheads, headdim), dt (batch, seqlen, nheads), A (nheads,),
+    B / C (batch, seqlen, ngroups, dstate), D (nheads,) or (nheads, headdim),
+    z like x, dt_bias (nheads,), initial_states (batch, nheads, headdim, dstate),
+    seq_idx (batch, seqlen) int32, cu_seqlens (nseq + 1,) int32.
+
+    Returns out (float32, like x), then final_states (batch, nheads, headdim,
+    dstate) if return_final_states, then varlen_states (nseq, nheads, headdim,
+    dstate) if return_varlen_states -- the reference's arity
+    (kernels/ssd_combined.py:194-203).
+
+    ``_stage_events`` (optional, 6 torch.cuda.Event) is a profiling hook: the
+    events are recorded before the first and after each of the five stages.
+    """
+    dev = L.device_of(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, cu_seqlens)
+    L.require(x.dim() == 4, "x must be (batch, seqlen, nheads, headdim)")
+    batch, seqlen, nheads, headdim = x.shape
+    L.require(B.dim() == 4 and tuple(B.shape[:2]) == (batch, seqlen),
+              "B must be (batch, seqlen, ngroups, dstate)")
+    _, _, ngroups, dstate = B.shape
+    L.require(tuple(C.shape) == tuple(B.shape), "C.shape != B.shape")
+    L.require(tuple(dt.shape) == (batch, seqlen, nheads), f"dt.shape={tuple(dt.shape)}")
+    L.require(tuple(A.shape) == (nheads,), f"A.shape={tuple(A.shape)} != ({nheads},)")
+    L.require(nheads % ngroups == 0, "nheads must be a multiple of ngroups")
+    if dt_bias is not None:
+        L.require(tuple(dt_bias.shape) == (nheads,), f"dt_bias.shape={tuple(dt_bias.shape)}")
+    D_has_hdim = 0
+    if D is not None:
+        if D.dim() == 2:
+            L.require(tuple(D.shape) == (nheads, headdim), f"D.shape={tuple(D.shape)}")
+            D_has_hdim = 1
+        else:
+            L.require(tuple(D.shape) == (nheads,), f"D.shape={tuple(D.shape)}")
+    if z is not None:
+        L.require(tuple(z.shape) == tuple(x.shape), "z.shape != x.shape")
+    if initial_states is not None:
+        L.require(tuple(initial_states.shape) == (batch, nheads, headdim, dstate),
+                  f"initial_states.shape={tuple(initial_states.shape)}")
+    chunk_size = int(chunk_size)
+    L.require(chunk_size > 0, "chunk_size must be positive")
+    if not return_varlen_states:
+        cu_seqlens = None
+    nseq = 0
+    if cu_seqlens is not None:
+        L.require(batch == 1, "cu_seqlens for varlen states is only supported with batch=1")
+        L.require(cu_seqlens.dim() == 1 and cu_seqlens.shape[0] >= 2,
+                  "cu_seqlens must be (num_sequences + 1,)")
+        nseq = int(cu_seqlens.shape[0]) - 1
+    elif return_varlen_states:
+        raise L.M2ShapeError("return_varlen_states needs cu_seqlens")
+
+    io = _io_dtype(x, B, C, z)
+    x_c, B_c, C_c, z_c = (L.dev_contig(t, io) for t in (x, B, C, z))
+    dt_c = L.dev_contig(dt if dt.dtype in (torch.float32, torch.bfloat16) else dt.float())
+    A_c, D_c, bias_c = (L.dev_contig(t, torch.float32) for t in (A, D, dt_bias))
+    init = L.dev_contig(initial_states, torch.float32)
+    seq = _seq_idx(seq_idx, batch, seqlen)
+    cu = L.dev_contig(cu_seqlens, torch.int32)
+
+    out = torch.empty((batch, seqlen, nheads, headdim), dtype=torch.float32, device=dev)
+    fin = (torch.empty((batch, nheads, headdim, dstate), dtype=torch.float32, device=dev)
+           if return_final_states else None)
+    vs = (torch.empty((nseq, nheads, headdim, dstate), dtype=torch.float32, device=dev)
+          if cu is not None else None)
+    ev_keep, ev_ptr = _events_array(_stage_events)
+    args = L.SsdCombinedArgs(
+        x=L.ptr(x_c), dt=L.ptr(dt_c), A=L.ptr(A_c), B=L.ptr(B_c), C=L.ptr(C_c), D=L.ptr(D_c),
+        z=L.ptr(z_c), dt_bias=L.ptr(bias_c), initial_states=L.ptr(init), seq_idx=L.ptr(seq),
+        cu_seqlens=L.ptr(cu), out=L.ptr(out), final_states=L.ptr(fin), varlen_states=L.ptr(vs),
+        batch=batch, seqlen=seqlen, nheads=nheads, headdim=headdim, ngroups=ngroups,
+        dstate=dstate, chunk_size=chunk_size, nseq=nseq, dtype=L.dtype_code(x_c, "x"),
+        dt_dtype=L.dtype_code(dt_c, "dt"), D_has_hdim=D_has_hdim,
+        dt_softplus=int(bool(dt_softplus)), dt_min=float(dt_limit[0]),
+        dt_max=float(dt_limit[1]), stage_events=ev_ptr)
+    lib = L.load_library()
+    import ctypes
+    ws_bytes = lib.m2_ssd_combined_workspace_size(ctypes.byref(args))
+    L.require(ws_bytes > 0, "m2_ssd_combined_workspace_size rejected the arguments")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    args.workspace = ws.data_ptr()
+    args.workspace_bytes = ws_bytes
+    with torch.cuda.device(dev):
+        L.call("m2_ssd_combined", args, L.stream_of(dev))
+    del ev_keep
+    if not return_varlen_states:
+        return (out, fin) if return_final_states else out
+    return (out, fin, vs) if return_final_states else (out, vs)

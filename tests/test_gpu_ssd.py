@@ -1,0 +1,152 @@
+"""Parity of the whole SSD forward (mamba_chunk_scan_combined_fwd) on the GPU.
+
+* against the CPU oracle (float64) at the benchmark shapes: c0 and c2 in full,
+  c1 / c3 with fewer heads or tokens (the oracle's memory grows with L*H*Q);
+* at the full c1 / c3 sizes through size-independent properties: agreement
+  with the naive formulation run on the GPU (c1) and packed == per-sequence
+  runs (c3);
+* chunk-size invariance, L % Q != 0, D per head-dim, z gate, dispatch.
+Tolerance: max|err|/rms <= 1e-3 (fp32 inputs), 2e-2 (bf16), outputs and
+final states alike.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TOL, announce, check, dev, host, tdtype
+from mamba2_jax import configs
+from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
+from mamba2_jax.modules.mamba2 import _ssd_combined_fwd
+from mamba2_jax.ops import mamba_chunk_scan_combined_naive
+from oracle import ssd_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev_inputs(d, dtype):
+    T = tdtype(dtype)
+    return dict(x=dev(d["x"], T), dt=dev(d["dt"], T), A=dev(d["A"]), B=dev(d["B"], T),
+                C=dev(d["C"], T), D=dev(d["D"]), z=dev(d["z"], T), dt_bias=dev(d["dt_bias"]),
+                initial_states=dev(d["initial_states"]), seq_idx=dev(d["seq_idx"]),
+                cu_seqlens=dev(d["cu_seqlens"]))
+
+
+def _run_and_check(cfg, with_z=False, varlen=False, Dhp=False):
+    d = configs.make_ssd_inputs(cfg, with_z=with_z)
+    if Dhp:
+        d["D"] = np.random.default_rng(1).uniform(0.5, 1.5, (cfg.nheads, cfg.headdim)).astype(np.float32)
+    kw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
+              return_varlen_states=varlen)
+    got = mamba_chunk_scan_combined_fwd(**_dev_inputs(d, cfg.dtype), **kw)
+    want = O.ssd_combined(io_dtype=cfg.dtype, **d, **kw)
+    tol = TOL[cfg.dtype]
+    check(got[0], want[0], tol, "out")
+    check(got[1], want[1], tol, "final_states")
+    if varlen:
+        check(got[2], want[2], tol, "varlen_states")
+    assert got[0].dtype == torch.float32 and got[1].dtype == torch.float32
+
+
+def test_c0_full_fp32():
+    announce("c0 full")
+    _run_and_check(configs.CONFIGS["c0"])
+
+
+def test_c2_full_headline():
+    announce("c2 full (nemotron-h-8b, headline)")
+    _run_and_check(configs.CONFIGS["c2"])
+
+
+def test_c1_fewer_tokens():
+    announce("c1 b=2 L=512")
+    _run_and_check(dataclasses.replace(configs.CONFIGS["c1"], batch=2, seqlen=512))
+
+
+def test_c3_fewer_heads_and_tokens_varlen():
+    announce("c3 L=2048 H=32 varlen")
+    cfg = dataclasses.replace(configs.CONFIGS["c3"], seqlen=2048, nheads=32, min_seqlen=64)
+    _run_and_check(cfg, varlen=True)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_gate_D_per_headdim_and_ragged_length(dtype):
+    announce("z + D[H,P] + L%Q", dtype)
+    cfg = configs.SSDConfig("ragged", 2, 333, 16, 4, 64, 64, 128, dtype, init_state=True, seed=21)
+    _run_and_check(cfg, with_z=True, Dhp=True)
+
+
+def test_headdim_128_dstate_256_chunk_64():
+    announce("P=128 N=256 Q=64")
+    cfg = configs.SSDConfig("wide", 1, 256, 8, 2, 128, 256, 64, "bf16", seed=22)
+    _run_and_check(cfg)
+
+
+def test_c1_full_vs_naive_on_gpu():
+    """Full c1 (with initial state) against the naive formulation in float32 on the GPU."""
+    announce("c1 full vs naive")
+    cfg = configs.CONFIGS["c1"]
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, cfg.dtype)
+    kw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True)
+    y, f = mamba_chunk_scan_combined_fwd(**t, **kw)
+    t.pop("seq_idx"), t.pop("cu_seqlens")
+    yn, fn = mamba_chunk_scan_combined_naive(**t, **kw)
+    check(y, host(yn), TOL["bf16"], "out")
+    check(f, host(fn), TOL["bf16"], "final_states")
+
+
+def test_c3_full_packed_equals_per_sequence():
+    """Full c3: the packed run equals independent runs of each sequence."""
+    announce("c3 full packed vs per-sequence")
+    cfg = configs.CONFIGS["c3"]
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, cfg.dtype)
+    y, fin, vs = mamba_chunk_scan_combined_fwd(
+        chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
+        return_varlen_states=True, **t)
+    cu = d["cu_seqlens"]
+    errs = []
+    for s in range(cfg.nseq):
+        sl = slice(int(cu[s]), int(cu[s + 1]))
+        part = {k: (v[:, sl].contiguous() if k in ("x", "dt", "B", "C") else v)
+                for k, v in t.items() if k not in ("seq_idx", "cu_seqlens", "z", "initial_states")}
+        ys, fs = mamba_chunk_scan_combined_fwd(chunk_size=cfg.chunk_size, dt_softplus=True,
+                                               return_final_states=True, **part)
+        errs.append(check(y[:, sl], host(ys), TOL["bf16"], f"seq {s} out"))
+        check(vs[s], host(fs[0]), TOL["bf16"], f"seq {s} varlen state")
+    check(fin[0], host(vs[-1]), 1e-6, "final == last varlen state")
+
+
+def test_chunk_size_invariance():
+    announce("chunk-size invariance")
+    cfg = dataclasses.replace(configs.CONFIGS["c2"], seqlen=1024)
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, cfg.dtype)
+    outs = [mamba_chunk_scan_combined_fwd(chunk_size=q, dt_softplus=True,
+                                          return_final_states=True, **t) for q in (64, 128, 256)]
+    for y, f in outs[1:]:
+        check(y, host(outs[0][0]), TOL["bf16"], "out")
+        check(f, host(outs[0][1]), TOL["bf16"], "final")
+
+
+def test_return_arity_and_dispatch():
+    announce("arity + dispatch")
+    cfg = configs.SSDConfig("small", 1, 256, 8, 2, 64, 64, 64, "f32", nseq=2, min_seqlen=64, seed=3)
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, "f32")
+    y = mamba_chunk_scan_combined_fwd(chunk_size=64, **t)
+    assert isinstance(y, torch.Tensor)
+    r = mamba_chunk_scan_combined_fwd(chunk_size=64, return_varlen_states=True, **t)
+    assert len(r) == 2 and r[1].shape == (2, 8, 64, 64)
+    r = mamba_chunk_scan_combined_fwd(chunk_size=64, return_final_states=True,
+                                      return_varlen_states=True, **t)
+    assert len(r) == 3
+    yd = _ssd_combined_fwd(use_pallas=True, chunk_size=64, **t)
+    torch.testing.assert_close(yd, y, rtol=0, atol=0)
+    t.pop("seq_idx"), t.pop("cu_seqlens")
+    yn = _ssd_combined_fwd(use_pallas=False, chunk_size=64, **t)
+    yh = _ssd_combined_fwd(use_pallas=True, chunk_size=64, **t)
+    check(yh, host(yn), TOL["f32"], "hip vs naive")

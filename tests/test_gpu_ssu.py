@@ -1,0 +1,119 @@
+"""Parity of the decode step (selective_state_update) on the GPU.
+
+* one step against the oracle's closed form at the c4 shape and with every
+  parameter-shape variant the reference supports;
+* 256 consecutive in-place steps against the oracle's float64 trajectory and
+  against the HIP prefill over the same tokens (decode == prefill);
+* in-place / copy semantics.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TOL, announce, check, dev, host
+from mamba2_jax import configs
+from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
+from mamba2_jax.ops import selective_state_update
+from oracle import ssd_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _step_inputs(rng, b, H, G, P, N, dt_hdim=False, A_full=False, D_hdim=False,
+                 bias_hdim=False, with_D=True, with_z=True):
+    bf = lambda a: configs.round_to(a.astype(np.float32), "bf16")
+    return dict(
+        state=(0.1 * rng.standard_normal((b, H, P, N))).astype(np.float32),
+        x=bf(rng.standard_normal((b, H, P))),
+        dt=rng.standard_normal((b, H, P) if dt_hdim else (b, H)).astype(np.float32),
+        A=(-np.exp(rng.uniform(0, np.log(16), (H, P, N) if A_full else H))).astype(np.float32),
+        B=bf(rng.standard_normal((b, G, N)) / np.sqrt(N)),
+        C=bf(rng.standard_normal((b, G, N)) / np.sqrt(N)),
+        D=rng.uniform(0.5, 1.5, (H, P) if D_hdim else H).astype(np.float32) if with_D else None,
+        z=bf(rng.standard_normal((b, H, P))) if with_z else None,
+        dt_bias=rng.uniform(-4, -2, (H, P) if bias_hdim else H).astype(np.float32),
+    )
+
+
+def _dev(d):
+    bfk = ("x", "B", "C", "z")
+    return {k: dev(v, torch.bfloat16 if k in bfk else None) for k, v in d.items()}
+
+
+@pytest.mark.parametrize("b,H,G,P,N,kw", [
+    (64, 128, 8, 64, 128, {}),                                  # c4 shape
+    (4, 16, 1, 64, 64, dict(dt_hdim=True, bias_hdim=True)),
+    (4, 16, 4, 32, 128, dict(A_full=True, D_hdim=True)),
+    (2, 8, 2, 128, 256, dict(with_z=False)),
+    (3, 6, 3, 64, 32, dict(with_D=False, with_z=False)),
+])
+@pytest.mark.parametrize("softplus", [True, False])
+def test_single_step(b, H, G, P, N, kw, softplus):
+    announce("ssu step", b, H, G, P, N, kw, softplus)
+    rng = np.random.default_rng(b + H + P + N)
+    d = _step_inputs(rng, b, H, G, P, N, **kw)
+    if not softplus:
+        d["dt"] = np.abs(d["dt"]) * 0.05
+        d["dt_bias"] = None
+    t = _dev(d)
+    new, y = selective_state_update(**t, dt_softplus=softplus)
+    ws, wy = O.selective_state_update(**d, dt_softplus=softplus)
+    check(new, ws, 1e-5, "state")
+    check(y, wy, 1e-4, "out")
+
+
+def test_256_steps_trajectory_and_prefill():
+    """c4 recurrence (b reduced to 2): 256 in-place steps == the oracle's float64
+    trajectory, and == the SSD prefill over the same 256 tokens."""
+    cfg = configs.DecodeConfig("c4-small", 2, 128, 8, 64, 128, 256)
+    announce("ssu 256 steps", cfg)
+    d = configs.make_decode_inputs(cfg)
+    state = dev(d["state"])
+    s0 = state.clone()
+    ys = []
+    ref = d["state"].astype(np.float64)
+    wys = []
+    for t in range(cfg.steps):
+        z = dev(d["z"][t], torch.bfloat16)
+        new, y = selective_state_update(state, dev(d["x"][t], torch.bfloat16), dev(d["dt"][t]),
+                                        dev(d["A"]), dev(d["B"][t], torch.bfloat16),
+                                        dev(d["C"][t], torch.bfloat16), D=dev(d["D"]), z=z,
+                                        dt_bias=dev(d["dt_bias"]), dt_softplus=True)
+        assert new.data_ptr() == state.data_ptr()
+        ys.append(y)
+        ref, wy = O.selective_state_update(ref, d["x"][t], d["dt"][t], d["A"], d["B"][t],
+                                           d["C"][t], D=d["D"], z=d["z"][t],
+                                           dt_bias=d["dt_bias"], dt_softplus=True)
+        wys.append(wy)
+    Y = torch.stack(ys, dim=1)                                 # (b, T, H, P)
+    check(state, ref, 1e-4, "state after 256 steps")
+    check(Y, np.stack(wys, axis=1), 1e-4, "outputs of 256 steps")
+    # prefill of the same tokens (bf16 inputs -> bf16 tolerance for the chunked path)
+    tok = lambda a: torch.from_numpy(np.ascontiguousarray(np.swapaxes(a, 0, 1)))
+    yp, fp = mamba_chunk_scan_combined_fwd(
+        tok(d["x"]).to(torch.bfloat16).cuda(), tok(d["dt"]).cuda(), dev(d["A"]),
+        tok(d["B"]).to(torch.bfloat16).cuda(), tok(d["C"]).to(torch.bfloat16).cuda(), 64,
+        D=dev(d["D"]), z=tok(d["z"]).to(torch.bfloat16).cuda(), dt_bias=dev(d["dt_bias"]),
+        initial_states=s0, dt_softplus=True, return_final_states=True)
+    check(Y, host(yp), TOL["bf16"], "decode == prefill (outputs)")
+    check(state, host(fp), TOL["bf16"], "decode == prefill (final state)")
+
+
+def test_inplace_and_copy_semantics():
+    announce("ssu in-place / copy")
+    rng = np.random.default_rng(5)
+    d = _step_inputs(rng, 2, 8, 2, 64, 128)
+    t = _dev(d)
+    s_before = t["state"].clone()
+    new, _ = selective_state_update(**{**t, "state": t["state"]}, dt_softplus=True, inplace=False)
+    assert new.data_ptr() != t["state"].data_ptr()
+    torch.testing.assert_close(t["state"], s_before, rtol=0, atol=0)
+    new2, _ = selective_state_update(**t, dt_softplus=True)
+    assert new2.data_ptr() == t["state"].data_ptr()
+    torch.testing.assert_close(new2, new, rtol=0, atol=0)
+    # a non-contiguous state is never written through: a fresh tensor comes back
+    st_nc = s_before.transpose(2, 3).contiguous().transpose(2, 3)
+    new3, _ = selective_state_update(**{**t, "state": st_nc}, dt_softplus=True)
+    assert new3.data_ptr() != st_nc.data_ptr()
+    torch.testing.assert_close(new3, new, rtol=0, atol=0)
