@@ -167,13 +167,15 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
                     acc[pt] = M::mma(af, bfr, acc[pt]);
                 }
             }
+            // C @ states has x's dtype as result type in the reference
+            // (ops/ssd_naive.py:294-297): round it before the fp32 decay
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int mr = m0 + kg * 4 + i;
                 float f = expf(dAs[mr]);
                 if (a.seq_idx && seqs[mr] != seq_prev) f = 0.f;
 #pragma unroll
-                for (int pt = 0; pt < PT; ++pt) acc[pt][i] *= f;
+                for (int pt = 0; pt < PT; ++pt) acc[pt][i] = to_f32(from_f32<T>(acc[pt][i])) * f;
             }
         }
 
@@ -187,13 +189,15 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
                 const int kb = k0 + kg * KPL;
                 float cbv[KPL];
                 if (kb < Q) load_cb<KPL>(cbrow + kb, cbv);
-                typename M::frag af;
+                // the weighted operand is split into bf16 hi + lo parts (x is
+                // exact in bf16): the intra-chunk sum keeps near-fp32 accuracy
+                typename M::frag af, al;
 #pragma unroll
                 for (int j = 0; j < KPL; ++j) {
                     const int k = kb + j;
                     float v = 0.f;
                     if (k <= m && k < Q) v = cbv[j] * expf(dAm - dAs[k]) * dts[k];
-                    M::set(af, j, v);
+                    M::set_split(af, al, j, v);
                 }
 #pragma unroll
                 for (int pt = 0; pt < PT; ++pt) {
@@ -204,6 +208,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
                         M::set_raw(bfr, j, k < Q ? xs[k * SX + pt * 16 + ln] : T(0.f));
                     }
                     acc[pt] = M::mma(af, bfr, acc[pt]);
+                    if constexpr (M::kSplit) acc[pt] = M::mma(al, bfr, acc[pt]);
                 }
             }
         }
@@ -221,7 +226,8 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
                 if (a.D) v += dv * to_f32(xs[mr * SX + p]);
                 const int64_t o = ((tok0 + mr) * H + h) * (int64_t)P + p;
                 if (a.out_x) a.out_x[o] = v;
-                if (a.z) v *= silu_f(to_f32(reinterpret_cast<const T*>(a.z)[o]));
+                // silu(z) is evaluated in z's dtype by the reference (ops/ssd_naive.py:316)
+                if (a.z) v *= to_f32(from_f32<T>(silu_f(to_f32(reinterpret_cast<const T*>(a.z)[o]))));
                 a.out[o] = v;
             }
         }

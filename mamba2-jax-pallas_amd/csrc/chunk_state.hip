@@ -7,7 +7,9 @@
 // both x [.., L, H, P] and B [.., L, G, N] in HBM, so x and B rows are staged
 // through LDS with coalesced 16-byte loads and the MFMA fragments (8
 // consecutive positions per lane for bf16) are gathered from LDS; the decay
-// weight w[q] is applied to the x operand as it is gathered.  Positions are
+// weight w[q] is applied to the x operand as it is gathered, and for bf16 the
+// weighted operand is split into hi + lo bf16 parts (two MFMAs) so that the
+// states keep near-fp32 accuracy, as the reference's fp32 einsum does.  Positions are
 // processed in blocks of KB rows to bound LDS.  Wavefront w owns all P/16 row
 // tiles and N/64 column tiles: [P x N] fp32 accumulators live in VGPRs and
 // are written once.
@@ -140,7 +142,9 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
         stage_rows<T>(bs, SB, bsrc + (int64_t)kb * a.G * N, (int64_t)a.G * N, KB, valid - kb, N);
         __syncthreads();
         for (int k0 = 0; k0 < KB; k0 += M::K) {
-            typename M::frag af[PT], bfr[CTW];
+            // x[q,p] * w[q] is split into bf16 hi + lo parts (x and B are exact
+            // in their dtype, so two MFMAs give near-fp32 weighted sums)
+            typename M::frag af[PT], al[PT], bfr[CTW];
 #pragma unroll
             for (int j = 0; j < M::KPL; ++j) {
                 const int kl = k0 + kg * M::KPL + j;      // position within the block
@@ -149,7 +153,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
 #pragma unroll
                 for (int pt = 0; pt < PT; ++pt) {
                     const float xv = kok ? to_f32(xs[kl * SX + pt * 16 + ln]) : 0.f;
-                    M::set(af[pt], j, xv * wk);
+                    M::set_split(af[pt], al[pt], j, xv * wk);
                 }
 #pragma unroll
                 for (int jj = 0; jj < CTW; ++jj) {
@@ -160,7 +164,10 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
 #pragma unroll
             for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
-                for (int jj = 0; jj < CTW; ++jj) acc[pt][jj] = M::mma(af[pt], bfr[jj], acc[pt][jj]);
+                for (int jj = 0; jj < CTW; ++jj) {
+                    acc[pt][jj] = M::mma(af[pt], bfr[jj], acc[pt][jj]);
+                    if constexpr (M::kSplit) acc[pt][jj] = M::mma(al[pt], bfr[jj], acc[pt][jj]);
+                }
         }
     }
 

@@ -47,6 +47,14 @@ template <> struct MF<bf16> {
     }
     static M2_DEV void set(frag& f, int j, float v) { f[j] = (bf16)v; }
     static M2_DEV void set_raw(frag& f, int j, bf16 v) { f[j] = v; }
+    // v ~= hi + lo with both parts bf16 (relative error ~2^-17): a scaled
+    // operand keeps near-fp32 accuracy through two bf16 MFMAs.
+    static constexpr bool kSplit = true;
+    static M2_DEV void set_split(frag& hi, frag& lo, int j, float v) {
+        const bf16 h = (bf16)v;
+        hi[j] = h;
+        lo[j] = (bf16)(v - (float)h);
+    }
 };
 
 template <> struct MF<float> {
@@ -58,6 +66,8 @@ template <> struct MF<float> {
     }
     static M2_DEV void set(frag& f, int, float v) { f = v; }
     static M2_DEV void set_raw(frag& f, int, float v) { f = v; }
+    static constexpr bool kSplit = false;   // fp32 operands are exact already
+    static M2_DEV void set_split(frag& hi, frag& lo, int, float v) { hi = v; lo = 0.f; }
 };
 
 // Load KPL consecutive elements (16 B for bf16, 4 B for fp32) as a fragment.

@@ -93,7 +93,8 @@ __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
         if (threadIdx.x % TPR == 0) {
             float y = part;
             if (a.D) y += (a.D_has_hdim ? a.D[h * P + p] : a.D[h]) * xv;
-            if (a.z) y *= silu_f(ld<T>(a.z, hp));
+            // silu(z) in z's dtype, as the reference (ops/selective_state_update.py:121)
+            if (a.z) y *= to_f32(from_f32<T>(silu_f(ld<T>(a.z, hp))));
             a.out[hp] = y;
         }
     }

@@ -6,8 +6,8 @@ formulation, float32 arithmetic) for device tensors.  It is what
 a full-size float32 cross-check for the HIP path; it is never used as a
 fallback.  Like the reference it ignores seq_idx / cu_seqlens, and pads the
 raw dt before the softplus (so padded positions carry softplus(dt_bias)).
-For bf16 inputs it rounds where the reference rounds: CB, the carried states
-and the C @ states product.
+For bf16 inputs it rounds where the reference rounds: CB, the carried states,
+the C @ states product and silu(z).
 """
 
 from __future__ import annotations
@@ -114,7 +114,7 @@ def chunk_scan_naive(CB, x, dt, dA_cumsum, C, prev_states, D=None, z=None):
     out_x = None
     if z is not None:
         out_x = out
-        out = out * F.silu(z.float())
+        out = out * F.silu(z).float()          # silu in z's dtype, as jax.nn.silu
     return out, out_x
 
 

@@ -14,6 +14,7 @@ given by ``acc`` (float64 for parity checks, float32 for the CPU baseline).
 Reference precision quirks reproduced on purpose (``round_fn``):
   * CB = C @ B^T is an einsum of the input dtype, so bf16 inputs give a bf16 CB
     (ssd_naive.py:214-216);
+  * jax.nn.silu(z) keeps z's dtype (ssd_naive.py:316, selective_state_update.py:121);
   * states_passed is cast to C.dtype before the inter-chunk term
     (ssd_naive.py:296, kernels/ssd_combined.py:140);
   * the inter-chunk einsum ``C @ states`` has the input dtype as result type and
@@ -310,7 +311,8 @@ def chunk_scan(CB, x, dt, dA_cumsum, C, prev_states, D=None, z=None,
     out_x = None
     if z is not None:
         out_x = out
-        out = out * silu(np.asarray(z, dtype=acc))
+        # jax.nn.silu(z) keeps z's dtype (ssd_naive.py:316)
+        out = out * round_fn(silu(np.asarray(z, dtype=acc)))
     return out, out_x
 
 
@@ -460,8 +462,11 @@ def ssd_sequential(x, dt, A, B, C, D=None, z=None, dt_bias=None,
 # ---------------------------------------------------------------------------
 
 def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
-                           dt_softplus=False, acc=np.float64):
-    """Returns (new_state (b,H,P,N), out (b,H,P)); no dt_limit clamp."""
+                           dt_softplus=False, round_fn=identity, acc=np.float64):
+    """Returns (new_state (b,H,P,N), out (b,H,P)); no dt_limit clamp.
+
+    ``round_fn`` rounds silu(z) to z's dtype, as jax.nn.silu does (:121).
+    """
     state = np.asarray(state, dtype=acc)
     x = np.asarray(x, dtype=acc)
     dt = np.asarray(dt, dtype=acc)
@@ -490,7 +495,7 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
         D = np.asarray(D, dtype=acc)
         out = out + (D[None, :, None] if D.ndim == 1 else D[None]) * x
     if z is not None:
-        out = out * silu(np.asarray(z, dtype=acc))
+        out = out * round_fn(silu(np.asarray(z, dtype=acc)))
     return new, out
 
 

@@ -116,8 +116,18 @@ def test_c3_full_packed_equals_per_sequence():
         ys, fs = mamba_chunk_scan_combined_fwd(chunk_size=cfg.chunk_size, dt_softplus=True,
                                                return_final_states=True, **part)
         errs.append(check(y[:, sl], host(ys), TOL["bf16"], f"seq {s} out"))
-        check(vs[s], host(fs[0]), TOL["bf16"], f"seq {s} varlen state")
-    check(fin[0], host(vs[-1]), 1e-6, "final == last varlen state")
+        # The packed varlen state adds exp(dA) * (state entering its last chunk)
+        # taken from the bf16 states_passed, as the reference does
+        # (kernels/ssd_combined.py:176-183): one bf16 rounding of that term.
+        _within_bf16_ulp(vs[s], fs[0], f"seq {s} varlen state")
+    _within_bf16_ulp(fin[0], vs[-1], "final == last varlen state")
+
+
+def _within_bf16_ulp(got, want, what):
+    g, w = host(got), host(want)
+    e = float(np.max(np.abs(g - w)) / np.max(np.abs(w)))
+    print(f"  {what}: max|err|/max|ref| = {e:.3e} (tol 2^-8)", flush=True)
+    assert e <= 2.0 ** -8, f"{what}: {e:.3e}"
 
 
 def test_chunk_size_invariance():

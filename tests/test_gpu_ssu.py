@@ -58,7 +58,7 @@ def test_single_step(b, H, G, P, N, kw, softplus):
         d["dt_bias"] = None
     t = _dev(d)
     new, y = selective_state_update(**t, dt_softplus=softplus)
-    ws, wy = O.selective_state_update(**d, dt_softplus=softplus)
+    ws, wy = O.selective_state_update(**d, dt_softplus=softplus, round_fn=O.round_fn_for("bf16"))
     check(new, ws, 1e-5, "state")
     check(y, wy, 1e-4, "out")
 
@@ -84,7 +84,8 @@ def test_256_steps_trajectory_and_prefill():
         ys.append(y)
         ref, wy = O.selective_state_update(ref, d["x"][t], d["dt"][t], d["A"], d["B"][t],
                                            d["C"][t], D=d["D"], z=d["z"][t],
-                                           dt_bias=d["dt_bias"], dt_softplus=True)
+                                           dt_bias=d["dt_bias"], dt_softplus=True,
+                                           round_fn=O.round_fn_for("bf16"))
         wys.append(wy)
     Y = torch.stack(ys, dim=1)                                 # (b, T, H, P)
     check(state, ref, 1e-4, "state after 256 steps")

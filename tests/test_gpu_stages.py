@@ -183,7 +183,10 @@ def test_bmm_chunk_bf16_output():
     got = bmm_chunk_fwd(dev(a, torch.bfloat16), dev(a, torch.bfloat16), 128,
                         output_dtype=torch.bfloat16)
     assert got.dtype == torch.bfloat16
-    check(got, O.bmm_chunk(a, a, 128), 4e-3, "CB bf16")
+    # fp32 accumulation then one round-to-nearest-even: within half a bf16 ulp
+    want = O.bmm_chunk(a, a, 128)
+    err = np.abs(host(got) - want)
+    assert np.all(err <= np.abs(want) * 2.0 ** -8 + 1e-6), float(err.max())
 
 
 # ---------------------------------------------------------------------------
@@ -252,7 +255,7 @@ def test_chunk_scan_large_decay_is_stable():
     overflows there; the kernel evaluates exp(dA_m - dA_k) directly."""
     b, L, H, P, N, G, Q = 1, 256, 4, 64, 64, 1, 256
     d = _inputs(b, L, H, G, P, N, Q, "f32", seed=9)
-    dt = np.full((b, L, H), 2.0, np.float32)                 # softplus(2 + bias) ~ 1-2
+    dt = np.full((b, L, H), 8.0, np.float32)                 # dt' = softplus(8 + bias) ~ 2-6
     A = np.full(H, -16.0, np.float32)
     wA, wdt = O.chunk_cumsum(dt, A, Q, d["dt_bias"], True)
     assert wA.min() < -2000
