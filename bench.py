@@ -51,7 +51,20 @@ def stage_work(cfg, with_init=False, with_z=False):
     w["chunk_scan"] = (s * b * nc * G * Q * Q + b * L * H * P * s + 8 * cq + b * L * G * N * s
                        + s * S + 4 * H + (b * L * H * P * s if with_z else 0) + 4 * b * L * H * P,
                        b * nc * H * P * Q * (Q + 1) + 2 * b * L * H * N * P)
+    if scan_is_fused(cfg):
+        # bmm_chunk runs inside the scan kernel: B is read instead of a CB buffer
+        sb, sf = w.pop("bmm_chunk")
+        cb_bytes = s * b * nc * G * Q * Q
+        by, fl = w.pop("chunk_scan")
+        w["bmm_chunk+chunk_scan"] = (by - cb_bytes + b * L * G * N * s, fl + sf)
     return w
+
+
+def scan_is_fused(cfg):
+    """The combined path fuses bmm_chunk into chunk_scan for bf16, headdim 64,
+    dstate 64/128/256 and chunk_size 64/128 (m2::scan_fused_supported)."""
+    return (cfg.dtype == "bf16" and cfg.headdim == 64 and cfg.dstate in (64, 128, 256)
+            and cfg.chunk_size in (64, 128))
 
 
 def cpu_baseline(cfg, heads, min_seconds=10.0, max_reps=20):
@@ -130,6 +143,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=32)
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="run one device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -155,6 +170,14 @@ def main(argv=None):
               chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
               return_varlen_states=d["cu_seqlens"] is not None)
 
+    if args.copy_mb:
+        # a plain copy of known size: reads and writes copy_mb MiB once each
+        src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         mamba_chunk_scan_combined_fwd(**kw)
     K = args.steps
@@ -172,19 +195,24 @@ def main(argv=None):
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms = g0.elapsed_time(g1) / K
-    stage_ms = {s: float(np.mean([evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(K)]))
-                for j, s in enumerate(STAGES)}
-
+    slot_ms = [float(np.mean([evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(K)]))
+               for j in range(5)]
     work = stage_work(cfg, with_init=d["initial_states"] is not None)
+    if scan_is_fused(cfg):
+        # event slots: cumsum, chunk_state, state_passing, (empty), fused scan
+        names = ["chunk_cumsum", "chunk_state", "state_passing", "bmm_chunk+chunk_scan"]
+        stage_ms = dict(zip(names, slot_ms[:3] + [slot_ms[3] + slot_ms[4]]))
+    else:
+        stage_ms = dict(zip(STAGES, slot_ms))
     peak_mfma = PEAK_MFMA_TFLOPS[cfg.dtype]
     stages = {}
-    for s in STAGES:
+    for s in stage_ms:
         by, fl = work[s]
         sec = stage_ms[s] * 1e-3
         stages[s] = {"ms": stage_ms[s], "bytes": by, "gflop": fl / 1e9,
                      "hbm_gbs": by / sec / 1e9, "hbm_frac": by / sec / 1e9 / PEAK_HBM_GBS,
                      "mfma_tflops": fl / sec / 1e12, "mfma_frac": fl / sec / 1e12 / peak_mfma}
-    dom = max(STAGES, key=lambda s: stage_ms[s])
+    dom = max(stage_ms, key=lambda s: stage_ms[s])
     by, fl = work[dom]
     ridge = peak_mfma * 1e12 / (PEAK_HBM_GBS * 1e9)
     bound = "mfma" if fl / by > ridge else "hbm"

@@ -28,6 +28,8 @@ ARCH = "gfx950"
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # private arrays (prefetch registers) stay in VGPRs instead of taking LDS
+    "-mllvm", "-disable-promote-alloca-to-lds",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
     "-I", INCLUDE, "-I", CSRC,
 ]

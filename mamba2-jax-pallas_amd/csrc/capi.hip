@@ -134,6 +134,12 @@ extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
     if ((rc = m2::launch_state_passing(c3, s))) return rc;
     if ((rc = record(a.stage_events, 3, s))) return rc;
 
+    if (a.dtype == M2_BF16 && m2::scan_fused_supported(a.headdim, a.dstate, a.chunk_size)) {
+        // CB is built inside the scan kernel: the bmm interval stays empty
+        if ((rc = record(a.stage_events, 4, s))) return rc;
+        if ((rc = m2::launch_scan_fused(a, dA, dto, passed, s))) return rc;
+        if ((rc = record(a.stage_events, 5, s))) return rc;
+    } else {
     m2_bmm_chunk_args c4{};
     c4.a = a.C; c4.b = a.B; c4.seq_idx = a.seq_idx; c4.out = cb;
     c4.batch = a.batch; c4.seqlen = a.seqlen; c4.ngroups = a.ngroups; c4.k = a.dstate;
@@ -149,6 +155,7 @@ extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
     c5.dtype = a.dtype; c5.cb_dtype = a.dtype; c5.states_dtype = a.dtype; c5.D_has_hdim = a.D_has_hdim;
     if ((rc = m2::launch_chunk_scan(c5, s))) return rc;
     if ((rc = record(a.stage_events, 5, s))) return rc;
+    }
 
     if (a.varlen_states) {
         m2_chunk_state_varlen_args c6{};

@@ -76,6 +76,12 @@ M2_DEV float load_frag(const float* p) { return *p; }
 
 M2_DEV f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() is a
+// workgroup release/acquire fence and waits for every outstanding global load
+// and store (vmcnt(0)); barriers that only hand LDS tiles between wavefronts
+// use this one so that prefetches and output stores stay in flight.
+M2_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---------------------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2).  Remap the hardware block id so that each XCD receives a contiguous

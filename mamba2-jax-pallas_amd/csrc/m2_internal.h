@@ -13,4 +13,9 @@ int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t stream);
 int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t stream);
 int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t stream);
 int launch_ssu(const m2_ssu_args& a, hipStream_t stream);
+
+// fused bmm_chunk + chunk_scan of the combined forward (bf16 inputs)
+bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size);
+int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const float* dt_out,
+                      const void* states_passed, hipStream_t stream);
 }  // namespace m2
