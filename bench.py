@@ -200,8 +200,9 @@ def main(argv=None):
     work = stage_work(cfg, with_init=d["initial_states"] is not None)
     if scan_is_fused(cfg):
         # event slots: cumsum, chunk_state, state_passing, (empty), fused scan
+        # (slot 3 holds only the back-to-back event records of the empty bmm slot)
         names = ["chunk_cumsum", "chunk_state", "state_passing", "bmm_chunk+chunk_scan"]
-        stage_ms = dict(zip(names, slot_ms[:3] + [slot_ms[3] + slot_ms[4]]))
+        stage_ms = dict(zip(names, slot_ms[:3] + [slot_ms[4]]))
     else:
         stage_ms = dict(zip(STAGES, slot_ms))
     peak_mfma = PEAK_MFMA_TFLOPS[cfg.dtype]
