@@ -57,7 +57,29 @@ def stage_work(cfg, with_init=False, with_z=False):
         cb_bytes = s * b * nc * G * Q * Q
         by, fl = w.pop("chunk_scan")
         w["bmm_chunk+chunk_scan"] = (by - cb_bytes + b * L * G * N * s, fl + sf)
+    if states_is_fused(cfg):
+        # chunk_cumsum also writes the chunk-state weights and the chunk decay;
+        # one chunk-sequential kernel then reads x, B and the weights and writes
+        # the states entering each chunk and the final states (no fp32 chunk states)
+        cb_, cf_ = w.pop("chunk_cumsum")
+        w.pop("chunk_state"), w.pop("state_passing")
+        w["chunk_cumsum"] = (cb_ + 4 * cq + 4 * b * H * nc, cf_ + 3 * cq)
+        w[FUSED_STATES] = (b * L * H * P * s + b * L * G * N * s + 4 * cq + 4 * b * H * nc
+                           + s * S + 4 * b * H * P * N + (4 * b * H * P * N if with_init else 0),
+                           2 * b * L * H * P * N + 2 * S)
     return w
+
+
+FUSED_STATES = "chunk_state+state_passing"
+
+
+def states_is_fused(cfg):
+    """The combined path runs chunk_state and state_passing as one kernel for
+    bf16, headdim 64, dstate a multiple of 64 and chunk_size a multiple of 64 up
+    to 256 (m2::states_fused_supported)."""
+    return (cfg.dtype == "bf16" and cfg.headdim == 64 and cfg.dstate % 64 == 0
+            and cfg.chunk_size % 64 == 0 and cfg.chunk_size <= 256
+            and cfg.nheads % cfg.ngroups == 0)
 
 
 def scan_is_fused(cfg):
@@ -198,13 +220,20 @@ def main(argv=None):
     slot_ms = [float(np.mean([evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(K)]))
                for j in range(5)]
     work = stage_work(cfg, with_init=d["initial_states"] is not None)
-    if scan_is_fused(cfg):
-        # event slots: cumsum, chunk_state, state_passing, (empty), fused scan
-        # (slot 3 holds only the back-to-back event records of the empty bmm slot)
-        names = ["chunk_cumsum", "chunk_state", "state_passing", "bmm_chunk+chunk_scan"]
-        stage_ms = dict(zip(names, slot_ms[:3] + [slot_ms[4]]))
+    # event slots: cumsum, chunk_state, state_passing, bmm_chunk, chunk_scan; a
+    # fused kernel's time lands in the first slot of its group, the other slots of
+    # the group hold only back-to-back event records
+    slots = dict(zip(STAGES, slot_ms))
+    stage_ms = {}
+    if states_is_fused(cfg):
+        stage_ms["chunk_cumsum"] = slots["chunk_cumsum"]
+        stage_ms[FUSED_STATES] = slots["chunk_state"]
     else:
-        stage_ms = dict(zip(STAGES, slot_ms))
+        stage_ms.update({k: slots[k] for k in STAGES[:3]})
+    if scan_is_fused(cfg):
+        stage_ms["bmm_chunk+chunk_scan"] = slots["chunk_scan"]
+    else:
+        stage_ms.update({k: slots[k] for k in STAGES[3:]})
     peak_mfma = PEAK_MFMA_TFLOPS[cfg.dtype]
     stages = {}
     for s in stage_ms:

@@ -49,23 +49,32 @@ M2_ENTRY(m2_selective_state_update, m2_ssu_args, launch_ssu)
 namespace {
 
 struct Layout {
-    size_t dA, dt, states, passed, cb, total;
+    size_t dA, dt, wts, scl, states, passed, cb, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 Layout layout_of(const m2_ssd_combined_args& a) {
+    // slots the fused kernels make unnecessary are left empty: the fp32 chunk
+    // states (chunk_state + state_passing fused, which need the weights and
+    // decay instead) and CB (bmm_chunk fused)
     Layout l{};
     const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
     const size_t es = m2_dtype_size(a.dtype);
     const size_t bhcq = (size_t)a.batch * a.nheads * nc * a.chunk_size;
     const size_t S = (size_t)a.batch * nc * a.nheads * a.headdim * a.dstate;
+    const bool states_fused = m2::states_fused_supported(a);
+    const bool scan_fused = a.dtype == M2_BF16 &&
+                            m2::scan_fused_supported(a.headdim, a.dstate, a.chunk_size);
     size_t off = 0;
     l.dA = off;     off += align256(bhcq * 4);
     l.dt = off;     off += align256(bhcq * 4);
-    l.states = off; off += align256(S * 4);
+    l.wts = off;    off += states_fused ? align256(bhcq * 4) : 0;
+    l.scl = off;    off += states_fused ? align256((size_t)a.batch * a.nheads * nc * 4) : 0;
+    l.states = off; off += states_fused ? 0 : align256(S * 4);
     l.passed = off; off += align256(S * es);
-    l.cb = off;     off += align256((size_t)a.batch * nc * a.ngroups * a.chunk_size * a.chunk_size * es);
+    l.cb = off;
+    off += scan_fused ? 0 : align256((size_t)a.batch * nc * a.ngroups * a.chunk_size * a.chunk_size * es);
     l.total = off;
     return l;
 }
@@ -109,30 +118,47 @@ extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
     int rc;
     if ((rc = record(a.stage_events, 0, s))) return rc;
 
-    m2_chunk_cumsum_args c1{};
-    c1.dt = a.dt; c1.A = a.A; c1.dt_bias = a.dt_bias; c1.dA_cumsum = dA; c1.dt_out = dto;
-    c1.batch = a.batch; c1.seqlen = a.seqlen; c1.nheads = a.nheads; c1.chunk_size = a.chunk_size;
-    c1.dt_dtype = a.dt_dtype; c1.dt_softplus = a.dt_softplus; c1.dt_min = a.dt_min; c1.dt_max = a.dt_max;
-    if ((rc = m2::launch_chunk_cumsum(c1, s))) return rc;
-    if ((rc = record(a.stage_events, 1, s))) return rc;
+    if (m2::states_fused_supported(a)) {
+        // cumsum (+ weights and decay), then chunk states and state passing in
+        // one kernel: its time lands in the second event interval, the third is
+        // empty
+        m2_chunk_cumsum_args c1{};
+        c1.dt = a.dt; c1.A = a.A; c1.dt_bias = a.dt_bias; c1.dA_cumsum = dA; c1.dt_out = dto;
+        c1.batch = a.batch; c1.seqlen = a.seqlen; c1.nheads = a.nheads; c1.chunk_size = a.chunk_size;
+        c1.dt_dtype = a.dt_dtype; c1.dt_softplus = a.dt_softplus; c1.dt_min = a.dt_min; c1.dt_max = a.dt_max;
+        float* wts = (float*)(ws + l.wts);
+        float* scl = (float*)(ws + l.scl);
+        if ((rc = m2::launch_chunk_cumsum_ex(c1, a.seq_idx, wts, scl, s))) return rc;
+        if ((rc = record(a.stage_events, 1, s))) return rc;
+        if ((rc = m2::launch_states_fused(a, wts, scl, passed, s))) return rc;
+        if ((rc = record(a.stage_events, 2, s))) return rc;
+        if ((rc = record(a.stage_events, 3, s))) return rc;
+    } else {
+        m2_chunk_cumsum_args c1{};
+        c1.dt = a.dt; c1.A = a.A; c1.dt_bias = a.dt_bias; c1.dA_cumsum = dA; c1.dt_out = dto;
+        c1.batch = a.batch; c1.seqlen = a.seqlen; c1.nheads = a.nheads; c1.chunk_size = a.chunk_size;
+        c1.dt_dtype = a.dt_dtype; c1.dt_softplus = a.dt_softplus; c1.dt_min = a.dt_min; c1.dt_max = a.dt_max;
+        if ((rc = m2::launch_chunk_cumsum(c1, s))) return rc;
+        if ((rc = record(a.stage_events, 1, s))) return rc;
 
-    m2_chunk_state_args c2{};
-    c2.x = a.x; c2.B = a.B; c2.dt = dto; c2.dA_cumsum = dA; c2.seq_idx = a.seq_idx; c2.states = states;
-    c2.batch = a.batch; c2.seqlen = a.seqlen; c2.nheads = a.nheads; c2.headdim = a.headdim;
-    c2.ngroups = a.ngroups; c2.dstate = a.dstate; c2.chunk_size = a.chunk_size; c2.dtype = a.dtype;
-    if ((rc = m2::launch_chunk_state(c2, s))) return rc;
-    if ((rc = record(a.stage_events, 2, s))) return rc;
+        m2_chunk_state_args c2{};
+        c2.x = a.x; c2.B = a.B; c2.dt = dto; c2.dA_cumsum = dA; c2.seq_idx = a.seq_idx; c2.states = states;
+        c2.batch = a.batch; c2.seqlen = a.seqlen; c2.nheads = a.nheads; c2.headdim = a.headdim;
+        c2.ngroups = a.ngroups; c2.dstate = a.dstate; c2.chunk_size = a.chunk_size; c2.dtype = a.dtype;
+        if ((rc = m2::launch_chunk_state(c2, s))) return rc;
+        if ((rc = record(a.stage_events, 2, s))) return rc;
 
-    m2_state_passing_args c3{};
-    c3.states = states; c3.dA_chunk_cumsum = dA + (a.chunk_size - 1);
-    c3.dA_stride_batch = a.nheads * nc * a.chunk_size; c3.dA_stride_head = nc * a.chunk_size;
-    c3.dA_stride_chunk = a.chunk_size;
-    c3.initial_states = a.initial_states; c3.seq_idx = a.seq_idx; c3.out = passed;
-    c3.final_states = a.final_states;
-    c3.batch = a.batch; c3.nchunks = nc; c3.nheads = a.nheads; c3.dim = a.headdim * a.dstate;
-    c3.seqlen = a.seqlen; c3.chunk_size = a.chunk_size; c3.out_dtype = a.dtype;
-    if ((rc = m2::launch_state_passing(c3, s))) return rc;
-    if ((rc = record(a.stage_events, 3, s))) return rc;
+        m2_state_passing_args c3{};
+        c3.states = states; c3.dA_chunk_cumsum = dA + (a.chunk_size - 1);
+        c3.dA_stride_batch = a.nheads * nc * a.chunk_size; c3.dA_stride_head = nc * a.chunk_size;
+        c3.dA_stride_chunk = a.chunk_size;
+        c3.initial_states = a.initial_states; c3.seq_idx = a.seq_idx; c3.out = passed;
+        c3.final_states = a.final_states;
+        c3.batch = a.batch; c3.nchunks = nc; c3.nheads = a.nheads; c3.dim = a.headdim * a.dstate;
+        c3.seqlen = a.seqlen; c3.chunk_size = a.chunk_size; c3.out_dtype = a.dtype;
+        if ((rc = m2::launch_state_passing(c3, s))) return rc;
+        if ((rc = record(a.stage_events, 3, s))) return rc;
+    }
 
     if (a.dtype == M2_BF16 && m2::scan_fused_supported(a.headdim, a.dstate, a.chunk_size)) {
         // CB is built inside the scan kernel: the bmm interval stays empty
@@ -140,21 +166,21 @@ extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
         if ((rc = m2::launch_scan_fused(a, dA, dto, passed, s))) return rc;
         if ((rc = record(a.stage_events, 5, s))) return rc;
     } else {
-    m2_bmm_chunk_args c4{};
-    c4.a = a.C; c4.b = a.B; c4.seq_idx = a.seq_idx; c4.out = cb;
-    c4.batch = a.batch; c4.seqlen = a.seqlen; c4.ngroups = a.ngroups; c4.k = a.dstate;
-    c4.chunk_size = a.chunk_size; c4.dtype = a.dtype; c4.out_dtype = a.dtype; c4.causal = 0;
-    if ((rc = m2::launch_bmm_chunk(c4, s))) return rc;
-    if ((rc = record(a.stage_events, 4, s))) return rc;
+        m2_bmm_chunk_args c4{};
+        c4.a = a.C; c4.b = a.B; c4.seq_idx = a.seq_idx; c4.out = cb;
+        c4.batch = a.batch; c4.seqlen = a.seqlen; c4.ngroups = a.ngroups; c4.k = a.dstate;
+        c4.chunk_size = a.chunk_size; c4.dtype = a.dtype; c4.out_dtype = a.dtype; c4.causal = 0;
+        if ((rc = m2::launch_bmm_chunk(c4, s))) return rc;
+        if ((rc = record(a.stage_events, 4, s))) return rc;
 
-    m2_chunk_scan_args c5{};
-    c5.cb = cb; c5.x = a.x; c5.dt = dto; c5.dA_cumsum = dA; c5.C = a.C; c5.states = passed;
-    c5.D = a.D; c5.z = a.z; c5.seq_idx = a.seq_idx; c5.out = a.out; c5.out_x = nullptr;
-    c5.batch = a.batch; c5.seqlen = a.seqlen; c5.nheads = a.nheads; c5.headdim = a.headdim;
-    c5.ngroups = a.ngroups; c5.dstate = a.dstate; c5.chunk_size = a.chunk_size;
-    c5.dtype = a.dtype; c5.cb_dtype = a.dtype; c5.states_dtype = a.dtype; c5.D_has_hdim = a.D_has_hdim;
-    if ((rc = m2::launch_chunk_scan(c5, s))) return rc;
-    if ((rc = record(a.stage_events, 5, s))) return rc;
+        m2_chunk_scan_args c5{};
+        c5.cb = cb; c5.x = a.x; c5.dt = dto; c5.dA_cumsum = dA; c5.C = a.C; c5.states = passed;
+        c5.D = a.D; c5.z = a.z; c5.seq_idx = a.seq_idx; c5.out = a.out; c5.out_x = nullptr;
+        c5.batch = a.batch; c5.seqlen = a.seqlen; c5.nheads = a.nheads; c5.headdim = a.headdim;
+        c5.ngroups = a.ngroups; c5.dstate = a.dstate; c5.chunk_size = a.chunk_size;
+        c5.dtype = a.dtype; c5.cb_dtype = a.dtype; c5.states_dtype = a.dtype; c5.D_has_hdim = a.D_has_hdim;
+        if ((rc = m2::launch_chunk_scan(c5, s))) return rc;
+        if ((rc = record(a.stage_events, 5, s))) return rc;
     }
 
     if (a.varlen_states) {

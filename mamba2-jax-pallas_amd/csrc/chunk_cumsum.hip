@@ -1,63 +1,133 @@
-// chunk_cumsum: dt processing + per-chunk inclusive cumsum of dt' * A.
+// chunk_cumsum: dt processing + per-chunk inclusive cumsum of dt' * A, and
+// (for the fused state pass of the combined forward) the chunk-state weights
+//   w[q]  = exp(min(dA[last] - dA[q], 0)) dt'[q]    (0 where seq_idx differs
+//           from the chunk's last position, or that id is negative)
+//   scl   = exp(dA[Q-1]), 0 where the chunk-end seq_idx differs from the
+//           previous chunk's (the previous id of chunk 0 is 0)
+// which are the chunk_state scale and the state_passing decay.
 //
-// One workgroup per (batch, chunk, block of 32 heads).  The [Q x 32] dt tile
-// is read row by row (coalesced along heads), processed (bias, softplus,
-// clamp; 0 past the end of the sequence) into LDS, then each wavefront scans
-// whole heads: 64 lanes take 64 consecutive positions, a 6-step shuffle scan
-// per 64-position segment plus a carried running sum.  Stores of dA_cumsum and
-// dt_out are contiguous along positions.
+// One workgroup per (batch, chunk, block of 32 heads), 256 threads: lane
+// h = thread & 31 is a head, thread >> 5 one of 8 position segments of the
+// chunk.  Each thread loads its segment's dt (coalesced across the 32 heads),
+// processes it and sums it sequentially in registers; segment totals meet in
+// LDS and each thread adds the totals of the segments before it.  Outputs are
+// transposed through LDS so that each row [b, h, c, :] is written by
+// consecutive lanes.
 //
 // Follows reference kernels/chunk_cumsum_fwd.py:213-235 (bias -> softplus ->
-// clip -> zero pad) and ops/ssd_naive.py:67-68 (dA = dt' * A, then cumsum).
+// clip -> zero pad) and ops/ssd_naive.py:67-68 (dA = dt' * A, then cumsum);
+// the weights and decay follow kernels/chunk_state_fwd.py:239-269 and
+// kernels/state_passing_fwd.py:108-151, :208-225.
 #include "m2_internal.h"
 
 namespace {
 
-constexpr int HB = 32;        // heads per workgroup
-constexpr int THREADS = 256;
+constexpr int HB = 32;                 // heads per workgroup
+constexpr int NSEG = 8;                // position segments per chunk
+constexpr int THREADS = HB * NSEG;
+constexpr int QMAX = 256;
 
-template <typename TD>
-__global__ void __launch_bounds__(THREADS)
-k_chunk_cumsum(const TD* __restrict__ dt, const float* __restrict__ A,
-               const float* __restrict__ bias, float* __restrict__ dA_cs,
-               float* __restrict__ dt_out, int L, int H, int Q, int nc,
-               int softplus, float lo, float hi) {
-    extern __shared__ float tile[];  // [Q][HB + 1]
-    const int hb = blockIdx.x * HB, c = blockIdx.y, bi = blockIdx.z;
-    const int nh = min(HB, H - hb);
-    for (int idx = threadIdx.x; idx < Q * HB; idx += THREADS) {
-        const int q = idx / HB, hh = idx % HB;
-        const int t = c * Q + q;
-        float v = 0.f;
-        if (hh < nh && t < L) {
-            v = to_f32(dt[((size_t)bi * L + t) * H + hb + hh]);
-            if (bias) v += bias[hb + hh];
-            if (softplus) v = softplus_f(v);
-            v = fminf(fmaxf(v, lo), hi);
-        }
-        tile[q * (HB + 1) + hh] = v;
-    }
-    __syncthreads();
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    for (int hh = w; hh < nh; hh += THREADS / 64) {
-        const float a = A[hb + hh];
-        const size_t base = (((size_t)bi * H + hb + hh) * nc + c) * Q;
-        float carry = 0.f;
-        for (int q0 = 0; q0 < Q; q0 += 64) {
-            const int q = q0 + lane;
-            const float v = q < Q ? tile[q * (HB + 1) + hh] : 0.f;
-            float incl = v * a;
+struct CumsumArgs {
+    const void* dt;
+    const float* A;
+    const float* bias;
+    const int32_t* seq;       // [b, L] or NULL (weights / decay only)
+    float* dA;
+    float* dto;
+    float* wts;               // [b, H, nc, Q] or NULL
+    float* scl;               // [b, H, nc] or NULL
+    int L, H, Q, nc, softplus;
+    float lo, hi;
+};
+
+// QS: positions per segment rounded up to a power of two (>= ceil(Q / 8)).
+// Every load is issued unconditionally (addresses clamped into the chunk's
+// valid range, results selected afterwards): loads under per-position
+// branches would each be waited for on their own.
+template <typename TD, int QS>
+__global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
+    __shared__ float tot[NSEG][HB];
+    __shared__ float tile[HB][QMAX + 1];
+    const int hh = threadIdx.x % HB, seg = threadIdx.x / HB;
+    const int h = blockIdx.x * HB + hh, c = blockIdx.y, bi = blockIdx.z;
+    const bool hok = h < a.H;
+    const int Q = a.Q, L = a.L;
+    const int qs = (Q + NSEG - 1) / NSEG;
+    const int q0 = seg * qs;
+    const int qe = min(q0 + qs, Q);                 // this segment: [q0, qe)
+    const int qhi = min(Q, L - c * Q);              // valid positions of the chunk
+    const int qv = min(qe, qhi);                    // valid positions of the segment: [q0, qv)
+    const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
+    const TD* dtp = reinterpret_cast<const TD*>(a.dt) + tok0 * a.H + min(h, a.H - 1);
+
+    TD raw[QS];
+    int sq[QS];
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float o = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += o;
+    for (int j = 0; j < QS; ++j) raw[j] = dtp[(int64_t)min(q0 + j, qhi - 1) * a.H];
+    int se = 0, sprev = 0;
+    if (a.seq) {
+#pragma unroll
+        for (int j = 0; j < QS; ++j) sq[j] = a.seq[tok0 + min(q0 + j, qhi - 1)];
+        se = a.seq[tok0 + qhi - 1];
+        if (c > 0) sprev = a.seq[tok0 - 1];
+    }
+    const float Ah = a.A[min(h, a.H - 1)];
+    const float bias = a.bias ? a.bias[min(h, a.H - 1)] : 0.f;
+
+    float v[QS], dA[QS];
+    float run = 0.f;
+#pragma unroll
+    for (int j = 0; j < QS; ++j) {
+        float d = to_f32(raw[j]);
+        if (a.bias) d += bias;
+        if (a.softplus) d = softplus_f(d);
+        d = fminf(fmaxf(d, a.lo), a.hi);
+        v[j] = (hok && q0 + j < qv) ? d : 0.f;
+        run += v[j] * Ah;
+        dA[j] = run;
+    }
+    tot[seg][hh] = run;
+    __syncthreads();
+    // totals summed in segment order: off + (last segment's total) is the
+    // same sum as `total`, so dA[Q - 1] == total exactly
+    float off = 0.f, total = 0.f;
+#pragma unroll
+    for (int k = 0; k < NSEG; ++k) {
+        const float t = tot[k][hh];
+        if (k < seg) off += t;
+        total += t;
+    }
+    // outputs go through LDS [head][position] so that the rows [b, h, c, :]
+    // are written by consecutive lanes
+    float* outs[3] = {a.dA, a.dto, a.wts};
+    const int nh = min(HB, a.H - (int)blockIdx.x * HB);
+    const int64_t row0 = (((int64_t)bi * a.H + blockIdx.x * HB) * a.nc + c) * Q;
+    const int64_t hstride = (int64_t)a.nc * Q;       // between heads' rows
+#pragma unroll
+    for (int o = 0; o < 3; ++o) {
+        if (o == 2 && !a.wts) break;
+#pragma unroll
+        for (int j = 0; j < QS; ++j) {
+            const int q = q0 + j;
+            const float d = off + dA[j];
+            float val = d;
+            if (o == 1) val = v[j];
+            if (o == 2) {
+                val = expf(fminf(total - d, 0.f)) * v[j];
+                if (a.seq && (q >= qhi || se < 0 || sq[j] != se)) val = 0.f;
             }
-            if (q < Q) {
-                dA_cs[base + q] = carry + incl;
-                dt_out[base + q] = v;
-            }
-            carry += __shfl(incl, 63, 64);
+            if (j < qs && q < qe) tile[hh][q] = val;
         }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < nh * Q; idx += THREADS) {
+            const int r = idx / Q, q = idx - r * Q;
+            outs[o][row0 + r * hstride + q] = tile[r][q];
+        }
+        __syncthreads();
+    }
+    if (a.scl && seg == 0 && hok) {
+        const bool keep = !a.seq || se == sprev;
+        a.scl[((int64_t)bi * a.H + h) * a.nc + c] = keep ? expf(total) : 0.f;
     }
 }
 
@@ -65,29 +135,38 @@ k_chunk_cumsum(const TD* __restrict__ dt, const float* __restrict__ A,
 
 namespace m2 {
 
-int launch_chunk_cumsum(const m2_chunk_cumsum_args& a, hipStream_t s) {
+int launch_chunk_cumsum_ex(const m2_chunk_cumsum_args& a, const int32_t* seq_idx, float* wts,
+                           float* scl, hipStream_t s) {
     M2_REQUIRE(a.dt && a.A && a.dA_cumsum && a.dt_out, M2_ERR_INVALID,
                "chunk_cumsum: dt, A, dA_cumsum and dt_out are required");
     M2_REQUIRE(a.batch > 0 && a.seqlen > 0 && a.nheads > 0 && a.chunk_size > 0, M2_ERR_INVALID,
                "chunk_cumsum: sizes must be positive");
-    M2_REQUIRE(a.chunk_size <= 256, M2_ERR_UNSUPPORTED, "chunk_cumsum: chunk_size %lld > 256",
-               (long long)a.chunk_size);
-    const int Q = (int)a.chunk_size;
-    const int nc = (int)((a.seqlen + Q - 1) / Q);
-    dim3 grid((unsigned)((a.nheads + HB - 1) / HB), (unsigned)nc, (unsigned)a.batch);
-    const size_t shm = (size_t)Q * (HB + 1) * sizeof(float);
-    if (a.dt_dtype == M2_F32) {
-        k_chunk_cumsum<float><<<grid, THREADS, shm, s>>>(
-            (const float*)a.dt, a.A, a.dt_bias, a.dA_cumsum, a.dt_out, (int)a.seqlen,
-            (int)a.nheads, Q, nc, a.dt_softplus, a.dt_min, a.dt_max);
-    } else if (a.dt_dtype == M2_BF16) {
-        k_chunk_cumsum<bf16><<<grid, THREADS, shm, s>>>(
-            (const bf16*)a.dt, a.A, a.dt_bias, a.dA_cumsum, a.dt_out, (int)a.seqlen,
-            (int)a.nheads, Q, nc, a.dt_softplus, a.dt_min, a.dt_max);
-    } else {
+    M2_REQUIRE(a.chunk_size <= QMAX, M2_ERR_UNSUPPORTED, "chunk_cumsum: chunk_size %lld > %d",
+               (long long)a.chunk_size, QMAX);
+    CumsumArgs k{};
+    k.dt = a.dt; k.A = a.A; k.bias = a.dt_bias; k.seq = seq_idx;
+    k.dA = a.dA_cumsum; k.dto = a.dt_out; k.wts = wts; k.scl = scl;
+    k.L = (int)a.seqlen; k.H = (int)a.nheads; k.Q = (int)a.chunk_size;
+    k.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
+    k.softplus = a.dt_softplus; k.lo = a.dt_min; k.hi = a.dt_max;
+    dim3 grid((unsigned)((a.nheads + HB - 1) / HB), (unsigned)k.nc, (unsigned)a.batch);
+    if (a.dt_dtype != M2_F32 && a.dt_dtype != M2_BF16)
         return set_error(M2_ERR_UNSUPPORTED, "chunk_cumsum: dt dtype %d", a.dt_dtype);
-    }
+    const int qs = (k.Q + NSEG - 1) / NSEG;
+    const bool f32 = a.dt_dtype == M2_F32;
+#define M2_CUMSUM_LAUNCH(QS)                                                  \
+    if (f32) k_chunk_cumsum<float, QS><<<grid, THREADS, 0, s>>>(k);           \
+    else k_chunk_cumsum<bf16, QS><<<grid, THREADS, 0, s>>>(k);
+    if (qs <= 4) { M2_CUMSUM_LAUNCH(4) }
+    else if (qs <= 8) { M2_CUMSUM_LAUNCH(8) }
+    else if (qs <= 16) { M2_CUMSUM_LAUNCH(16) }
+    else { M2_CUMSUM_LAUNCH(32) }
+#undef M2_CUMSUM_LAUNCH
     return check_launch("chunk_cumsum");
+}
+
+int launch_chunk_cumsum(const m2_chunk_cumsum_args& a, hipStream_t s) {
+    return launch_chunk_cumsum_ex(a, nullptr, nullptr, nullptr, s);
 }
 
 }  // namespace m2

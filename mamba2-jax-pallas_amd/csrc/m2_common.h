@@ -82,6 +82,20 @@ M2_DEV f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 // use this one so that prefetches and output stores stay in flight.
 M2_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Vector global stores the compiler does not track.  On gfx9-family targets
+// stores and loads share the vmcnt counter, and once both are pending the
+// compiler's wait insertion falls back to vmcnt(0) before the next use of any
+// load: a store inside a prefetch loop would drain every load in flight.
+// Loads still complete in issue order, so waits the compiler computes from
+// its own loads stay correct (they can only wait longer) with these stores
+// pending.
+M2_DEV void store_untracked(float* p, float v) {
+    asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+M2_DEV void store_untracked(void* p, uint64_t v) {
+    asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
+}
+
 // ---------------------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2).  Remap the hardware block id so that each XCD receives a contiguous

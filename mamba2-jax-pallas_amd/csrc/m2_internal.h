@@ -7,6 +7,10 @@
 
 namespace m2 {
 int launch_chunk_cumsum(const m2_chunk_cumsum_args& a, hipStream_t stream);
+// chunk_cumsum that also writes the chunk-state weights wts [b, H, nc, Q] and
+// the carried-state decay scl [b, H, nc] (seq_idx rules applied) when non-NULL
+int launch_chunk_cumsum_ex(const m2_chunk_cumsum_args& a, const int32_t* seq_idx, float* wts,
+                           float* scl, hipStream_t stream);
 int launch_chunk_state(const m2_chunk_state_args& a, hipStream_t stream);
 int launch_state_passing(const m2_state_passing_args& a, hipStream_t stream);
 int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t stream);
@@ -18,4 +22,11 @@ int launch_ssu(const m2_ssu_args& a, hipStream_t stream);
 bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size);
 int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const float* dt_out,
                       const void* states_passed, hipStream_t stream);
+
+// chunk_state + state_passing of the combined forward in one chunk-sequential
+// pass (bf16 inputs), from the weights / decay of launch_chunk_cumsum_ex;
+// writes the states entering each chunk (bf16) and the final states
+bool states_fused_supported(const m2_ssd_combined_args& a);
+int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const float* scl,
+                        void* states_passed, hipStream_t stream);
 }  // namespace m2

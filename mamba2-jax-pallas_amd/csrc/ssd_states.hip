@@ -1,0 +1,282 @@
+// ssd_states: chunk_state + state_passing of the combined forward in one pass.
+//
+//   S_c = sum_q w[q] x[q, :]^T B[q, :]                              (chunk_state)
+//   h_0 = initial state (or 0),  passed[c] = h_c,
+//   h_{c+1} = scl[c] h_c + S_c                                     (state_passing)
+//
+// with the weights w[q] = exp(min(dA[last] - dA[q], 0)) dt'[q] and the decay
+// scl[c] = exp(dA[Q-1]) (seq_idx rules applied) precomputed by chunk_cumsum.
+// The unfused stages write the fp32 chunk states S_c to HBM and read them
+// back; here the running state h stays in the MFMA accumulators of one
+// workgroup that walks the chunks of a (batch, head, 64-column dstate block) in
+// order, so HBM sees only x, B, w, the bf16 states entering each chunk and the
+// final states.
+//
+// Workgroup = 8 wavefronts (two per SIMD, so that one hides the other's LDS
+// and MFMA latency).  Positions stream through a ring of DEPTH LDS slots in
+// stages of KB = 64: each slot holds the x rows [64 x 64], the B rows
+// [64 x 64] and the stage's weights (+ the chunk's decay).  Wavefront w owns
+// head-dim rows 16 (w & 3) .. +15, all 64 dstate columns of the block (four
+// 16 x 16 tiles) and the positions 32 (w >> 2) .. +31 of every stage: the two
+// halves accumulate separate partial states (the recurrence is linear), which
+// are summed through LDS only where the state is written (chunk starts and
+// the end).  Slots are filled by direct global -> LDS loads
+// (global_load_lds_dwordx4), DEPTH - 1 stages ahead of use, with explicit
+// vmcnt waits: no load result passes through VGPRs, so nothing forces the
+// compiler to drain the loads in flight.  Tiles are dense in LDS with the
+// 16-byte chunks of each row XOR-swizzled so that the transposed reads below
+// hit 64 distinct banks per 32 lanes.
+//
+// MFMA operands need 8 consecutive positions per lane for a fixed row / column:
+// they come straight from the row-major tiles through the gfx950 LDS transpose
+// read (ds_read_b64_tr_b16: lane i of a 16-lane group receives column i of the
+// 4 x 16 block the group addresses).  The product is computed transposed,
+// h^T[n, p] += B^T[n, q] (w x)[q, p], so that each lane holds 4 consecutive
+// dstate columns of one head-dim row (8-byte bf16 and 16-byte fp32 stores).
+// w x is split into hi + lo bf16 parts (two MFMAs): the weighted operand keeps
+// near-fp32 accuracy as in the fp32 einsum of the reference.
+//
+// Follows reference kernels/chunk_state_fwd.py:104-187 (product),
+// kernels/state_passing_fwd.py:108-151 (recurrence) and ops/ssd_naive.py:77-182.
+#include "m2_internal.h"
+
+namespace {
+
+constexpr int THREADS = 512;
+constexpr int KB = 64;       // positions per stage (two MFMA K steps, one per half)
+constexpr int DEPTH = 6;     // LDS stage slots: DEPTH - 1 stages of loads in flight
+constexpr int P = 64;        // head dim
+constexpr int NB = 64;       // dstate columns per workgroup
+constexpr int CPR = 8;       // 16-byte chunks per 128-byte tile row
+constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
+constexpr int SLOT = XB + BB + 512;                // + 64 weights, 64 copies of the decay
+static_assert(KB * CPR == THREADS, "one x and one B chunk per thread and stage");
+
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// LDS transpose read: 4 consecutive rows of one column per lane (see above).
+M2_DEV bf16x4 ds_read_tr(const char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(const_cast<char*>(p)));
+}
+
+// Direct global -> LDS loads: lane l's 16 (4) bytes land at LDS byte address
+// M0 + 16 l (4 l); `lds` must be the same in every lane of the wavefront.
+// They are counted by vmcnt like any vector load; the kernel waits for them
+// explicitly (wait_vmem) before the barrier that hands a slot to the other
+// wavefronts.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+M2_DEV void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
+}
+M2_DEV void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+                 ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N> M2_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+// Lane J of each 16-lane row, broadcast to the row (DPP row_newbcast).
+template <int J> M2_DEV float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xf, 0xf, false));
+}
+
+// 16-byte chunk swizzle of tile row R (128-byte rows): 8 consecutive rows read
+// at one chunk pair land on disjoint banks.
+M2_DEV int swz(int R) { return ((R >> 1) & 3) << 1; }
+
+struct StatesArgs {
+    const bf16* x;
+    const bf16* B;
+    const float* wts;      // [b, H, nc, Q]
+    const float* scl;      // [b, H, nc]
+    const float* init;
+    bf16* passed;
+    float* fin;
+    int L, H, G, N, Q, nc, nblk, nwork;
+};
+
+__global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
+    __shared__ __align__(16) char ring[DEPTH * SLOT];
+    __shared__ __align__(16) f32x4 xchg[4][4][64];   // partial states of the second half
+
+    const int work = xcd_remap(blockIdx.x, a.nwork);
+    const int nb = work % a.nblk;
+    const int bh = work / a.nblk;
+    const int h = bh % a.H, bi = bh / a.H;
+    const int g = h / (a.H / a.G);
+    const int L = a.L, Q = a.Q, nc = a.nc, N = a.N, H = a.H;
+    const int SPC = Q / KB, S = nc * SPC;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int ln = lane & 15, kg = lane >> 4;
+    const int pw = w & 3, kh = w >> 2;          // row tile, position half
+
+    // ---- running (partial) state h^T tiles: acc[j][i] = h[p][n],
+    // p = 16 pw + ln, n = NB nb + 16 j + 4 kg + i.  The initial state goes to
+    // the first half.  Loaded (and consumed) before any direct load is issued,
+    // so the compiler's own waits never cover those.
+    f32x4 acc[4];
+    const int64_t hoff = ((int64_t)bi * H + h) * P * N;
+    const int prow = 16 * pw + ln;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = NB * nb + 16 * j + 4 * kg;
+        if (a.init && kh == 0) {
+            const float4 v = *reinterpret_cast<const float4*>(a.init + hoff + (int64_t)prow * N + n);
+            acc[j][0] = v.x; acc[j][1] = v.y; acc[j][2] = v.z; acc[j][3] = v.w;
+        } else {
+            acc[j] = zero4();
+        }
+        asm volatile("" ::"v"(acc[j]));
+    }
+
+    // ---- direct-load sources: one x and one B chunk of each stage per thread
+    // (row, swizzled column); wavefront 0 also the weights, wavefront 1 the
+    // chunk's decay.
+    const int lr = threadIdx.x / CPR;
+    const int lc = ((threadIdx.x % CPR) ^ swz(lr)) * 8;
+    const bf16* xsrc = a.x + ((int64_t)bi * L * H + h) * P + lc;
+    const int64_t xstr = (int64_t)H * P;
+    const bf16* bsrc = a.B + ((int64_t)bi * L * a.G + g) * N + nb * NB + lc;
+    const int64_t bstr = (int64_t)a.G * N;
+    const int64_t bhc = ((int64_t)bi * H + h) * nc;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
+    const uint32_t tile_off = 64 * w * 16;
+
+    auto issue = [&](int st, int k) {
+        const uint32_t sb = ring_lds + k * SLOT;
+        const int64_t t = min(st * KB + lr, L - 1);      // past the end: weight 0
+        dma16(xsrc + t * xstr, sb + tile_off);
+        dma16(bsrc + t * bstr, sb + XB + tile_off);
+        if (w < 2) {
+            const int c = st / SPC;
+            const float* p = w == 0 ? a.wts + (bhc + c) * Q + (st - c * SPC) * KB + lane
+                                    : a.scl + bhc + c;
+            dma4(p, sb + XB + BB + 256 * w);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i) issue(min(i, S - 1), i);
+
+    const int rA = 32 * kh + 4 * kg + (ln >> 2);   // tile rows of MFMA k = 0..3 (+16: 4..7)
+    const int c1 = ln & 3;                         // 8-byte column group of the read
+    const int cb = 8 * (c1 & 1);
+    const int wpos = 32 * kh + (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // k index ln & 7
+    const int xo0 = rA * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
+    const int xo1 = (rA + 16) * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
+    int bo0[4], bo1[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
+        bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
+    }
+    for (int s = 0; s < S; ++s) {
+        const int k = s % DEPTH;
+        const int c = s / SPC, kb = s - c * SPC;
+        // own loads of stage s done (DEPTH - 2 later stages may still be in flight)
+        if (w < 2) wait_vmem<(DEPTH - 2) * 3>();
+        else wait_vmem<(DEPTH - 2) * 2>();
+        lds_barrier();                               // slot k complete, slot k-1 free
+        issue(min(s + DEPTH - 1, S - 1), (s + DEPTH - 1) % DEPTH);
+        const char* slot = ring + k * SLOT;
+        const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
+        if (kb == 0) {
+            // h_c (sum of the halves) is the state entering chunk c; then both
+            // halves h <- scl[c] h
+            if (kh == 1) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) xchg[pw][j][lane] = acc[j];
+            }
+            lds_barrier();
+            if (kh == 0) {
+                bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + prow) * N + NB * nb + 4 * kg;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 o2 = xchg[pw][j][lane];
+                    const bf16x4 o = {(bf16)(acc[j][0] + o2[0]), (bf16)(acc[j][1] + o2[1]),
+                                      (bf16)(acc[j][2] + o2[2]), (bf16)(acc[j][3] + o2[3])};
+                    store_untracked(pp + 16 * j, __builtin_bit_cast(uint64_t, o));
+                }
+            }
+            const float sc = aux[64];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[j][r] *= sc;
+        }
+        // acc += B^T (w x) over this half's 32 positions.  MFMA k index j < 4 is
+        // position 32 kh + 4 kg + j, j >= 4 is 32 kh + 16 + 4 kg + j - 4.
+        // Lane j < 8 of each row reads the weight of k index j; the row shares them.
+        const float wl = aux[wpos];
+        const float wv[8] = {row_bcast<0>(wl), row_bcast<1>(wl), row_bcast<2>(wl), row_bcast<3>(wl),
+                             row_bcast<4>(wl), row_bcast<5>(wl), row_bcast<6>(wl), row_bcast<7>(wl)};
+        bf16x8 xh, xl;
+        {
+            const bf16x4 x0 = ds_read_tr(slot + xo0);
+            const bf16x4 x1 = ds_read_tr(slot + xo1);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = (float)(j < 4 ? x0[j] : x1[j - 4]) * wv[j];
+                const bf16 hi = (bf16)v;
+                xh[j] = hi;
+                xl[j] = (bf16)(v - (float)hi);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bf16x4 b0 = ds_read_tr(slot + bo0[j]);
+            const bf16x4 b1 = ds_read_tr(slot + bo1[j]);
+            const bf16x8 bf = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
+        }
+    }
+    wait_vmem<0>();     // the tail stages re-loaded into unused slots
+
+    if (kh == 1) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xchg[pw][j][lane] = acc[j];
+    }
+    __syncthreads();
+    if (a.fin && kh == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = NB * nb + 16 * j + 4 * kg;
+            const f32x4 o2 = xchg[pw][j][lane];
+            *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n) =
+                make_float4(acc[j][0] + o2[0], acc[j][1] + o2[1], acc[j][2] + o2[2], acc[j][3] + o2[3]);
+        }
+    }
+}
+
+}  // namespace
+
+namespace m2 {
+
+bool states_fused_supported(const m2_ssd_combined_args& a) {
+    return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
+           a.chunk_size % KB == 0 && a.chunk_size <= 256 && a.ngroups > 0 &&
+           a.nheads % a.ngroups == 0;
+}
+
+int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const float* scl,
+                        void* passed, hipStream_t s) {
+    M2_REQUIRE(states_fused_supported(a), M2_ERR_UNSUPPORTED,
+               "ssd_states: unsupported shape / dtype");
+    StatesArgs sa{};
+    sa.x = (const bf16*)a.x; sa.B = (const bf16*)a.B; sa.wts = wts; sa.scl = scl;
+    sa.init = a.initial_states; sa.passed = (bf16*)passed; sa.fin = a.final_states;
+    sa.L = (int)a.seqlen; sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.N = (int)a.dstate;
+    sa.Q = (int)a.chunk_size; sa.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
+    sa.nblk = (int)(a.dstate / NB);
+    const int64_t nwork = a.batch * a.nheads * sa.nblk;
+    M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "ssd_states: too many workgroups");
+    sa.nwork = (int)nwork;
+    k_ssd_states<<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    return check_launch("ssd_states");
+}
+
+}  // namespace m2
