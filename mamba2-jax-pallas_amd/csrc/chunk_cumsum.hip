@@ -6,8 +6,8 @@
 //           previous chunk's (the previous id of chunk 0 is 0)
 // which are the chunk_state scale and the state_passing decay.
 //
-// One workgroup per (batch, chunk, block of 32 heads), 256 threads: lane
-// h = thread & 31 is a head, thread >> 5 one of 8 position segments of the
+// One workgroup per (batch, chunk, block of 32 heads), 512 threads: lane
+// h = thread & 31 is a head, thread >> 5 one of 16 position segments of the
 // chunk.  Each thread loads its segment's dt (coalesced across the 32 heads),
 // processes it and sums it sequentially in registers; segment totals meet in
 // LDS and each thread adds the totals of the segments before it.  Outputs are
@@ -23,9 +23,10 @@
 namespace {
 
 constexpr int HB = 32;                 // heads per workgroup
-constexpr int NSEG = 8;                // position segments per chunk
+constexpr int NSEG = 16;               // position segments per chunk
 constexpr int THREADS = HB * NSEG;
 constexpr int QMAX = 256;
+constexpr int TS = QMAX + 4;          // LDS tile row stride (16-byte rows)
 
 struct CumsumArgs {
     const void* dt;
@@ -40,14 +41,14 @@ struct CumsumArgs {
     float lo, hi;
 };
 
-// QS: positions per segment rounded up to a power of two (>= ceil(Q / 8)).
+// QS: positions per segment rounded up to a power of two (>= ceil(Q / 16)).
 // Every load is issued unconditionally (addresses clamped into the chunk's
 // valid range, results selected afterwards): loads under per-position
 // branches would each be waited for on their own.
-template <typename TD, int QS>
+template <typename TD, int QS, bool VEC>
 __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
     __shared__ float tot[NSEG][HB];
-    __shared__ float tile[HB][QMAX + 1];
+    __shared__ __align__(16) float tile[3][HB][TS];
     const int hh = threadIdx.x % HB, seg = threadIdx.x / HB;
     const int h = blockIdx.x * HB + hh, c = blockIdx.y, bi = blockIdx.z;
     const bool hok = h < a.H;
@@ -98,32 +99,41 @@ __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
         total += t;
     }
     // outputs go through LDS [head][position] so that the rows [b, h, c, :]
-    // are written by consecutive lanes
+    // are written by consecutive lanes (16 bytes per lane when VEC)
+    const int nout = a.wts ? 3 : 2;
+#pragma unroll
+    for (int j = 0; j < QS; ++j) {
+        const int q = q0 + j;
+        if (j < qs && q < qe) {
+            const float d = off + dA[j];
+            tile[0][hh][q] = d;
+            tile[1][hh][q] = v[j];
+            if (a.wts) {
+                float wv = expf(fminf(total - d, 0.f)) * v[j];
+                if (a.seq && (q >= qhi || se < 0 || sq[j] != se)) wv = 0.f;
+                tile[2][hh][q] = wv;
+            }
+        }
+    }
+    __syncthreads();
     float* outs[3] = {a.dA, a.dto, a.wts};
     const int nh = min(HB, a.H - (int)blockIdx.x * HB);
     const int64_t row0 = (((int64_t)bi * a.H + blockIdx.x * HB) * a.nc + c) * Q;
     const int64_t hstride = (int64_t)a.nc * Q;       // between heads' rows
-#pragma unroll
-    for (int o = 0; o < 3; ++o) {
-        if (o == 2 && !a.wts) break;
-#pragma unroll
-        for (int j = 0; j < QS; ++j) {
-            const int q = q0 + j;
-            const float d = off + dA[j];
-            float val = d;
-            if (o == 1) val = v[j];
-            if (o == 2) {
-                val = expf(fminf(total - d, 0.f)) * v[j];
-                if (a.seq && (q >= qhi || se < 0 || sq[j] != se)) val = 0.f;
-            }
-            if (j < qs && q < qe) tile[hh][q] = val;
+    if (VEC) {
+        const int q4n = Q / 4;
+        for (int idx = threadIdx.x; idx < nout * nh * q4n; idx += THREADS) {
+            const int o = idx / (nh * q4n), rem = idx - o * (nh * q4n);
+            const int r = rem / q4n, q = 4 * (rem - r * q4n);
+            *reinterpret_cast<float4*>(outs[o] + row0 + r * hstride + q) =
+                *reinterpret_cast<const float4*>(&tile[o][r][q]);
         }
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < nh * Q; idx += THREADS) {
-            const int r = idx / Q, q = idx - r * Q;
-            outs[o][row0 + r * hstride + q] = tile[r][q];
+    } else {
+        for (int idx = threadIdx.x; idx < nout * nh * Q; idx += THREADS) {
+            const int o = idx / (nh * Q), rem = idx - o * (nh * Q);
+            const int r = rem / Q, q = rem - r * Q;
+            outs[o][row0 + r * hstride + q] = tile[o][r][q];
         }
-        __syncthreads();
     }
     if (a.scl && seg == 0 && hok) {
         const bool keep = !a.seq || se == sprev;
@@ -154,13 +164,21 @@ int launch_chunk_cumsum_ex(const m2_chunk_cumsum_args& a, const int32_t* seq_idx
         return set_error(M2_ERR_UNSUPPORTED, "chunk_cumsum: dt dtype %d", a.dt_dtype);
     const int qs = (k.Q + NSEG - 1) / NSEG;
     const bool f32 = a.dt_dtype == M2_F32;
-#define M2_CUMSUM_LAUNCH(QS)                                                  \
-    if (f32) k_chunk_cumsum<float, QS><<<grid, THREADS, 0, s>>>(k);           \
-    else k_chunk_cumsum<bf16, QS><<<grid, THREADS, 0, s>>>(k);
-    if (qs <= 4) { M2_CUMSUM_LAUNCH(4) }
+    // 16-byte row stores need 16-byte aligned outputs and chunk_size % 4 == 0
+    const bool vec = k.Q % 4 == 0 && ((uintptr_t)k.dA % 16 == 0) && ((uintptr_t)k.dto % 16 == 0) &&
+                     ((uintptr_t)k.wts % 16 == 0);
+#define M2_CUMSUM_LAUNCH(QS)                                                          \
+    if (vec) {                                                                        \
+        if (f32) k_chunk_cumsum<float, QS, true><<<grid, THREADS, 0, s>>>(k);         \
+        else k_chunk_cumsum<bf16, QS, true><<<grid, THREADS, 0, s>>>(k);              \
+    } else {                                                                          \
+        if (f32) k_chunk_cumsum<float, QS, false><<<grid, THREADS, 0, s>>>(k);        \
+        else k_chunk_cumsum<bf16, QS, false><<<grid, THREADS, 0, s>>>(k);             \
+    }
+    if (qs <= 2) { M2_CUMSUM_LAUNCH(2) }
+    else if (qs <= 4) { M2_CUMSUM_LAUNCH(4) }
     else if (qs <= 8) { M2_CUMSUM_LAUNCH(8) }
-    else if (qs <= 16) { M2_CUMSUM_LAUNCH(16) }
-    else { M2_CUMSUM_LAUNCH(32) }
+    else { M2_CUMSUM_LAUNCH(16) }
 #undef M2_CUMSUM_LAUNCH
     return check_launch("chunk_cumsum");
 }

@@ -24,8 +24,18 @@ template <typename T> M2_DEV T from_f32(float v);
 template <> M2_DEV float from_f32<float>(float v) { return v; }
 template <> M2_DEV bf16 from_f32<bf16>(float v) { return (bf16)v; }  // RNE
 
-// softplus(v) = log(1 + exp(v)), stable for all v
-M2_DEV float softplus_f(float v) { return fmaxf(v, 0.f) + log1pf(expf(-fabsf(v))); }
+// softplus(v) = log(1 + exp(v)) = max(v, 0) + log1p(exp(-|v|)), stable for
+// all v.  log1p(e) for e in (0, 1] is evaluated with Goldberg's compensated
+// formula log(u) * e / (u - 1), u = 1 + e (D. Goldberg, "What every computer
+// scientist should know about floating-point arithmetic", 1991, Thm. 4): the
+// hardware exp / log are accurate to a few ulp and the rounding of 1 + e is
+// cancelled exactly.
+M2_DEV float softplus_f(float v) {
+    const float e = __expf(-fabsf(v));
+    const float u = 1.f + e;
+    const float l = u == 1.f ? e : __logf(u) * __fdividef(e, u - 1.f);
+    return fmaxf(v, 0.f) + l;
+}
 M2_DEV float silu_f(float v) { return v / (1.f + expf(-v)); }
 
 // ---------------------------------------------------------------------------
