@@ -106,6 +106,43 @@ M2_DEV void store_untracked(void* p, uint64_t v) {
     asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
 }
 
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// LDS transpose read (gfx950 ds_read_b64_tr_b16): lane i of each 16-lane group
+// receives column i of the 4 x 16 block of 16-bit elements whose rows the
+// group's lanes address (lane 4 r + c supplies row r, columns 4 c .. 4 c + 3).
+M2_DEV bf16x4 ds_read_tr(const void* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(const_cast<void*>(p)));
+}
+
+// Direct global -> LDS loads: lane l's 16 (4) bytes land at LDS byte address
+// M0 + 16 l (4 l); `lds` (an LDS byte address) must be the same in every lane
+// of the wavefront.  They are counted by vmcnt like any vector load but are
+// invisible to the compiler's wait insertion: kernels wait for them
+// explicitly (wait_vmem) before the barrier that hands the data to other
+// wavefronts, and keep their own vector loads out of loops that have these in
+// flight (the compiler would wait for those with too small a count).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+M2_DEV void dma16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
+}
+M2_DEV void dma4(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+                 ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+template <int N> M2_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+// LDS byte address of a __shared__ object
+M2_DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
+
+// Lane J of each 16-lane row, broadcast to the row (DPP row_newbcast).
+template <int J> M2_DEV float row_bcast(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xf, 0xf, false));
+}
+
 // ---------------------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
 // L2).  Remap the hardware block id so that each XCD receives a contiguous

@@ -52,37 +52,6 @@ constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
 constexpr int SLOT = XB + BB + 512;                // + 64 weights, 64 copies of the decay
 static_assert(KB * CPR == THREADS, "one x and one B chunk per thread and stage");
 
-typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-
-// LDS transpose read: 4 consecutive rows of one column per lane (see above).
-M2_DEV bf16x4 ds_read_tr(const char* p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(const_cast<char*>(p)));
-}
-
-// Direct global -> LDS loads: lane l's 16 (4) bytes land at LDS byte address
-// M0 + 16 l (4 l); `lds` must be the same in every lane of the wavefront.
-// They are counted by vmcnt like any vector load; the kernel waits for them
-// explicitly (wait_vmem) before the barrier that hands a slot to the other
-// wavefronts.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-M2_DEV void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                 ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
-}
-M2_DEV void dma4(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
-                 ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
-}
-#pragma clang diagnostic pop
-template <int N> M2_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
-
-// Lane J of each 16-lane row, broadcast to the row (DPP row_newbcast).
-template <int J> M2_DEV float row_bcast(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xf, 0xf, false));
-}
-
 // 16-byte chunk swizzle of tile row R (128-byte rows): 8 consecutive rows read
 // at one chunk pair land on disjoint banks.
 M2_DEV int swz(int R) { return ((R >> 1) & 3) << 1; }
@@ -142,7 +111,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
     const bf16* bsrc = a.B + ((int64_t)bi * L * a.G + g) * N + nb * NB + lc;
     const int64_t bstr = (int64_t)a.G * N;
     const int64_t bhc = ((int64_t)bi * H + h) * nc;
-    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
+    const uint32_t ring_lds = lds_addr(ring);
     const uint32_t tile_off = 64 * w * 16;
 
     auto issue = [&](int st, int k) {
