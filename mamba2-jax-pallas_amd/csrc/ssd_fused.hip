@@ -6,22 +6,28 @@
 // with CB = bf16(C B^T) (seq_idx-masked), h_c the bf16 state entering chunk c.
 //
 // One workgroup per (batch, chunk, group) covers every head of the group, so
-// CB is built once and used by all of them.  8 wavefronts; the chunk's 16-row
+// CB is built once and used by all of them.  8 compute wavefronts (+ one that
+// only loads, below); the chunk's 16-row
 // output tiles are paired (t, Q/16-1-t) so that every pair carries the same
-// causal (triangular) work, and the head dim is split among the wavefronts of
-// a pair: wavefront w owns pair w % NPAIRS and PTW 16-column head-dim tiles.
+// causal (triangular) work; the wavefronts of a pair split that work in two
+// halves of (row tile, k-tile) units, the first accumulating the long tile's
+// first KA k-tiles, the second the rest of it (a partial, summed through LDS)
+// and the short tile, and (for Q = 64) the head dim in PPARTS parts.
 //
 // Per head, the x rows [Q x 64], the carried state [64 x N], dA / dt of the
-// chunk, D (and the z rows) are brought into a ring of R LDS slots by direct
-// global -> LDS loads (global_load_lds_dwordx4), R - 1 heads ahead of use,
-// with explicit vmcnt waits; the group's B rows use the same path once, for
-// the CB build.  Rows are dense in LDS with their 16-byte chunks
-// XOR-swizzled so that the reads below hit distinct banks.
+// chunk and D are brought into a ring of R LDS slots by direct
+// global -> LDS loads (global_load_lds_dwordx4), R - 1 heads ahead of use;
+// the group's B rows use the same path once, for the CB build.  A ninth
+// wavefront issues all of these loads and waits for them (vmcnt) before the
+// barrier that hands a slot over: vmcnt is one in-order counter per
+// wavefront for loads and stores alike, so a wavefront that also stored the
+// outputs would wait for its stores as well.  Rows are dense in LDS with their
+// 16-byte chunks XOR-swizzled so that the reads below hit distinct banks.
 //
 // The products are computed transposed, y^T = h_c C^T + x^T W^T with
 // W[m, k] = CB[m, k] exp(dA[m] - dA[k]) dt[k], so that each lane ends with 4
 // consecutive head-dim values of one output row (16-byte stores, 8-byte D / z
-// reads):
+// reads; the z rows come straight from HBM, issued before the compute):
 //   * carried state: A = state rows (16-byte reads), B = C rows (registers),
 //     16x16x32 MFMAs; the product is rounded to bf16 and scaled by exp(dA[m])
 //     as in the reference (ops/ssd_naive.py:294-297);
@@ -37,8 +43,8 @@
 
 namespace {
 
-constexpr int THREADS = 512;
-constexpr int NWAVES = THREADS / 64;
+constexpr int NWAVES = 8;                 // compute wavefronts
+constexpr int THREADS = (NWAVES + 1) * 64; // + the load wavefront
 constexpr int P = 64;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int LDS_BYTES = 160 * 1024;
@@ -76,22 +82,28 @@ struct ScanFusedArgs {
 template <int NS, int QT, bool HASZ>
 struct Shape {
     static constexpr int N = 32 * NS, Q = 16 * QT;
-    static constexpr int NPAIRS = QT / 2, PSPLIT = NWAVES / NPAIRS, PTW = 4 / PSPLIT;
+    // wavefronts per row-tile pair: two halves of the pair's causal work (the
+    // k-tiles of the long row tile up to KA, and the rest) times PPARTS parts
+    // of the head dim with PTW 16-column tiles each
+    static constexpr int NPAIRS = QT / 2, WPP = NWAVES / NPAIRS, PPARTS = WPP / 2, PTW = 4 / PPARTS;
+    static constexpr int KA = QT / 2 + 1;
     static constexpr int SCPR = N / 8;                      // 16-byte chunks per state row
-    static constexpr int XB = Q * P * 2, SB = P * N * 2, ZB = HASZ ? Q * P * 2 : 0;
+    static constexpr int XB = Q * P * 2, SB = P * N * 2, ZB = 0;
     static constexpr int AUXB = 2 * Q * 4 + 64 * 4;         // dA, dt, D
     static constexpr int SLOT = XB + SB + ZB + AUXB;
     static constexpr int BT = Q * N * 2;                    // the group's B rows
     static constexpr int CBL = NPAIRS * (QT + 1) * 64 * 8;  // CB^T tiles
-    static constexpr int FIXED = CBL + Q * 4 + 256;
+    static constexpr int XCHG = NPAIRS * 4 * 64 * 16;       // second-half partials
+    static constexpr int FIXED = CBL + XCHG + Q * 4 + 256;
     static constexpr int ring_bytes(int r) { return r * SLOT > SLOT + BT ? r * SLOT : SLOT + BT; }
     static constexpr int R = ring_bytes(3) + FIXED <= LDS_BYTES ? 3 : 2;
     static constexpr int RING = ring_bytes(R);
-    static constexpr int XV = XB / 16 / THREADS, SV = SB / 16 / THREADS;
-    static constexpr int ZV = ZB / 16 / THREADS, BV = BT / 16 / THREADS;
-    static_assert(NPAIRS * PSPLIT == NWAVES && PTW * PSPLIT == 4, "wavefront split");
-    static_assert(XV >= 1 && SV >= 1 && BV >= 1, "tiles too small for the workgroup");
+    // 1 KB direct loads of the load wavefront per head / for the B rows
+    static constexpr int XI = XB / 1024, SI = SB / 1024, ZI = ZB / 1024, BI = BT / 1024;
+    static constexpr int CNT = XI + SI + ZI + 2;             // + dA / dt, D
+    static_assert(NPAIRS * WPP == NWAVES && PPARTS * PTW == 4 && PPARTS >= 1, "wavefront split");
     static_assert(ring_bytes(R) + FIXED <= LDS_BYTES, "LDS budget");
+    static_assert((R - 2) * CNT <= 63, "vmcnt range");
 };
 
 template <int NS, int QT, bool HASZ>
@@ -101,6 +113,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     constexpr int XB = S::XB, SB = S::SB, ZB = S::ZB, SLOT = S::SLOT, SCPR = S::SCPR;
     __shared__ __align__(16) char ring[S::RING];
     __shared__ __align__(16) bf16x4 cbl[NPAIRS][QT + 1][64];
+    __shared__ __align__(16) f32x4 xchg[NPAIRS][4][64];
     __shared__ int seqs[Q];
 
     const int L = a.L, H = a.H, G = a.G, nc = a.nc, hpg = a.hpg;
@@ -111,6 +124,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int ln = lane & 15, kg = lane >> 4;
     const int pi = w % NPAIRS, ph = w / NPAIRS;
+    const int kh = ph & 1, pp = ph >> 1;                  // work half, head-dim part
     const int t1 = pi, t2 = QT - 1 - pi;
     const int64_t tok0 = (int64_t)bi * L + (int64_t)ci * Q;
     const int valid = min(Q, L - ci * Q);
@@ -118,82 +132,69 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     const int seq_prev = (a.seq_idx && ci > 0) ? a.seq_idx[tok0 - 1] : 0;
     const uint32_t ring_lds = lds_addr(ring);
 
+    const bool loader = w == NWAVES;
+
     // ---- plain loads: C fragments of the pair's two row tiles, seq ids -----
     bf16x8 cfr[2][NS];
+    if (!loader) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int row = min(16 * (tt ? t2 : t1) + ln, valid - 1);   // clamped; masked below
-        const bf16* cp = a.C + ((tok0 + row) * G + g) * N + kg * 8;
+        for (int tt = 0; tt < 2; ++tt) {
+            const int row = min(16 * (tt ? t2 : t1) + ln, valid - 1);   // clamped; masked below
+            const bf16* cp = a.C + ((tok0 + row) * G + g) * N + kg * 8;
 #pragma unroll
-        for (int ns = 0; ns < NS; ++ns) cfr[tt][ns] = *reinterpret_cast<const bf16x8*>(cp + ns * 32);
+            for (int ns = 0; ns < NS; ++ns) cfr[tt][ns] = *reinterpret_cast<const bf16x8*>(cp + ns * 32);
+        }
     }
     for (int q = threadIdx.x; q < Q; q += THREADS)
         seqs[q] = (a.seq_idx && q < valid) ? a.seq_idx[tok0 + q] : -1;
 
-    // ---- per-thread direct-load sources (row, swizzled column) -------------
-    int64_t xo[S::XV];
-#pragma unroll
-    for (int u = 0; u < S::XV; ++u) {
-        const int gi = u * THREADS + threadIdx.x, r = gi / 8;
-        xo[u] = (tok0 + min(r, valid - 1)) * H * P + 8 * ((gi % 8) ^ xswz(r));
-    }
-    int so[S::SV];
-#pragma unroll
-    for (int u = 0; u < S::SV; ++u) {
-        const int gi = u * THREADS + threadIdx.x, p = gi / SCPR;
-        so[u] = p * N + 8 * ((gi % SCPR) ^ sswz<SCPR>(p));
-    }
+    // ---- the load wavefront: head j -> slot k.  Lane l of load u brings
+    // 16-byte chunk 64 u + l of a tile (row, swizzled column).
     const int64_t cq0 = ((int64_t)bi * H * nc + ci) * Q;  // dA / dt row of head 0 (+ h nc Q)
     const int64_t st0 = ((int64_t)bi * nc + ci) * H * P * N;
-    // head j -> slot k: XV + SV (+ ZV) loads per thread; wavefront 0 adds dA / dt
-    // (lanes < Q/2, 16 bytes each), wavefront 1 adds D (64 words)
     auto issue = [&](int j, int k) {
         const int h = g * hpg + j;
         const uint32_t sb = ring_lds + k * SLOT;
 #pragma unroll
-        for (int u = 0; u < S::XV; ++u)
-            dma16(a.x + xo[u] + h * P, sb + (u * THREADS + 64 * w) * 16);
+        for (int u = 0; u < S::XI; ++u) {
+            const int gi = 64 * u + lane, r = gi / 8;
+            const int64_t off = (tok0 + min(r, valid - 1)) * H * P + h * P + 8 * ((gi % 8) ^ xswz(r));
+            dma16(a.x + off, sb + 1024 * u);
+        }
         const bf16* sp = a.states + st0 + (int64_t)h * P * N;
 #pragma unroll
-        for (int u = 0; u < S::SV; ++u)
-            dma16(sp + so[u], sb + XB + (u * THREADS + 64 * w) * 16);
-        if (HASZ) {
-#pragma unroll
-            for (int u = 0; u < S::ZV; ++u)
-                dma16(a.z + xo[u] + h * P, sb + XB + SB + (u * THREADS + 64 * w) * 16);
+        for (int u = 0; u < S::SI; ++u) {
+            const int gi = 64 * u + lane, p = gi / SCPR;
+            dma16(sp + p * N + 8 * ((gi % SCPR) ^ sswz<SCPR>(p)), sb + XB + 1024 * u);
         }
-        if (w == 0) {
-            const int64_t row = cq0 + (int64_t)h * nc * Q;
-            if (lane < Q / 2) {
-                const float* src = lane < Q / 4 ? a.dA + row + 4 * lane : a.dt + row + 4 * (lane - Q / 4);
-                dma16(src, sb + XB + SB + ZB);
-            }
-        } else if (w == 1) {
-            const float* src = a.D ? (a.D_has_hdim ? a.D + h * P + lane : a.D + h) : a.dA + cq0;
-            dma4(src, sb + XB + SB + ZB + 2 * Q * 4);
+        const int64_t row = cq0 + (int64_t)h * nc * Q;
+        if (lane < Q / 2) {
+            const float* src = lane < Q / 4 ? a.dA + row + 4 * lane : a.dt + row + 4 * (lane - Q / 4);
+            dma16(src, sb + XB + SB + ZB);
         }
+        const float* dsrc = a.D ? (a.D_has_hdim ? a.D + h * P + lane : a.D + h) : a.dA + cq0;
+        dma4(dsrc, sb + XB + SB + ZB + 2 * Q * 4);
     };
-    constexpr int CNT = S::XV + S::SV + S::ZV;   // loads per head, wavefronts >= 2
 
     // ---- the group's B rows (aliasing ring slots 1..) and head 0 -----------
-    {
+    if (loader) {
         const bf16* Bg = a.B + (tok0 * G + g) * N;
 #pragma unroll
-        for (int u = 0; u < S::BV; ++u) {
-            const int gi = u * THREADS + threadIdx.x, r = gi / SCPR;
+        for (int u = 0; u < S::BI; ++u) {
+            const int gi = 64 * u + lane, r = gi / SCPR;
             dma16(Bg + min(r, valid - 1) * rs + 8 * ((gi % SCPR) ^ sswz<SCPR>(r)),
-                  ring_lds + SLOT + (u * THREADS + 64 * w) * 16);
+                  ring_lds + SLOT + 1024 * u);
         }
+        issue(0, 0);
+        wait_vmem<0>();
     }
-    issue(0, 0);
-    wait_vmem<0>();
     __syncthreads();
 
     // ---- CB^T tiles of each pair: (t1, kt <= t1) in slots 0..t1, (t2, kt <= t2)
     // in slots t1+1..; the pair's wavefronts share them out
-    {
+    if (!loader) {
         const char* bt = ring + SLOT;
-        for (int j = ph; j < QT + 1; j += NWAVES / NPAIRS) {
+        for (int j = ph; j < QT + 1; j += S::WPP) {
             const bool second = j > t1;
             const int t = second ? t2 : t1;
             const int kt = second ? j - t1 - 1 : j;
@@ -219,8 +220,6 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
         }
     }
     __syncthreads();                                        // B rows no longer read
-#pragma unroll
-    for (int i = 1; i < R; ++i) issue(min(i, hpg - 1), i);
 
     // seq masks of the carried-state term (per output row m = 16 t + ln)
     float fmask[2];
@@ -230,56 +229,87 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
         fmask[tt] = (a.seq_idx && seqs[m] != seq_prev) ? 0.f : 1.f;
     }
 
+    if (loader) {
+#pragma unroll
+        for (int i = 1; i < R - 1; ++i) issue(min(i, hpg - 1), i);
+        for (int j = 0; j < hpg; ++j) {
+            // head j's loads done (R - 2 later heads may still be in flight)
+            wait_vmem<(R - 2) * S::CNT>();
+            lds_barrier();                                  // slot j % R complete, slot (j-1) % R free
+            issue(min(j + R - 1, hpg - 1), (j + R - 1) % R);
+            lds_barrier();                                  // the compute wavefronts' exchange
+        }
+        wait_vmem<0>();     // the tail heads re-loaded into unused slots
+        return;
+    }
+    // this wavefront's row tiles: the first half (kh == 0) accumulates the
+    // long tile t2 over k-tiles [0, KA); the second half t2 over [KA, t2] (a
+    // partial, added in through LDS) and the short tile t1 over [0, t1]
+    constexpr int KA = S::KA;
+    const int tmine = kh ? t1 : t2;                    // the tile this wavefront stores
     for (int j = 0; j < hpg; ++j) {
         const int k = j % R;
-        // own loads of head j done (R - 2 later heads may still be in flight)
-        if (w == 0 || w == 1) wait_vmem<(R - 2) * (CNT + 1)>();
-        else wait_vmem<(R - 2) * CNT>();
-        lds_barrier();                                      // slot k complete, slot k-1 free
-        issue(min(j + R - 1, hpg - 1), (j + R - 1) % R);
+        lds_barrier();
         const char* slot = ring + k * SLOT;
         const float* dAs = reinterpret_cast<const float*>(slot + XB + SB + ZB);
         const float* dts = dAs + Q;
         const float* Ds = dAs + 2 * Q;
         const int h = g * hpg + j;
+        const int mrow = 16 * tmine + ln;              // output row of this lane
+        bf16x4 zr[PTW];
+        if (HASZ) {
+            // gate rows from HBM, in flight during the compute below
+            const bf16* zp = a.z + ((tok0 + min(mrow, valid - 1)) * H + h) * P;
+#pragma unroll
+            for (int pt = 0; pt < PTW; ++pt)
+                zr[pt] = *reinterpret_cast<const bf16x4*>(zp + 16 * (PTW * pp + pt) + 4 * kg);
+        }
 
-        f32x4 acc[2][PTW];
-        // 1. carried state: y^T = h_c C^T, rounded to bf16, times exp(dA[m])
+        f32x4 acc[2][PTW];                             // [0]: tile t1, [1]: tile t2
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
             for (int pt = 0; pt < PTW; ++pt) acc[tt][pt] = zero4();
+        // 1. carried state of the stored tile: y^T = h_c C^T, rounded to bf16,
+        // times exp(dA[m])
+        {
+            f32x4 ci_[PTW];
 #pragma unroll
-        for (int pt = 0; pt < PTW; ++pt) {
-            const int p = 16 * (PTW * ph + pt) + ln;
+            for (int pt = 0; pt < PTW; ++pt) ci_[pt] = zero4();
 #pragma unroll
-            for (int ns = 0; ns < NS; ++ns) {
-                const bf16x8 sfr = *reinterpret_cast<const bf16x8*>(
-                    slot + XB + p * (2 * N) + (((4 * ns + kg) ^ sswz<SCPR>(p)) * 16));
-                acc[0][pt] = mma32(sfr, cfr[0][ns], acc[0][pt]);
-                acc[1][pt] = mma32(sfr, cfr[1][ns], acc[1][pt]);
+            for (int pt = 0; pt < PTW; ++pt) {
+                const int p = 16 * (PTW * pp + pt) + ln;
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns) {
+                    const bf16x8 sfr = *reinterpret_cast<const bf16x8*>(
+                        slot + XB + p * (2 * N) + (((4 * ns + kg) ^ sswz<SCPR>(p)) * 16));
+                    ci_[pt] = mma32(sfr, kh ? cfr[0][ns] : cfr[1][ns], ci_[pt]);
+                }
             }
-        }
-        float dAm[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int m = 16 * (tt ? t2 : t1) + ln;
-            dAm[tt] = dAs[m] * LOG2E;
-            const float f = __builtin_amdgcn_exp2f(dAm[tt]) * fmask[tt];
+            const float f = __builtin_amdgcn_exp2f(dAs[mrow] * LOG2E) * (kh ? fmask[0] : fmask[1]);
 #pragma unroll
             for (int pt = 0; pt < PTW; ++pt)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[tt][pt][i] = rbf(acc[tt][pt][i]) * f;
+                for (int i = 0; i < 4; ++i) ci_[pt][i] = rbf(ci_[pt][i]) * f;
+#pragma unroll
+            for (int pt = 0; pt < PTW; ++pt) {
+                if (kh) acc[0][pt] = ci_[pt];
+                else acc[1][pt] = ci_[pt];
+            }
         }
-        // 2. intra chunk: y^T += x^T W^T over k-tiles kt <= t
+        // 2. intra chunk: y^T += x^T W^T over this wavefront's (tile, k-tile) units
+        const float dAm1 = dAs[16 * t1 + ln] * LOG2E, dAm2 = dAs[16 * t2 + ln] * LOG2E;
         for (int kt = 0; kt <= t2; ++kt) {
+            const bool do2 = kh ? kt >= KA : kt < KA;    // tile t2
+            const bool do1 = kh && kt <= t1;             // tile t1
+            if (!do1 && !do2) continue;
             const int k0 = 16 * kt + 4 * kg;
             bf16x4 xfr[PTW];
             {
-                const int r = k0 + (ln >> 2);                   // rows k0 .. k0+3 of the group
+                const int r = k0 + (ln >> 2);            // rows k0 .. k0+3 of the group
 #pragma unroll
                 for (int pt = 0; pt < PTW; ++pt) {
-                    const int ch = 2 * (PTW * ph + pt) + ((ln & 3) >> 1);
+                    const int ch = 2 * (PTW * pp + pt) + ((ln & 3) >> 1);
                     xfr[pt] = ds_read_tr(slot + r * 128 + ((ch ^ xswz(r)) * 16) + 8 * (ln & 1));
                 }
             }
@@ -289,16 +319,15 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
             const float tkv[4] = {tk.x, tk.y, tk.z, tk.w};
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                const int t = tt ? t2 : t1;
-                if (kt > t) continue;
-                const int m = 16 * t + ln;
+                if (tt ? !do2 : !do1) continue;
                 const bf16x4 cb4 = cbl[pi][tt ? t1 + 1 + kt : kt][lane];
+                const float dAm = tt ? dAm2 : dAm1;
                 bf16x4 whi, wlo;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    // decay exp(dA[m]-dA[k]) in the log2 domain; k > m is masked
-                    const float e = __builtin_amdgcn_exp2f(fminf(dAm[tt] - dkv[i], 0.f));
-                    const float v = (k0 + i <= m) ? (float)cb4[i] * e * tkv[i] : 0.f;
+                    // decay exp(dA[m]-dA[k]) in the log2 domain; CB is 0 for k > m
+                    const float e = __builtin_amdgcn_exp2f(fminf(dAm - dkv[i], 0.f));
+                    const float v = (float)cb4[i] * e * tkv[i];
                     const bf16 hv = (bf16)v;
                     whi[i] = hv;
                     wlo[i] = (bf16)(v - (float)hv);
@@ -310,18 +339,30 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                 }
             }
         }
-        // 3. epilogue: + D x, silu(z) gate in z's dtype, 16-byte fp32 stores
+        // the second half's part of tile t2 joins the first half's
+        if (kh) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int m = 16 * (tt ? t2 : t1) + ln;
-            if (m >= valid) continue;
-            float* op = a.out + ((tok0 + m) * H + h) * P;
+            for (int pt = 0; pt < PTW; ++pt) xchg[pi][PTW * pp + pt][lane] = acc[1][pt];
+        }
+        lds_barrier();
+        if (!kh) {
 #pragma unroll
             for (int pt = 0; pt < PTW; ++pt) {
-                const int p0 = 16 * (PTW * ph + pt) + 4 * kg;
-                const int xoff = m * 128 + (((p0 >> 3) ^ xswz(m)) * 16) + 2 * (p0 & 7);
-                float v[4] = {acc[tt][pt][0], acc[tt][pt][1], acc[tt][pt][2], acc[tt][pt][3]};
+                const f32x4 o = xchg[pi][PTW * pp + pt][lane];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[1][pt][i] += o[i];
+            }
+        }
+        // 3. epilogue: + D x, silu(z) gate in z's dtype, 16-byte fp32 stores
+        if (mrow < valid) {
+            float* op = a.out + ((tok0 + mrow) * H + h) * P;
+#pragma unroll
+            for (int pt = 0; pt < PTW; ++pt) {
+                const int p0 = 16 * (PTW * pp + pt) + 4 * kg;
+                const f32x4 r = kh ? acc[0][pt] : acc[1][pt];
+                float v[4] = {r[0], r[1], r[2], r[3]};
                 if (a.D) {
+                    const int xoff = mrow * 128 + (((p0 >> 3) ^ xswz(mrow)) * 16) + 2 * (p0 & 7);
                     const bf16x4 xv = *reinterpret_cast<const bf16x4*>(slot + xoff);
                     float dv[4];
                     if (a.D_has_hdim) {
@@ -334,15 +375,13 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                     for (int i = 0; i < 4; ++i) v[i] += dv[i] * (float)xv[i];
                 }
                 if (HASZ) {
-                    const bf16x4 zv = *reinterpret_cast<const bf16x4*>(slot + XB + SB + xoff);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) v[i] *= rbf(silu_f((float)zv[i]));
+                    for (int i = 0; i < 4; ++i) v[i] *= rbf(silu_f((float)zr[pt][i]));
                 }
                 *reinterpret_cast<float4*>(op + p0) = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
     }
-    wait_vmem<0>();     // the tail heads re-loaded into unused slots
 }
 
 }  // namespace
