@@ -6,8 +6,8 @@
 // with CB = bf16(C B^T) (seq_idx-masked), h_c the bf16 state entering chunk c.
 //
 // One workgroup per (batch, chunk, group) covers every head of the group, so
-// CB is built once and used by all of them.  8 compute wavefronts (+ one that
-// only loads, below); the chunk's 16-row
+// CB is built once and used by all of them.  8 compute wavefronts (+ four that
+// only load, below); the chunk's 16-row
 // output tiles are paired (t, Q/16-1-t) so that every pair carries the same
 // causal (triangular) work; the wavefronts of a pair split that work in two
 // halves of (row tile, k-tile) units, the first accumulating the long tile's
@@ -17,11 +17,12 @@
 // Per head, the x rows [Q x 64], the carried state [64 x N], dA / dt of the
 // chunk and D are brought into a ring of R LDS slots by direct
 // global -> LDS loads (global_load_lds_dwordx4), R - 1 heads ahead of use;
-// the group's B rows use the same path once, for the CB build.  A ninth
-// wavefront issues all of these loads and waits for them (vmcnt) before the
-// barrier that hands a slot over: vmcnt is one in-order counter per
-// wavefront for loads and stores alike, so a wavefront that also stored the
-// outputs would wait for its stores as well.  Rows are dense in LDS with their
+// the group's B rows use the same path once, for the CB build.  Four
+// wavefronts besides the compute ones issue these loads (one alone cannot keep
+// enough in flight) and wait for them (vmcnt) before the barrier that hands a
+// slot over: vmcnt is one in-order counter per wavefront for loads and stores
+// alike, so a wavefront that also stored the outputs would wait for its
+// stores as well.  Rows are dense in LDS with their
 // 16-byte chunks XOR-swizzled so that the reads below hit distinct banks.
 //
 // The products are computed transposed, y^T = h_c C^T + x^T W^T with
@@ -44,7 +45,9 @@
 namespace {
 
 constexpr int NWAVES = 8;                 // compute wavefronts
-constexpr int THREADS = (NWAVES + 1) * 64; // + the load wavefront
+constexpr int NLOAD = 4;                  // load wavefronts (one alone cannot keep
+                                          // enough direct loads in flight)
+constexpr int THREADS = (NWAVES + NLOAD) * 64;
 constexpr int P = 64;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int LDS_BYTES = 160 * 1024;
@@ -100,10 +103,13 @@ struct Shape {
     static constexpr int RING = ring_bytes(R);
     // 1 KB direct loads of the load wavefront per head / for the B rows
     static constexpr int XI = XB / 1024, SI = SB / 1024, ZI = ZB / 1024, BI = BT / 1024;
-    static constexpr int CNT = XI + SI + ZI + 2;             // + dA / dt, D
+    // per load wavefront: XL + SL tile loads (+ dA / dt or D for wavefronts 0, 1)
+    static constexpr int XL = XI / NLOAD, SL = SI / NLOAD, BL = BI / NLOAD;
+    static constexpr int WAIT01 = (R - 2) * (XL + SL + 1), WAIT23 = (R - 2) * (XL + SL);
+    static_assert(XI % NLOAD == 0 && SI % NLOAD == 0 && BI % NLOAD == 0, "even load split");
     static_assert(NPAIRS * WPP == NWAVES && PPARTS * PTW == 4 && PPARTS >= 1, "wavefront split");
     static_assert(ring_bytes(R) + FIXED <= LDS_BYTES, "LDS budget");
-    static_assert((R - 2) * CNT <= 63, "vmcnt range");
+    static_assert(WAIT01 <= 63, "vmcnt range");
 };
 
 template <int NS, int QT, bool HASZ>
@@ -132,7 +138,8 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     const int seq_prev = (a.seq_idx && ci > 0) ? a.seq_idx[tok0 - 1] : 0;
     const uint32_t ring_lds = lds_addr(ring);
 
-    const bool loader = w == NWAVES;
+    const bool loader = w >= NWAVES;
+    const int li = w - NWAVES;                            // load wavefront index
 
     // ---- plain loads: C fragments of the pair's two row tiles, seq ids -----
     bf16x8 cfr[2][NS];
@@ -148,39 +155,45 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     for (int q = threadIdx.x; q < Q; q += THREADS)
         seqs[q] = (a.seq_idx && q < valid) ? a.seq_idx[tok0 + q] : -1;
 
-    // ---- the load wavefront: head j -> slot k.  Lane l of load u brings
-    // 16-byte chunk 64 u + l of a tile (row, swizzled column).
+    // ---- the load wavefronts: head j -> slot k.  Lane l of load u brings
+    // 16-byte chunk 64 u + l of a tile (row, swizzled column); load wavefront
+    // li takes its share of every tile's loads.
     const int64_t cq0 = ((int64_t)bi * H * nc + ci) * Q;  // dA / dt row of head 0 (+ h nc Q)
     const int64_t st0 = ((int64_t)bi * nc + ci) * H * P * N;
     auto issue = [&](int j, int k) {
         const int h = g * hpg + j;
         const uint32_t sb = ring_lds + k * SLOT;
 #pragma unroll
-        for (int u = 0; u < S::XI; ++u) {
+        for (int uu = 0; uu < S::XL; ++uu) {
+            const int u = li * S::XL + uu;
             const int gi = 64 * u + lane, r = gi / 8;
             const int64_t off = (tok0 + min(r, valid - 1)) * H * P + h * P + 8 * ((gi % 8) ^ xswz(r));
             dma16(a.x + off, sb + 1024 * u);
         }
         const bf16* sp = a.states + st0 + (int64_t)h * P * N;
 #pragma unroll
-        for (int u = 0; u < S::SI; ++u) {
+        for (int uu = 0; uu < S::SL; ++uu) {
+            const int u = li * S::SL + uu;
             const int gi = 64 * u + lane, p = gi / SCPR;
             dma16(sp + p * N + 8 * ((gi % SCPR) ^ sswz<SCPR>(p)), sb + XB + 1024 * u);
         }
         const int64_t row = cq0 + (int64_t)h * nc * Q;
-        if (lane < Q / 2) {
+        if (li == 0 && lane < Q / 2) {
             const float* src = lane < Q / 4 ? a.dA + row + 4 * lane : a.dt + row + 4 * (lane - Q / 4);
             dma16(src, sb + XB + SB + ZB);
         }
-        const float* dsrc = a.D ? (a.D_has_hdim ? a.D + h * P + lane : a.D + h) : a.dA + cq0;
-        dma4(dsrc, sb + XB + SB + ZB + 2 * Q * 4);
+        if (li == 1) {
+            const float* dsrc = a.D ? (a.D_has_hdim ? a.D + h * P + lane : a.D + h) : a.dA + cq0;
+            dma4(dsrc, sb + XB + SB + ZB + 2 * Q * 4);
+        }
     };
 
     // ---- the group's B rows (aliasing ring slots 1..) and head 0 -----------
     if (loader) {
         const bf16* Bg = a.B + (tok0 * G + g) * N;
 #pragma unroll
-        for (int u = 0; u < S::BI; ++u) {
+        for (int uu = 0; uu < S::BL; ++uu) {
+            const int u = li * S::BL + uu;
             const int gi = 64 * u + lane, r = gi / SCPR;
             dma16(Bg + min(r, valid - 1) * rs + 8 * ((gi % SCPR) ^ sswz<SCPR>(r)),
                   ring_lds + SLOT + 1024 * u);
@@ -234,7 +247,8 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
         for (int i = 1; i < R - 1; ++i) issue(min(i, hpg - 1), i);
         for (int j = 0; j < hpg; ++j) {
             // head j's loads done (R - 2 later heads may still be in flight)
-            wait_vmem<(R - 2) * S::CNT>();
+            if (li < 2) wait_vmem<S::WAIT01>();
+            else wait_vmem<S::WAIT23>();
             lds_barrier();                                  // slot j % R complete, slot (j-1) % R free
             issue(min(j + R - 1, hpg - 1), (j + R - 1) % R);
             lds_barrier();                                  // the compute wavefronts' exchange

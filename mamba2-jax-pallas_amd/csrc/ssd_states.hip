@@ -42,7 +42,10 @@
 
 namespace {
 
-constexpr int THREADS = 512;
+constexpr int NWAVES = 8;                  // compute wavefronts
+constexpr int NLOAD = 4;                   // load wavefronts (one alone cannot keep
+                                           // enough direct loads in flight)
+constexpr int THREADS = (NWAVES + NLOAD) * 64;
 constexpr int KB = 64;       // positions per stage (two MFMA K steps, one per half)
 constexpr int DEPTH = 6;     // LDS stage slots: DEPTH - 1 stages of loads in flight
 constexpr int P = 64;        // head dim
@@ -50,7 +53,14 @@ constexpr int NB = 64;       // dstate columns per workgroup
 constexpr int CPR = 8;       // 16-byte chunks per 128-byte tile row
 constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
 constexpr int SLOT = XB + BB + 512;                // + 64 weights, 64 copies of the decay
-static_assert(KB * CPR == THREADS, "one x and one B chunk per thread and stage");
+constexpr int TI = KB * CPR / 64;                  // 1 KB loads per tile and stage
+constexpr int TL = TI / NLOAD;                     // ... per load wavefront
+static_assert(TI % NLOAD == 0, "tiles split evenly over the load wavefronts");
+// loads of one load wavefront that may still be in flight when stage s is
+// needed: DEPTH - 2 later stages of 2 TL tile loads (+ weights / decay for
+// load wavefronts 0 and 1)
+constexpr int WAIT01 = (DEPTH - 2) * (2 * TL + 1), WAIT23 = (DEPTH - 2) * 2 * TL;
+static_assert(WAIT01 <= 63, "vmcnt range");
 
 // 16-byte chunk swizzle of tile row R (128-byte rows): 8 consecutive rows read
 // at one chunk pair land on disjoint banks.
@@ -101,34 +111,47 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         asm volatile("" ::"v"(acc[j]));
     }
 
-    // ---- direct-load sources: one x and one B chunk of each stage per thread
-    // (row, swizzled column); wavefront 0 also the weights, wavefront 1 the
-    // chunk's decay.
-    const int lr = threadIdx.x / CPR;
-    const int lc = ((threadIdx.x % CPR) ^ swz(lr)) * 8;
-    const bf16* xsrc = a.x + ((int64_t)bi * L * H + h) * P + lc;
+    // ---- the load wavefronts: stage st -> slot k.  Lane l of load u brings
+    // 16-byte chunk 64 u + l of the x / B tile (row, swizzled column); load
+    // wavefront li takes loads u in [li TL, li TL + TL), wavefront 0 also the
+    // stage's weights (64 words), wavefront 1 64 copies of the chunk's decay.
+    const bf16* xsrc = a.x + ((int64_t)bi * L * H + h) * P;
     const int64_t xstr = (int64_t)H * P;
-    const bf16* bsrc = a.B + ((int64_t)bi * L * a.G + g) * N + nb * NB + lc;
+    const bf16* bsrc = a.B + ((int64_t)bi * L * a.G + g) * N + nb * NB;
     const int64_t bstr = (int64_t)a.G * N;
     const int64_t bhc = ((int64_t)bi * H + h) * nc;
     const uint32_t ring_lds = lds_addr(ring);
-    const uint32_t tile_off = 64 * w * 16;
-
+    const int li = w - NWAVES;
     auto issue = [&](int st, int k) {
         const uint32_t sb = ring_lds + k * SLOT;
-        const int64_t t = min(st * KB + lr, L - 1);      // past the end: weight 0
-        dma16(xsrc + t * xstr, sb + tile_off);
-        dma16(bsrc + t * bstr, sb + XB + tile_off);
-        if (w < 2) {
-            const int c = st / SPC;
-            const float* p = w == 0 ? a.wts + (bhc + c) * Q + (st - c * SPC) * KB + lane
-                                    : a.scl + bhc + c;
-            dma4(p, sb + XB + BB + 256 * w);
-        }
-    };
-
 #pragma unroll
-    for (int i = 0; i < DEPTH - 1; ++i) issue(min(i, S - 1), i);
+        for (int uu = 0; uu < TL; ++uu) {
+            const int u = li * TL + uu;
+            const int gi = 64 * u + lane, r = gi / CPR;
+            const int64_t t = min(st * KB + r, L - 1);   // past the end: weight 0
+            const int col = ((gi % CPR) ^ swz(r)) * 8;
+            dma16(xsrc + t * xstr + col, sb + 1024 * u);
+            dma16(bsrc + t * bstr + col, sb + XB + 1024 * u);
+        }
+        const int c = st / SPC;
+        if (li == 0) dma4(a.wts + (bhc + c) * Q + (st - c * SPC) * KB + lane, sb + XB + BB);
+        if (li == 1) dma4(a.scl + bhc + c, sb + XB + BB + 256);
+    };
+    if (w >= NWAVES) {
+#pragma unroll
+        for (int i = 0; i < DEPTH - 1; ++i) issue(min(i, S - 1), i);
+        for (int s = 0; s < S; ++s) {
+            // stage s complete (later stages may be in flight)
+            if (li < 2) wait_vmem<WAIT01>();
+            else wait_vmem<WAIT23>();
+            lds_barrier();               // slot s % DEPTH complete, slot (s-1) % DEPTH free
+            issue(min(s + DEPTH - 1, S - 1), (s + DEPTH - 1) % DEPTH);
+            if (s % SPC == 0) lds_barrier();   // the compute wavefronts' exchange
+        }
+        wait_vmem<0>();                  // the tail stages re-loaded into unused slots
+        __syncthreads();                 // the final exchange
+        return;
+    }
 
     const int rA = 32 * kh + 4 * kg + (ln >> 2);   // tile rows of MFMA k = 0..3 (+16: 4..7)
     const int c1 = ln & 3;                         // 8-byte column group of the read
@@ -145,11 +168,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
     for (int s = 0; s < S; ++s) {
         const int k = s % DEPTH;
         const int c = s / SPC, kb = s - c * SPC;
-        // own loads of stage s done (DEPTH - 2 later stages may still be in flight)
-        if (w < 2) wait_vmem<(DEPTH - 2) * 3>();
-        else wait_vmem<(DEPTH - 2) * 2>();
-        lds_barrier();                               // slot k complete, slot k-1 free
-        issue(min(s + DEPTH - 1, S - 1), (s + DEPTH - 1) % DEPTH);
+        lds_barrier();                               // slot k complete (load wavefront)
         const char* slot = ring + k * SLOT;
         const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
         if (kb == 0) {
@@ -203,8 +222,6 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
         }
     }
-    wait_vmem<0>();     // the tail stages re-loaded into unused slots
-
     if (kh == 1) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) xchg[pw][j][lane] = acc[j];
