@@ -2,10 +2,11 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu-baseline]
 
-A step is one call of mamba2_jax.kernels.mamba_chunk_scan_combined_fwd (the five
-stage kernels: chunk_cumsum, chunk_state, state_passing, bmm_chunk, chunk_scan)
-on synthetic inputs already resident in HBM, returning the output and the final
-states.  Prints ONE JSON line (rank 0): tokens/s, ms per layer, the roofline
+A step is one call of mamba2_jax.kernels.mamba_chunk_scan_combined_fwd on
+synthetic inputs already resident in HBM, returning the output and the final
+states.  For bf16 at the benchmark shapes the five stages run as three kernels:
+chunk_cumsum (+ chunk-state weights), chunk_state + state_passing (one
+chunk-sequential kernel) and bmm_chunk + chunk_scan (one kernel).  Prints ONE JSON line (rank 0): tokens/s, ms per layer, the roofline
 fraction of the dominant kernel (per-stage durations come from HIP events
 recorded on the launch stream between the stages, inside the timed region),
 the per-stage table, a decode-step measurement (c4: 256 in-place
@@ -87,6 +88,17 @@ def scan_is_fused(cfg):
     dstate 64/128/256 and chunk_size 64/128 (m2::scan_fused_supported)."""
     return (cfg.dtype == "bf16" and cfg.headdim == 64 and cfg.dstate in (64, 128, 256)
             and cfg.chunk_size in (64, 128))
+
+
+def measured_traffic(config):
+    """HBM bytes per launch of each stage as measured by rocprofv3 FETCH_SIZE /
+    WRITE_SIZE (scaled by a plain copy's readings) for this config, from
+    profiles/hbm_traffic_<config>.json; empty when there is none."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config}.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
 
 
 def cpu_baseline(cfg, heads, min_seconds=10.0, max_reps=20):
@@ -252,8 +264,11 @@ def main(argv=None):
     else:
         roof = {"bound": "mfma", "achieved": stages[dom]["mfma_tflops"], "peak": peak_mfma,
                 "unit": "TFLOP/s", "frac": stages[dom]["mfma_frac"]}
+    traffic = measured_traffic(args.config)
     roof.update({"kernel": dom, "algorithmic_bytes": by, "algorithmic_flop": fl,
-                 "avg_launch_ms": stage_ms[dom], "traffic": None})
+                 "avg_launch_ms": stage_ms[dom], "traffic": traffic.get(dom)})
+    if traffic:
+        roof["traffic_source"] = traffic.get("source")
     tot_by = sum(w[0] for w in work.values())
     res = {
         "metric": METRIC, "value": cfg.tokens / (ms * 1e-3), "unit": "tokens/s",

@@ -43,8 +43,8 @@
 namespace {
 
 constexpr int NWAVES = 8;                  // compute wavefronts
-constexpr int NLOAD = 4;                   // load wavefronts (one alone cannot keep
-                                           // enough direct loads in flight)
+constexpr int NLOAD = 4;                   // load wavefronts: each keeps only so many
+                                           // direct loads in flight
 constexpr int THREADS = (NWAVES + NLOAD) * 64;
 constexpr int KB = 64;       // positions per stage (two MFMA K steps, one per half)
 constexpr int DEPTH = 6;     // LDS stage slots: DEPTH - 1 stages of loads in flight
