@@ -12,20 +12,22 @@
 // order, so HBM sees only x, B, w, the bf16 states entering each chunk and the
 // final states.
 //
-// Workgroup = 8 wavefronts (two per SIMD, so that one hides the other's LDS
-// and MFMA latency).  Positions stream through a ring of DEPTH LDS slots in
-// stages of KB = 64: each slot holds the x rows [64 x 64], the B rows
-// [64 x 64] and the stage's weights (+ the chunk's decay).  Wavefront w owns
-// head-dim rows 16 (w & 3) .. +15, all 64 dstate columns of the block (four
-// 16 x 16 tiles) and the positions 32 (w >> 2) .. +31 of every stage: the two
-// halves accumulate separate partial states (the recurrence is linear), which
-// are summed through LDS only where the state is written (chunk starts and
-// the end).  Slots are filled by direct global -> LDS loads
-// (global_load_lds_dwordx4), DEPTH - 1 stages ahead of use, with explicit
-// vmcnt waits: no load result passes through VGPRs, so nothing forces the
-// compiler to drain the loads in flight.  Tiles are dense in LDS with the
-// 16-byte chunks of each row XOR-swizzled so that the transposed reads below
-// hit 64 distinct banks per 32 lanes.
+// Workgroup = 8 compute wavefronts (two per SIMD, so that one hides the
+// other's LDS and MFMA latency) + 4 load wavefronts.  Positions stream through
+// a ring of DEPTH LDS slots in stages of KB = 64 or 128: each slot holds the x
+// rows [KB x 64], the B rows [KB x 64] and the stage's weights (+ the chunk's
+// decay).  Compute wavefront w owns head-dim rows 16 (w & 3) .. +15, all 64
+// dstate columns of the block (four 16 x 16 tiles) and the positions
+// (KB/2) (w >> 2) .. +KB/2-1 of every stage: the two halves accumulate
+// separate partial states (the recurrence is linear), which are summed
+// through LDS only where the state is written (chunk starts and the end).
+// The load wavefronts fill the slots with direct global -> LDS loads
+// (global_load_lds_dwordx4), DEPTH - 1 stages ahead of use, and wait for them
+// with explicit vmcnt waits: no load result passes through VGPRs, so nothing
+// forces the compiler to drain the loads in flight, and the compute
+// wavefronts' stores never hold up those waits.  Tiles are dense in LDS with
+// the 16-byte chunks of each row XOR-swizzled so that the transposed reads
+// below hit 64 distinct banks per 32 lanes.
 //
 // MFMA operands need 8 consecutive positions per lane for a fixed row / column:
 // they come straight from the row-major tiles through the gfx950 LDS transpose
@@ -46,21 +48,28 @@ constexpr int NWAVES = 8;                  // compute wavefronts
 constexpr int NLOAD = 4;                   // load wavefronts: each keeps only so many
                                            // direct loads in flight
 constexpr int THREADS = (NWAVES + NLOAD) * 64;
-constexpr int KB = 64;       // positions per stage (two MFMA K steps, one per half)
-constexpr int DEPTH = 6;     // LDS stage slots: DEPTH - 1 stages of loads in flight
 constexpr int P = 64;        // head dim
 constexpr int NB = 64;       // dstate columns per workgroup
 constexpr int CPR = 8;       // 16-byte chunks per 128-byte tile row
-constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
-constexpr int SLOT = XB + BB + 512;                // + 64 weights, 64 copies of the decay
-constexpr int TI = KB * CPR / 64;                  // 1 KB loads per tile and stage
-constexpr int TL = TI / NLOAD;                     // ... per load wavefront
-static_assert(TI % NLOAD == 0, "tiles split evenly over the load wavefronts");
-// loads of one load wavefront that may still be in flight when stage s is
-// needed: DEPTH - 2 later stages of 2 TL tile loads (+ weights / decay for
-// load wavefronts 0 and 1)
-constexpr int WAIT01 = (DEPTH - 2) * (2 * TL + 1), WAIT23 = (DEPTH - 2) * 2 * TL;
-static_assert(WAIT01 <= 63, "vmcnt range");
+
+// Stages of KB positions (64 or 128): each half of the compute wavefronts
+// takes KB/2 positions (KS MFMA K steps of 32).
+template <int KB>
+struct StCfg {
+    static constexpr int DEPTH = KB == 64 ? 6 : 4;   // LDS stage slots: DEPTH - 1 in flight
+    static constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
+    static constexpr int AUXB = KB * 4 + 256;        // weights, 64 copies of the decay
+    static constexpr int SLOT = XB + BB + AUXB;
+    static constexpr int TI = KB * CPR / 64;         // 1 KB loads per tile and stage
+    static constexpr int TL = TI / NLOAD;            // ... per load wavefront
+    static constexpr int KS = KB / 64;               // K steps per half
+    // loads of one load wavefront that may still be in flight when stage s is
+    // needed: DEPTH - 2 later stages of 2 TL tile loads (+ weights / decay for
+    // load wavefronts 0 and 1)
+    static constexpr int WAIT01 = (DEPTH - 2) * (2 * TL + 1), WAIT23 = (DEPTH - 2) * 2 * TL;
+    static_assert(TI % NLOAD == 0, "tiles split evenly over the load wavefronts");
+    static_assert(WAIT01 <= 63, "vmcnt range");
+};
 
 // 16-byte chunk swizzle of tile row R (128-byte rows): 8 consecutive rows read
 // at one chunk pair land on disjoint banks.
@@ -77,7 +86,10 @@ struct StatesArgs {
     int L, H, G, N, Q, nc, nblk, nwork;
 };
 
+template <int KB>
 __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
+    typedef StCfg<KB> C;
+    constexpr int DEPTH = C::DEPTH, XB = C::XB, BB = C::BB, SLOT = C::SLOT, TL = C::TL;
     __shared__ __align__(16) char ring[DEPTH * SLOT];
     __shared__ __align__(16) f32x4 xchg[4][4][64];   // partial states of the second half
 
@@ -134,16 +146,20 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
             dma16(bsrc + t * bstr + col, sb + XB + 1024 * u);
         }
         const int c = st / SPC;
-        if (li == 0) dma4(a.wts + (bhc + c) * Q + (st - c * SPC) * KB + lane, sb + XB + BB);
-        if (li == 1) dma4(a.scl + bhc + c, sb + XB + BB + 256);
+        const float* wsrc = a.wts + (bhc + c) * Q + (st - c * SPC) * KB;
+        if (li == 0) {
+            if (KB == 64) dma4(wsrc + lane, sb + XB + BB);
+            else if (lane < KB / 4) dma16(wsrc + 4 * lane, sb + XB + BB);
+        }
+        if (li == 1) dma4(a.scl + bhc + c, sb + XB + BB + KB * 4);
     };
     if (w >= NWAVES) {
 #pragma unroll
         for (int i = 0; i < DEPTH - 1; ++i) issue(min(i, S - 1), i);
         for (int s = 0; s < S; ++s) {
             // stage s complete (later stages may be in flight)
-            if (li < 2) wait_vmem<WAIT01>();
-            else wait_vmem<WAIT23>();
+            if (li < 2) wait_vmem<C::WAIT01>();
+            else wait_vmem<C::WAIT23>();
             lds_barrier();               // slot s % DEPTH complete, slot (s-1) % DEPTH free
             issue(min(s + DEPTH - 1, S - 1), (s + DEPTH - 1) % DEPTH);
             if (s % SPC == 0) lds_barrier();   // the compute wavefronts' exchange
@@ -153,10 +169,12 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         return;
     }
 
-    const int rA = 32 * kh + 4 * kg + (ln >> 2);   // tile rows of MFMA k = 0..3 (+16: 4..7)
+    // this half's K steps ks: tile rows (KB/2) kh + 32 ks + ...; the row swizzle
+    // repeats every 8 rows, so step ks is step 0 moved by 32 rows
+    const int rA = (KB / 2) * kh + 4 * kg + (ln >> 2);   // rows of MFMA k = 0..3 (+16: 4..7)
     const int c1 = ln & 3;                         // 8-byte column group of the read
     const int cb = 8 * (c1 & 1);
-    const int wpos = 32 * kh + (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // k index ln & 7
+    const int wpos = (KB / 2) * kh + (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // k index ln & 7
     const int xo0 = rA * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
     const int xo1 = (rA + 16) * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
     int bo0[4], bo1[4];
@@ -189,37 +207,40 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
                     store_untracked(pp + 16 * j, __builtin_bit_cast(uint64_t, o));
                 }
             }
-            const float sc = aux[64];
+            const float sc = aux[KB];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[j][r] *= sc;
         }
-        // acc += B^T (w x) over this half's 32 positions.  MFMA k index j < 4 is
-        // position 32 kh + 4 kg + j, j >= 4 is 32 kh + 16 + 4 kg + j - 4.
+        // acc += B^T (w x) over this half's KB/2 positions.  In step ks, MFMA k
+        // index j < 4 is position (KB/2) kh + 32 ks + 4 kg + j, j >= 4 is 16 more.
         // Lane j < 8 of each row reads the weight of k index j; the row shares them.
-        const float wl = aux[wpos];
-        const float wv[8] = {row_bcast<0>(wl), row_bcast<1>(wl), row_bcast<2>(wl), row_bcast<3>(wl),
-                             row_bcast<4>(wl), row_bcast<5>(wl), row_bcast<6>(wl), row_bcast<7>(wl)};
-        bf16x8 xh, xl;
-        {
-            const bf16x4 x0 = ds_read_tr(slot + xo0);
-            const bf16x4 x1 = ds_read_tr(slot + xo1);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float v = (float)(j < 4 ? x0[j] : x1[j - 4]) * wv[j];
-                const bf16 hi = (bf16)v;
-                xh[j] = hi;
-                xl[j] = (bf16)(v - (float)hi);
+        for (int ks = 0; ks < C::KS; ++ks) {
+            const float wl = aux[wpos + 32 * ks];
+            const float wv[8] = {row_bcast<0>(wl), row_bcast<1>(wl), row_bcast<2>(wl), row_bcast<3>(wl),
+                                 row_bcast<4>(wl), row_bcast<5>(wl), row_bcast<6>(wl), row_bcast<7>(wl)};
+            bf16x8 xh, xl;
+            {
+                const bf16x4 x0 = ds_read_tr(slot + xo0 + ks * 32 * (2 * P));
+                const bf16x4 x1 = ds_read_tr(slot + xo1 + ks * 32 * (2 * P));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float v = (float)(j < 4 ? x0[j] : x1[j - 4]) * wv[j];
+                    const bf16 hi = (bf16)v;
+                    xh[j] = hi;
+                    xl[j] = (bf16)(v - (float)hi);
+                }
             }
-        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const bf16x4 b0 = ds_read_tr(slot + bo0[j]);
-            const bf16x4 b1 = ds_read_tr(slot + bo1[j]);
-            const bf16x8 bf = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) {
+                const bf16x4 b0 = ds_read_tr(slot + bo0[j] + ks * 32 * (2 * NB));
+                const bf16x4 b1 = ds_read_tr(slot + bo1[j] + ks * 32 * (2 * NB));
+                const bf16x8 bf = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
+            }
         }
     }
     if (kh == 1) {
@@ -244,7 +265,7 @@ namespace m2 {
 
 bool states_fused_supported(const m2_ssd_combined_args& a) {
     return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
-           a.chunk_size % KB == 0 && a.chunk_size <= 256 && a.ngroups > 0 &&
+           a.chunk_size % 64 == 0 && a.chunk_size <= 256 && a.ngroups > 0 &&
            a.nheads % a.ngroups == 0;
 }
 
@@ -261,7 +282,8 @@ int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const f
     const int64_t nwork = a.batch * a.nheads * sa.nblk;
     M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "ssd_states: too many workgroups");
     sa.nwork = (int)nwork;
-    k_ssd_states<<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    if (sa.Q % 128 == 0) k_ssd_states<128><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    else k_ssd_states<64><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
     return check_launch("ssd_states");
 }
 
