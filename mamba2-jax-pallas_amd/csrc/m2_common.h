@@ -105,6 +105,12 @@ M2_DEV void store_untracked(float* p, float v) {
 M2_DEV void store_untracked(void* p, uint64_t v) {
     asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
 }
+// (a store of more than 8 bytes needs one wait state before a VALU may
+// overwrite its data registers; the compiler cannot see that inside asm)
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+M2_DEV void store_untracked_x4(void* p, u32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 0" ::"v"(p), "v"(v) : "memory");
+}
 
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;

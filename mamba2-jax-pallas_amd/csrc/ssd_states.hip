@@ -92,6 +92,9 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
     constexpr int DEPTH = C::DEPTH, XB = C::XB, BB = C::BB, SLOT = C::SLOT, TL = C::TL;
     __shared__ __align__(16) char ring[DEPTH * SLOT];
     __shared__ __align__(16) f32x4 xchg[4][4][64];   // partial states of the second half
+    // bf16 state rows of each first-half wavefront on their way to HBM: rows
+    // of 64 columns + 8 pad (144 bytes), 16 per wavefront
+    __shared__ __align__(16) bf16 pst[4][16][72];
 
     const int work = xcd_remap(blockIdx.x, a.nwork);
     const int nb = work % a.nblk;
@@ -198,13 +201,23 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
             }
             lds_barrier();
             if (kh == 0) {
-                bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + prow) * N + NB * nb + 4 * kg;
+                // round the summed state to bf16, then store whole 128-byte rows:
+                // lane (ln, kg) writes 4 columns of row ln, then reads back 16
+                // bytes (8 columns) of rows (lane >> 3) and 8 + (lane >> 3)
+                bf16* pr = &pst[pw][0][0];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const f32x4 o2 = xchg[pw][j][lane];
                     const bf16x4 o = {(bf16)(acc[j][0] + o2[0]), (bf16)(acc[j][1] + o2[1]),
                                       (bf16)(acc[j][2] + o2[2]), (bf16)(acc[j][3] + o2[3])};
-                    store_untracked(pp + 16 * j, __builtin_bit_cast(uint64_t, o));
+                    *reinterpret_cast<bf16x4*>(pr + ln * 72 + 16 * j + 4 * kg) = o;
+                }
+                bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + 16 * pw) * N + NB * nb;
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int row = 8 * half + (lane >> 3), col = 8 * (lane & 7);
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(pr + row * 72 + col);
+                    store_untracked_x4(pp + (int64_t)row * N + col, v);
                 }
             }
             const float sc = aux[KB];
