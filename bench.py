@@ -6,10 +6,11 @@ A step is one call of mamba2_jax.kernels.mamba_chunk_scan_combined_fwd on
 synthetic inputs already resident in HBM, returning the output and the final
 states.  For bf16 at the benchmark shapes the five stages run as three kernels:
 chunk_cumsum (+ chunk-state weights), chunk_state + state_passing (one
-chunk-sequential kernel) and bmm_chunk + chunk_scan (one kernel).  Prints ONE JSON line (rank 0): tokens/s, ms per layer, the roofline
-fraction of the dominant kernel (per-stage durations come from HIP events
-recorded on the launch stream between the stages, inside the timed region),
-the per-stage table, a decode-step measurement (c4: 256 in-place
+chunk-sequential kernel) and bmm_chunk + chunk_scan (one kernel).  Prints ONE
+JSON line (rank 0): tokens/s and ms per layer (K back-to-back steps with events
+only around them), the roofline fraction of the dominant kernel and the
+per-stage table (a second timed pass of K steps with HIP events recorded on the
+launch stream at every kernel boundary), a decode-step measurement (c4: 256 in-place
 selective_state_update steps) and the CPU baseline (the oracle's NumPy
 restatement of the reference's naive path, timed on a bounded head sample on
 this host's cores).
@@ -101,6 +102,48 @@ def measured_traffic(config):
         return json.load(f)
 
 
+class HipEvents:
+    """Raw HIP events for the per-stage timing, created with
+    hipEventDisableSystemFence: recording one does not write back and
+    invalidate the caches between the kernels it separates (a default event
+    does, which adds ~4 us per record).  Uses the HIP runtime torch loaded."""
+
+    FLAGS = 0x20000000          # hipEventDisableSystemFence
+
+    class Event:
+        def __init__(self, handle):
+            self.cuda_event = handle
+
+    def __init__(self):
+        import ctypes
+        self._ct = ctypes
+        self._hip = ctypes.CDLL("libamdhip64.so.7")
+        self._hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self._hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                  ctypes.c_void_p]
+        self._hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self._made = []
+
+    def new(self):
+        e = self._ct.c_void_p()
+        rc = self._hip.hipEventCreateWithFlags(self._ct.byref(e), self.FLAGS)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+        self._made.append(e.value)
+        return self.Event(e.value)
+
+    def elapsed_ms(self, a, b):
+        f = self._ct.c_float()
+        rc = self._hip.hipEventElapsedTime(self._ct.byref(f), a.cuda_event, b.cuda_event)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return f.value
+
+    def __del__(self):
+        for e in getattr(self, "_made", []):
+            self._hip.hipEventDestroy(e)
+
+
 def cpu_baseline(cfg, heads, min_seconds=10.0, max_reps=20):
     """The oracle's NumPy restatement of the reference naive path (float32), on
     the first `heads` heads (whole groups) of the workload, scaled to all heads."""
@@ -171,8 +214,8 @@ def bench_decode(steps=256, warmup=16):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
@@ -215,26 +258,41 @@ def main(argv=None):
     for _ in range(args.warmup):
         mamba_chunk_scan_combined_fwd(**kw)
     K = args.steps
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(K)]
-    for e in evs:                                   # create the events outside the timed region
-        for x in e:
-            x.record()
+    # timed region 1 (value): K back-to-back steps, events only around them
     torch.cuda.synchronize()
     g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
     g0.record()
     for i in range(K):
-        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[i])
+        mamba_chunk_scan_combined_fwd(**kw)
     g1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms = g0.elapsed_time(g1) / K
-    slot_ms = [float(np.mean([evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(K)]))
-               for j in range(5)]
+    # timed region 2 (stages): the same K steps with HIP events recorded on the
+    # launch stream at each kernel boundary; a fused kernel's time lands in the
+    # first slot of its group (the other slots of the group are not recorded)
+    hev = HipEvents()
+    fs, fc = states_is_fused(cfg), scan_is_fused(cfg)
+    keep = [True, True, True, not fs, not fc, True]
+    evs = [[hev.new() if k else None for k in keep] for _ in range(K)]
+    for _ in range(3):
+        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[0])
+    torch.cuda.synchronize()
+    for i in range(K):
+        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[i])
+    torch.cuda.synchronize()
+
+    def slot(j):
+        # interval j: from event j (or the last recorded one before it) to event j + 1
+        a = max(x for x in range(j + 1) if keep[x])
+        if not keep[j + 1]:
+            return 0.0
+        return float(np.mean([hev.elapsed_ms(evs[i][a], evs[i][j + 1]) for i in range(K)]))
+    slot_ms = [slot(j) for j in range(5)]
+    stages_ms_total = float(np.mean([hev.elapsed_ms(evs[i][0], evs[i][5]) for i in range(K)]))
     work = stage_work(cfg, with_init=d["initial_states"] is not None)
-    # event slots: cumsum, chunk_state, state_passing, bmm_chunk, chunk_scan; a
-    # fused kernel's time lands in the first slot of its group, the other slots of
-    # the group hold only back-to-back event records
+    # event slots: cumsum, chunk_state, state_passing, bmm_chunk, chunk_scan
     slots = dict(zip(STAGES, slot_ms))
     stage_ms = {}
     if states_is_fused(cfg):
@@ -280,6 +338,7 @@ def main(argv=None):
                    "ngroups": cfg.ngroups, "headdim": cfg.headdim, "dstate": cfg.dstate,
                    "chunk_size": cfg.chunk_size, "parallelism": "single-gpu"},
         "ms_per_layer": ms, "wall_ms_per_step": wall / K * 1e3,
+        "ms_per_layer_with_stage_events": stages_ms_total,
         "layer_hbm_frac": tot_by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
         "roofline": roof, "stages": stages,
         "reference_published": {"hardware": "H100", "dtype": "fp32", "pallas_ms": 0.94,

@@ -80,7 +80,7 @@ Layout layout_of(const m2_ssd_combined_args& a) {
 }
 
 int record(void** ev, int i, hipStream_t s) {
-    if (!ev) return M2_OK;
+    if (!ev || !ev[i]) return M2_OK;
     if (hipEventRecord((hipEvent_t)ev[i], s) != hipSuccess)
         return m2::set_error(M2_ERR_LAUNCH, "m2_ssd_combined: hipEventRecord failed");
     return M2_OK;

@@ -269,6 +269,7 @@ int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t s
                "chunk_state_varlen: chunk_size must be a multiple of 16 and <= 256");
     M2_REQUIRE(a.states_dtype == M2_F32 || a.states_dtype == M2_BF16, M2_ERR_UNSUPPORTED,
                "chunk_state_varlen: states dtype %d", a.states_dtype);
+    if (varlen_states_fast_supported(a)) return launch_varlen_states(a, s);
     StateArgs sa{};
     sa.x = a.x; sa.B = a.B; sa.dt = a.dt; sa.dA = a.dA_cumsum; sa.cu_seqlens = a.cu_seqlens;
     sa.chunk_states = a.chunk_states; sa.states_bf16 = a.states_dtype == M2_BF16; sa.out = a.out;

@@ -18,6 +18,11 @@ int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t stream);
 int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t stream);
 int launch_ssu(const m2_ssu_args& a, hipStream_t stream);
 
+// chunk_state_varlen for bf16, head dim 64, dstate % 64 == 0, chunk_size % 32
+// == 0 (<= 256): one workgroup per (sequence, head, 64-column dstate block)
+bool varlen_states_fast_supported(const m2_chunk_state_varlen_args& a);
+int launch_varlen_states(const m2_chunk_state_varlen_args& a, hipStream_t stream);
+
 // fused bmm_chunk + chunk_scan of the combined forward (bf16 inputs)
 bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size);
 int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const float* dt_out,

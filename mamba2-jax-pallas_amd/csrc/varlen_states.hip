@@ -1,0 +1,228 @@
+// chunk_state_varlen for bf16 inputs, head dim 64 and dstate a multiple of 64:
+// the final state of each packed sequence s (batch 1) over the chunk c that
+// holds its last token,
+//   out[s, h] = sum_{q in [qlo, qhi)} w[q] x[q, :]^T B[q, :]  (+ carry)
+//   w[q]      = exp(min(dA[qhi - 1] - dA[q], 0)) dt[q]
+//   carry     = exp(dA[qhi - 1]) states[c, h]   when s started before chunk c
+// with q the positions of chunk c, [qlo, qhi) the part of s in it, and
+// states[c] the state entering chunk c.
+//
+// One workgroup per (sequence, head, 64-column dstate block): 6144 at the
+// packed 47b shape, several per CU, so a one-shot kernel hides its latency
+// by occupancy.  The x rows [Q x 64] and the block's B rows [Q x 64] arrive by
+// direct global -> LDS loads (16-byte chunks of each 128-byte row
+// XOR-swizzled, so the transposed reads hit distinct banks); the weights are
+// computed from dA / dt while they are in flight.  Wavefront w owns head-dim
+// rows 16 w .. 16 w + 15 and all 64 columns (four 16 x 16 tiles): it computes
+// h^T[n, p] += B^T[n, q] (w x)[q, p] with MFMA operands read through the
+// gfx950 LDS transpose read, w x split into hi + lo bf16 parts (near-fp32
+// accuracy, as the reference's fp32 einsum).  The result goes through LDS so
+// that each output row of 64 fp32 (and its carry row) moves as 16 lanes x 16
+// bytes.
+//
+// Follows reference kernels/chunk_state_fwd.py:448-597 (varlen states) and
+// :239-269 (weights).
+#include "m2_internal.h"
+
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int P = 64;        // head dim
+constexpr int NB = 64;       // dstate columns per workgroup
+constexpr int CPR = 8;       // 16-byte chunks per 128-byte tile row
+constexpr int OS = NB + 4;   // output staging row stride (floats)
+
+// 16-byte chunk swizzle of tile row R (128-byte rows): 8 consecutive rows read
+// at one chunk pair land on disjoint banks.
+M2_DEV int swz(int R) { return ((R >> 1) & 3) << 1; }
+
+// LDS bytes of the x and B tiles, which the output staging [64][OS] fp32
+// later reuses
+__host__ __device__ inline int tiles_bytes(int Q) {
+    return Q * (P + NB) * 2 > P * OS * 4 ? Q * (P + NB) * 2 : P * OS * 4;
+}
+
+struct VarlenArgs {
+    const bf16* x;
+    const bf16* B;
+    const float* dt;        // [H, nc, Q]
+    const float* dA;        // [H, nc, Q]
+    const int32_t* cu;      // [nseq + 1]
+    const void* states;     // [nc, H, P, N]
+    float* out;             // [nseq, H, P, N]
+    int L, H, G, N, Q, nc, nblk, nwork, states_bf16;
+};
+
+__global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
+    extern __shared__ __align__(16) char smem[];
+    const int Q = a.Q, H = a.H, N = a.N;
+    const int XB = Q * P * 2;                                   // x tile bytes
+    char* xs = smem;                                            // [Q][64] bf16, then B
+    float* ot = reinterpret_cast<float*>(smem);                 // [64][OS], after the tiles
+    float* wq = reinterpret_cast<float*>(smem + tiles_bytes(Q)); // [Q]
+
+    const int work = xcd_remap(blockIdx.x, a.nwork);
+    const int nb = work % a.nblk;
+    const int sh = work / a.nblk;
+    const int h = sh % H, s = sh / H;
+    const int g = h / (H / a.G);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int ln = lane & 15, kg = lane >> 4;
+    float* op = a.out + (((int64_t)s * H + h) * P) * N + NB * nb;
+
+    // clamp malformed boundaries into [0, L] so every access stays in bounds
+    const int end = min(max(a.cu[s + 1], 0), a.L);
+    const int start = min(max(a.cu[s], 0), end);
+    if (end <= start) {                         // empty sequence: zero state
+        for (int i = threadIdx.x; i < P * NB / 4; i += THREADS) {
+            const int r = i / (NB / 4), c4 = 4 * (i % (NB / 4));
+            *reinterpret_cast<float4*>(op + (int64_t)r * N + c4) = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        return;
+    }
+    const int c = (end - 1) / Q;
+    const int qlo = max(start - c * Q, 0), qhi = end - c * Q;
+    const bool carry = start < c * Q;
+
+    // ---- direct loads of the chunk's x rows and the block's B rows: load u
+    // (64 lanes x 16 bytes = 8 rows) goes to tile bytes [1024 u, 1024 u + 1024);
+    // rows past the end of the sequence batch are clamped (their weight is 0)
+    const int64_t t0 = (int64_t)c * Q;
+    const bf16* xsrc = a.x + (int64_t)h * P;
+    const bf16* bsrc = a.B + (int64_t)g * N + NB * nb;
+    const uint32_t xl = lds_addr(xs);
+    for (int u = w; u < Q * CPR / 64; u += THREADS / 64) {
+        const int gi = 64 * u + lane, r = gi / CPR;
+        const int64_t t = min(t0 + r, (int64_t)a.L - 1);
+        const int col = ((gi % CPR) ^ swz(r)) * 8;
+        dma16(xsrc + t * H * P + col, xl + 1024 * u);
+        dma16(bsrc + t * a.G * N + col, xl + XB + 1024 * u);
+    }
+
+    // ---- the carry rows of this lane's outputs (rows 16 w + 4 it + (lane >> 4),
+    // columns 4 (lane & 15) + i), loaded now so that their latency overlaps
+    // the tiles'
+    const int64_t soff = (((int64_t)c * H + h) * P) * N + NB * nb;
+    const int orr = 16 * w + (lane >> 4), occ = 4 * (lane & 15);
+    bf16x4 cv16[4];
+    float4 cv32[4];
+    if (carry) {
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            const int64_t e = soff + (int64_t)(orr + 4 * it) * N + occ;
+            if (a.states_bf16)
+                cv16[it] = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16*>(a.states) + e);
+            else
+                cv32[it] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.states) + e);
+        }
+    }
+
+    // ---- weights (while the tiles are in flight)
+    const float* dAp = a.dA + ((int64_t)h * a.nc + c) * Q;
+    const float* dtp = a.dt + ((int64_t)h * a.nc + c) * Q;
+    const float dA_ref = dAp[qhi - 1];
+    for (int q = threadIdx.x; q < Q; q += THREADS)
+        wq[q] = (q >= qlo && q < qhi) ? expf(fminf(dA_ref - dAp[q], 0.f)) * dtp[q] : 0.f;
+    wait_vmem<0>();
+    __syncthreads();
+
+    // ---- acc[j] = h^T tile: lane (ln, kg) holds row p = 16 w + ln, columns
+    // n = 16 j + 4 kg + i.  K step ks covers positions 32 ks .. 32 ks + 31:
+    // MFMA k index j < 4 is position 32 ks + 4 kg + j, j >= 4 is 16 more.
+    const int rA = 4 * kg + (ln >> 2);                // rows read by this lane (+16)
+    const int c1 = ln & 3;                            // 8-byte column group of the read
+    const int cb = 8 * (c1 & 1);
+    const int wpos = (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // k index ln & 7
+    const int xo0 = rA * (2 * P) + (((2 * w + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
+    const int xo1 = (rA + 16) * (2 * P) + (((2 * w + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
+    int bo0[4], bo1[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
+        bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = zero4();
+    // the row swizzle repeats every 8 rows, so step ks is step 0 moved by 32 rows
+    for (int ks = 0; ks < Q / 32; ++ks) {
+        const float wl = wq[wpos + 32 * ks];
+        const float wv[8] = {row_bcast<0>(wl), row_bcast<1>(wl), row_bcast<2>(wl), row_bcast<3>(wl),
+                             row_bcast<4>(wl), row_bcast<5>(wl), row_bcast<6>(wl), row_bcast<7>(wl)};
+        bf16x8 xh, xlo;
+        const bf16x4 x0 = ds_read_tr(xs + xo0 + ks * 32 * (2 * P));
+        const bf16x4 x1 = ds_read_tr(xs + xo1 + ks * 32 * (2 * P));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = (float)(j < 4 ? x0[j] : x1[j - 4]) * wv[j];
+            const bf16 hi = (bf16)v;
+            xh[j] = hi;
+            xlo[j] = (bf16)(v - (float)hi);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bf16x4 b0 = ds_read_tr(xs + bo0[j] + ks * 32 * (2 * NB));
+            const bf16x4 b1 = ds_read_tr(xs + bo1[j] + ks * 32 * (2 * NB));
+            const bf16x8 bf = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xlo, acc[j], 0, 0, 0);
+        }
+    }
+
+    // ---- through LDS (in place of the tiles, once every wavefront is done
+    // with them; each wavefront its own 16 rows), then whole rows
+    lds_barrier();
+    float* orow = ot + (16 * w) * OS;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<f32x4*>(orow + ln * OS + 16 * j + 4 * kg) = acc[j];
+    const float cs = carry ? expf(dA_ref) : 0.f;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int r = orr + 4 * it;
+        float4 v = *reinterpret_cast<const float4*>(ot + r * OS + occ);
+        if (carry) {
+            float cv[4];
+            if (a.states_bf16) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) cv[i] = (float)cv16[it][i];
+            } else {
+                cv[0] = cv32[it].x; cv[1] = cv32[it].y; cv[2] = cv32[it].z; cv[3] = cv32[it].w;
+            }
+            v.x += cs * cv[0]; v.y += cs * cv[1]; v.z += cs * cv[2]; v.w += cs * cv[3];
+        }
+        *reinterpret_cast<float4*>(op + (int64_t)r * N + occ) = v;
+    }
+}
+
+}  // namespace
+
+namespace m2 {
+
+bool varlen_states_fast_supported(const m2_chunk_state_varlen_args& a) {
+    return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
+           a.chunk_size % 32 == 0 && a.chunk_size <= 256;
+}
+
+int launch_varlen_states(const m2_chunk_state_varlen_args& a, hipStream_t s) {
+    M2_REQUIRE(varlen_states_fast_supported(a), M2_ERR_UNSUPPORTED,
+               "varlen_states: unsupported shape / dtype");
+    VarlenArgs k{};
+    k.x = (const bf16*)a.x; k.B = (const bf16*)a.B; k.dt = a.dt; k.dA = a.dA_cumsum;
+    k.cu = a.cu_seqlens; k.states = a.chunk_states; k.out = a.out;
+    k.states_bf16 = a.states_dtype == M2_BF16;
+    k.L = (int)a.seqlen; k.H = (int)a.nheads; k.G = (int)a.ngroups; k.N = (int)a.dstate;
+    k.Q = (int)a.chunk_size; k.nc = (int)a.nchunks; k.nblk = (int)(a.dstate / NB);
+    const int64_t nwork = a.nseq * a.nheads * k.nblk;
+    M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "varlen_states: too many workgroups");
+    k.nwork = (int)nwork;
+    const size_t shm = (size_t)tiles_bytes(k.Q) + (size_t)k.Q * 4;
+    if (shm > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(k_varlen_states),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return set_error(M2_ERR_LAUNCH, "varlen_states: cannot reserve %zu B of LDS", shm);
+    k_varlen_states<<<(unsigned)k.nwork, THREADS, shm, s>>>(k);
+    return check_launch("varlen_states");
+}
+
+}  // namespace m2

@@ -272,16 +272,20 @@ def test_chunk_scan_large_decay_is_stable():
 # chunk_state_varlen
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("nseq,H,P,N,G,Q,states_dtype", [
-    (10, 8, 64, 64, 1, 64, "f32"),        # reference varlen configs
-    (5, 8, 64, 64, 8, 64, "bf16"),
-    (6, 16, 64, 256, 8, 128, "bf16"),     # c3-like
+@pytest.mark.parametrize("nseq,H,P,N,G,Q,states_dtype,empty", [
+    (10, 8, 64, 64, 1, 64, "f32", False),        # reference varlen configs
+    (5, 8, 64, 64, 8, 64, "bf16", False),
+    (6, 16, 64, 256, 8, 128, "bf16", False),     # c3-like
+    (5, 8, 64, 128, 2, 256, "bf16", True),       # chunk 256, an empty sequence
+    (7, 4, 32, 64, 1, 64, "bf16", True),         # head dim 32 (general kernel)
 ])
-def test_chunk_state_varlen(nseq, H, P, N, G, Q, states_dtype):
-    announce("chunk_state_varlen", nseq, H, P, N, G, Q, states_dtype)
+def test_chunk_state_varlen(nseq, H, P, N, G, Q, states_dtype, empty):
+    announce("chunk_state_varlen", nseq, H, P, N, G, Q, states_dtype, empty)
     rng = np.random.default_rng(nseq * 7 + N)
     lens = rng.integers(1, 3 * Q, nseq)
     lens[0] = Q                                  # one ending exactly on a chunk edge
+    if empty:
+        lens[2] = 0                              # zero state
     total = int(lens.sum())
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     d = _inputs(1, total, H, G, P, N, Q, "bf16", seed=nseq)
