@@ -28,7 +28,7 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
     rest /= G;
     const int c = rest % nc;
     const int bi = rest / nc;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int r0 = rb * 64 + w * 16;
     if (r0 >= Q) return;
     const int ln = lane & 15, kg = lane >> 4;

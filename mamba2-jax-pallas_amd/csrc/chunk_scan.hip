@@ -135,7 +135,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
     }
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int ln = lane & 15, kg = lane >> 4;
     const T* Cbase = reinterpret_cast<const T*>(a.C) + (tok0 * a.G + g) * N;
     const TCB* cbbase = reinterpret_cast<const TCB*>(a.cb) +

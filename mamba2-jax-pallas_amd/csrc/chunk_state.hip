@@ -123,7 +123,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
         wq[q] = v;
     }
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int ln = lane & 15, kg = lane >> 4;
     const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;   // token of position 0
     const int valid = min(Q, L - c * Q);

@@ -86,6 +86,11 @@ M2_DEV float load_frag(const float* p) { return *p; }
 
 M2_DEV f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
+// Index of the calling wavefront in its workgroup, as a scalar: branches and
+// selects on it (or on values derived from it) stay scalar instead of being
+// treated as divergent per lane.
+M2_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() is a
 // workgroup release/acquire fence and waits for every outstanding global load
 // and store (vmcnt(0)); barriers that only hand LDS tiles between wavefronts

@@ -127,7 +127,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     const int g = work % G;
     const int rest = work / G;
     const int ci = rest % nc, bi = rest / nc;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int ln = lane & 15, kg = lane >> 4;
     const int pi = w % NPAIRS, ph = w / NPAIRS;
     const int kh = ph & 1, pp = ph >> 1;                  // work half, head-dim part
@@ -346,10 +346,13 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                     whi[i] = hv;
                     wlo[i] = (bf16)(v - (float)hv);
                 }
+                // one K = 32 MFMA: k index i < 4 pairs x with the hi part,
+                // 4 + i the same x with the lo part
+                const bf16x8 w8 = __builtin_shufflevector(whi, wlo, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int pt = 0; pt < PTW; ++pt) {
-                    acc[tt][pt] = mma16(xfr[pt], whi, acc[tt][pt]);
-                    acc[tt][pt] = mma16(xfr[pt], wlo, acc[tt][pt]);
+                    const bf16x8 x8 = __builtin_shufflevector(xfr[pt], xfr[pt], 0, 1, 2, 3, 0, 1, 2, 3);
+                    acc[tt][pt] = mma32(x8, w8, acc[tt][pt]);
                 }
             }
         }

@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
     const int g = h / (a.H / a.G);
     const int L = a.L, Q = a.Q, nc = a.nc, N = a.N, H = a.H;
     const int SPC = Q / KB, S = nc * SPC;
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int ln = lane & 15, kg = lane >> 4;
     const int pw = w & 3, kh = w >> 2;          // row tile, position half
 

@@ -66,7 +66,7 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     const int sh = work / a.nblk;
     const int h = sh % H, s = sh / H;
     const int g = h / (H / a.G);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = wave_id();
     const int ln = lane & 15, kg = lane >> 4;
     float* op = a.out + (((int64_t)s * H + h) * P) * N + NB * nb;
 
