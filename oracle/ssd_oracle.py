@@ -149,8 +149,14 @@ def _chunk_end_seq(seq_idx, nc, chunk_size):
 # 2. chunk_state  (ssd_naive.py:77-128; seq_idx: chunk_state_fwd.py:245-269)
 # ---------------------------------------------------------------------------
 
-def chunk_state(B, x, dt, dA_cumsum, seq_idx=None, acc=np.float64):
-    """states[b,c,h,p,n] = sum_l exp(dA[-1]-dA[l]) * dt[l] * x[l,p] * B[l,n]."""
+def chunk_state(B, x, dt, dA_cumsum, seq_idx=None, decay_clamp=False, acc=np.float64):
+    """states[b,c,h,p,n] = sum_l exp(dA[-1]-dA[l]) * dt[l] * x[l,p] * B[l,n].
+
+    ``decay_clamp`` clamps the exponent at 0 as the reference's chunk_state
+    kernel does (kernels/chunk_state_fwd.py:251); its naive path
+    (ops/ssd_naive.py:113-115) does not.  The two differ only where dA_cumsum
+    increases within a chunk (dt' * A > 0 somewhere).
+    """
     x = np.asarray(x, dtype=acc)
     B = np.asarray(B, dtype=acc)
     dt = np.asarray(dt, dtype=acc)
@@ -163,7 +169,8 @@ def chunk_state(B, x, dt, dA_cumsum, seq_idx=None, acc=np.float64):
     if L < T:
         x = np.pad(x, ((0, 0), (0, T - L), (0, 0), (0, 0)))
         B = np.pad(B, ((0, 0), (0, T - L), (0, 0), (0, 0)))
-    decay = np.exp(dA_cumsum[:, :, :, -1:] - dA_cumsum)          # (b,H,nc,Q)
+    expo = dA_cumsum[:, :, :, -1:] - dA_cumsum
+    decay = np.exp(np.minimum(expo, 0.0) if decay_clamp else expo)   # (b,H,nc,Q)
     w = decay * dt
     if seq_idx is not None:
         last = _chunk_end_seq(seq_idx, nc, Q)                      # (b,nc)
@@ -368,12 +375,12 @@ def ssd_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
                  initial_states=None, seq_idx=None, cu_seqlens=None,
                  dt_softplus=False, dt_limit=(0.0, INF),
                  return_final_states=False, return_varlen_states=False,
-                 io_dtype="f32", pad="kernel", acc=np.float64):
+                 io_dtype="f32", pad="kernel", decay_clamp=False, acc=np.float64):
     """The five-stage SSD forward with the reference's return arity.
 
     ``io_dtype`` names the dtype of x/B/C ('f32' or 'bf16'); the inputs must
     already hold values of that dtype.  It selects the rounding applied where
-    the reference casts to C.dtype.
+    the reference casts to C.dtype.  ``decay_clamp``: see chunk_state.
     """
     rf = round_fn_for(io_dtype)
     b, L, H, P = np.shape(x)
@@ -382,7 +389,7 @@ def ssd_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
         cu_seqlens = None
     dA, dto = chunk_cumsum(dt, A, chunk_size, dt_bias, dt_softplus, dt_limit,
                            pad=pad, acc=acc)
-    st = chunk_state(B, x, dto, dA, seq_idx=seq_idx, acc=acc)
+    st = chunk_state(B, x, dto, dA, seq_idx=seq_idx, decay_clamp=decay_clamp, acc=acc)
     nc = st.shape[1]
     init = None if initial_states is None else np.asarray(
         initial_states, dtype=acc).reshape(b, H, P * N)

@@ -50,6 +50,34 @@ def _run_and_check(cfg, with_z=False, varlen=False, Dhp=False):
     assert got[0].dtype == torch.float32 and got[1].dtype == torch.float32
 
 
+@pytest.mark.parametrize("Q", [64, 128])
+def test_increasing_decay(Q):
+    """dt' of both signs (no softplus, dt_limit below 0), so dA_cumsum rises and
+    falls within chunks: the fused scan takes its direct-weight path.  The
+    chunk-state decay is clamped at 0 as in the reference's chunk_state kernel
+    (kernels/chunk_state_fwd.py:251); the scan decay is not
+    (kernels/chunk_scan_fwd.py:329, ops/ssd_naive.py:260-268)."""
+    announce("increasing decay, Q", Q)
+    cfg = dataclasses.replace(configs.CONFIGS["c2"], seqlen=512, nheads=16, ngroups=2)
+    d = configs.make_ssd_inputs(cfg)
+    # mostly positive steps with some negative ones: dA still rises within
+    # chunks, while exp(dA) stays near 1 (a rising dA would amplify the bf16
+    # rounding of C h_c, a rounding point of the reference, beyond the
+    # tolerance)
+    rng = np.random.default_rng(21)
+    sign = np.where(rng.random(d["dt"].shape) < 0.15, -1.0, 1.0)
+    d["dt"] = O.bf16_round(0.05 * np.abs(rng.standard_normal(d["dt"].shape)) * sign).astype(np.float32)
+    d["dt_bias"] = None
+    kw = dict(chunk_size=Q, dt_softplus=False, dt_limit=(-1.0, float("inf")),
+              return_final_states=True)
+    got = mamba_chunk_scan_combined_fwd(**_dev_inputs(d, cfg.dtype), **kw)
+    want = O.ssd_combined(io_dtype=cfg.dtype, decay_clamp=True, **d, **kw)
+    dA, _ = O.chunk_cumsum(d["dt"], d["A"], Q, None, False, (-1.0, float("inf")))
+    assert np.any(np.diff(dA, axis=-1) > 0) and np.any(np.diff(dA, axis=-1) < 0)
+    check(got[0], want[0], TOL[cfg.dtype], "out")
+    check(got[1], want[1], TOL[cfg.dtype], "final_states")
+
+
 def test_c0_full_fp32():
     announce("c0 full")
     _run_and_check(configs.CONFIGS["c0"])

@@ -146,6 +146,29 @@ def test_chunk_state_brute_force(seq):
     np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
 
 
+def test_chunk_state_decay_clamp():
+    """decay_clamp (the reference kernel's min(., 0)) only matters where dA
+    increases: identical for a non-increasing dA; for Q = 2 with dt' A > 0 at
+    the second position the first weight is dt'_0 (clamped) instead of
+    exp(A dt'_1) dt'_0."""
+    rng = np.random.default_rng(14)
+    d = _rand_inputs(rng, 1, 16, 2, 1, 3, 4)
+    dA, dto = O.chunk_cumsum(d["dt"], d["A"], 8, d["dt_bias"], True)
+    assert np.all(np.diff(dA, axis=-1) <= 0)
+    np.testing.assert_array_equal(O.chunk_state(d["B"], d["x"], dto, dA, decay_clamp=True),
+                                  O.chunk_state(d["B"], d["x"], dto, dA))
+    x = rng.standard_normal((1, 2, 1, 3))
+    B = rng.standard_normal((1, 2, 1, 4))
+    A, d0, d1 = 0.7, 0.3, 0.5
+    dA2, dt2 = O.chunk_cumsum(np.array([[[d0], [d1]]]), np.array([A]), 2)
+    term0 = d0 * np.outer(x[0, 0, 0], B[0, 0, 0])
+    term1 = d1 * np.outer(x[0, 1, 0], B[0, 1, 0])
+    np.testing.assert_allclose(O.chunk_state(B, x, dt2, dA2, decay_clamp=True)[0, 0, 0],
+                               term0 + term1, rtol=1e-13)
+    np.testing.assert_allclose(O.chunk_state(B, x, dt2, dA2)[0, 0, 0],
+                               math.exp(A * d1) * term0 + term1, rtol=1e-13)
+
+
 def test_chunk_state_q1_closed_form():
     rng = np.random.default_rng(5)
     d = _rand_inputs(rng, 1, 6, 2, 1, 3, 4)
