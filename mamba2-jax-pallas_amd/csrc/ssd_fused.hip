@@ -11,8 +11,10 @@
 // output tiles are paired (t, Q/16-1-t) so that every pair carries the same
 // causal (triangular) work; the wavefronts of a pair split that work in two
 // halves of (row tile, k-tile) units, the first accumulating the long tile's
-// first KA k-tiles, the second the rest of it (a partial, summed through LDS)
-// and the short tile, and (for Q = 64) the head dim in PPARTS parts.
+// first KA k-tiles and its diagonal tile, the second the rest of it (a
+// partial, summed through LDS) and the short tile (each half one of the two
+// diagonal tiles, the dearer units), and (for Q = 64) the head dim in PPARTS
+// parts.
 //
 // Per head, the x rows [Q x 64], the carried state [64 x N], dA / dt of the
 // chunk and D are brought into a ring of R LDS slots by direct
@@ -107,10 +109,10 @@ template <int NS, int QT, bool HASZ>
 struct Shape {
     static constexpr int N = 32 * NS, Q = 16 * QT;
     // wavefronts per row-tile pair: two halves of the pair's causal work (the
-    // k-tiles of the long row tile up to KA, and the rest) times PPARTS parts
-    // of the head dim with PTW 16-column tiles each
+    // long row tile's first KA k-tiles and diagonal, and the rest) times
+    // PPARTS parts of the head dim with PTW 16-column tiles each
     static constexpr int NPAIRS = QT / 2, WPP = NWAVES / NPAIRS, PPARTS = WPP / 2, PTW = 4 / PPARTS;
-    static constexpr int KA = QT / 2 + 1;
+    static constexpr int KA = QT / 2;                       // <= the long tile t2
     static constexpr int SCPR = N / 8;                      // 16-byte chunks per state row
     static constexpr int XB = Q * P * 2, SB = P * N * 2, ZB = 0;
     static constexpr int AUXB = 2 * Q * 4 + 64 * 4;         // dA, dt, D
@@ -121,7 +123,11 @@ struct Shape {
     static constexpr int FTAB = NWAVES * 8 * 16 * 4;            // decay factor tables
     static constexpr int FIXED = CBL + XCHG + FTAB + Q * 4 + 256;
     static constexpr int ring_bytes(int r) { return r * SLOT > SLOT + BT ? r * SLOT : SLOT + BT; }
-    static constexpr int R = ring_bytes(3) + FIXED <= LDS_BYTES ? 3 : 2;
+    // output staging: each compute wavefront's finished 16 x 16 PTW fp32 tile,
+    // stored to HBM by the load wavefronts (when it fits beside the ring)
+    static constexpr int STW = 16 * 16 * PTW * 4, STG = NWAVES * STW;
+    static constexpr bool STAGE = ring_bytes(2) + FIXED + STG <= LDS_BYTES;
+    static constexpr int R = ring_bytes(3) + FIXED + (STAGE ? STG : 0) <= LDS_BYTES ? 3 : 2;
     static constexpr int RING = ring_bytes(R);
     // 1 KB direct loads of the load wavefront per head / for the B rows
     static constexpr int XI = XB / 1024, SI = SB / 1024, ZI = ZB / 1024, BI = BT / 1024;
@@ -130,7 +136,7 @@ struct Shape {
     static constexpr int WAIT01 = (R - 2) * (XL + SL + 1), WAIT23 = (R - 2) * (XL + SL);
     static_assert(XI % NLOAD == 0 && SI % NLOAD == 0 && BI % NLOAD == 0, "even load split");
     static_assert(NPAIRS * WPP == NWAVES && PPARTS * PTW == 4 && PPARTS >= 1, "wavefront split");
-    static_assert(ring_bytes(R) + FIXED <= LDS_BYTES, "LDS budget");
+    static_assert(ring_bytes(R) + FIXED + (STAGE ? STG : 0) <= LDS_BYTES, "LDS budget");
     static_assert(WAIT01 <= 63, "vmcnt range");
 };
 
@@ -143,6 +149,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     __shared__ __align__(16) bf16x4 cbl[NPAIRS][QT + 1][64];
     __shared__ __align__(16) f32x4 xchg[NPAIRS][4][64];
     __shared__ __align__(16) float ftab[NWAVES][8 * 16];   // decay factors of each wavefront's units
+    __shared__ __align__(16) char stg[S::STAGE ? S::STG : 16];  // output tiles on their way to HBM
     __shared__ int seqs[Q];
 
     const int L = a.L, H = a.H, G = a.G, nc = a.nc, hpg = a.hpg;
@@ -265,23 +272,52 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
         fmask[tt] = (a.seq_idx && seqs[m] != seq_prev) ? 0.f : 1.f;
     }
 
+    // the output tiles of head j (staged by the compute wavefronts) to HBM:
+    // load wavefront li stores those of compute wavefronts li and li + 4, one
+    // 16-byte chunk per lane, 16 PTW (4 PTW with PTW 16 KB rows) per store
+    auto store_staged = [&](int j) {
+        const int h = g * hpg + j;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int cw = li + 4 * half;                   // compute wavefront
+            const int cph = cw / NPAIRS, ckh = cph & 1, cpp = cph >> 1, cpi = cw % NPAIRS;
+            const int ct = ckh ? cpi : QT - 1 - cpi;        // its row tile
+#pragma unroll
+            for (int it = 0; it < PTW; ++it) {
+                const int o = 1024 * it + 16 * lane;
+                const int row = o / (64 * PTW), c = ((o % (64 * PTW)) / 16) ^ (row & (4 * PTW - 1));
+                const float4 v = *reinterpret_cast<const float4*>(stg + cw * S::STW + o);
+                const int m = 16 * ct + row;
+                if (m < valid)
+                    *reinterpret_cast<float4*>(a.out + ((tok0 + m) * H + h) * P + 16 * PTW * cpp + 4 * c) = v;
+            }
+        }
+    };
     if (loader) {
 #pragma unroll
         for (int i = 1; i < R - 1; ++i) issue(min(i, hpg - 1), i);
         for (int j = 0; j < hpg; ++j) {
-            // head j's loads done (R - 2 later heads may still be in flight)
+            // head j's loads done (R - 2 later heads may still be in flight;
+            // the output stores issued in between only make the wait longer)
             if (li < 2) wait_vmem<S::WAIT01>();
             else wait_vmem<S::WAIT23>();
-            lds_barrier();                                  // slot j % R complete, slot (j-1) % R free
+            lds_barrier();                                  // slot j % R complete, slot (j-1) % R free,
+                                                            // head j-1's outputs staged
+            if (S::STAGE && j > 0) store_staged(j - 1);
             issue(min(j + R - 1, hpg - 1), (j + R - 1) % R);
             lds_barrier();                                  // the compute wavefronts' exchange
+        }
+        if (S::STAGE) {
+            lds_barrier();                                  // the last head's outputs staged
+            store_staged(hpg - 1);
         }
         wait_vmem<0>();     // the tail heads re-loaded into unused slots
         return;
     }
     // this wavefront's row tiles: the first half (kh == 0) accumulates the
-    // long tile t2 over k-tiles [0, KA); the second half t2 over [KA, t2] (a
-    // partial, added in through LDS) and the short tile t1 over [0, t1]
+    // long tile t2 over k-tiles [0, KA) and t2; the second half t2 over
+    // [KA, t2) (a partial, added in through LDS) and the short tile t1 over
+    // [0, t1]
     constexpr int KA = S::KA;
     const int tmine = kh ? t1 : t2;                    // the tile this wavefront stores
     // x^T fragment reads: lane (ln, kg) of a 16-lane group reads row
@@ -382,8 +418,9 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
 
         // 1. intra chunk: y^T += x^T W^T over this wavefront's (tile, k-tile)
         // units: the first half (kh == 0) the long tile t2 over k-tiles
-        // [0, KA), the second half t2 over [KA, t2] (a partial, added in
-        // through LDS) and the short tile t1 over [0, t1].
+        // [0, KA) and its diagonal k-tile t2, the second half t2 over
+        // [KA, t2) (a partial, added in through LDS) and the short tile t1
+        // over [0, t1].
         // When dA does not increase over the chunk (dt >= 0, A <= 0: every
         // Mamba2 layer) the off-diagonal k-tiles (kt < t) of row tile t factor
         // through its first row r = 16 t:
@@ -397,7 +434,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
         if (__all(mono)) {
             // units: tile t2 over k-tiles [lo2, hi2) -> table slots kt - lo2,
             // tile t1 over [0, hi1) -> slots 4 + kt
-            const int lo2 = kh ? KA : 0, hi2 = kh ? t2 : min(KA, t2), hi1 = kh ? t1 : 0;
+            const int lo2 = kh ? KA : 0, hi2 = kh ? t2 : KA, hi1 = kh ? t1 : 0;
             float* ft = ftab[w];
 #pragma unroll
             for (int pass = 0; pass < 2; ++pass) {
@@ -447,12 +484,12 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                     acc[0][pt][i] *= e1;
                     acc[1][pt][i] *= e2;
                 }
-            if (kh ? t2 >= KA : t2 < KA) direct(T2c, t2);
             if (kh) direct(T1c, t1);
+            else direct(T2c, t2);
         } else {
             for (int kt = 0; kt <= t2; ++kt) {
                 if (kh && kt <= t1) direct(T1c, kt);
-                if (kh ? kt >= KA : kt < KA) direct(T2c, kt);
+                if (kh ? kt >= KA && kt < t2 : kt < KA || kt == t2) direct(T2c, kt);
             }
         }
 
@@ -484,6 +521,29 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                     for (int i = 0; i < 4; ++i) acc[1][pt][i] += rbf(ci_[pt][i]) * f;
             }
         }
+        // 3. + D x for the stored tile
+        if (a.D) {
+#pragma unroll
+            for (int pt = 0; pt < PTW; ++pt) {
+                const int p0 = 16 * (PTW * pp + pt) + 4 * kg;
+                const int xoff = mrow * 128 + (((p0 >> 3) ^ xswz(mrow)) * 16) + 2 * (p0 & 7);
+                const bf16x4 xv = *reinterpret_cast<const bf16x4*>(slot + xoff);
+                float dv[4];
+                if (a.D_has_hdim) {
+                    const float4 d4 = *reinterpret_cast<const float4*>(Ds + p0);
+                    dv[0] = d4.x; dv[1] = d4.y; dv[2] = d4.z; dv[3] = d4.w;
+                } else {
+                    dv[0] = dv[1] = dv[2] = dv[3] = Ds[0];
+                }
+                if (kh) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[0][pt][i] += dv[i] * (float)xv[i];
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[1][pt][i] += dv[i] * (float)xv[i];
+                }
+            }
+        }
         // the second half's part of tile t2 joins the first half's
         if (kh) {
 #pragma unroll
@@ -498,35 +558,29 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                 for (int i = 0; i < 4; ++i) acc[1][pt][i] += o[i];
             }
         }
-        // 3. epilogue: + D x, silu(z) gate in z's dtype, 16-byte fp32 stores
-        if (mrow < valid) {
-            float* op = a.out + ((tok0 + mrow) * H + h) * P;
+        // 4. epilogue: silu(z) gate in z's dtype; the tile goes to the staging
+        // area (stored by the load wavefronts) or straight to HBM
 #pragma unroll
-            for (int pt = 0; pt < PTW; ++pt) {
+        for (int pt = 0; pt < PTW; ++pt) {
+            const f32x4 r = kh ? acc[0][pt] : acc[1][pt];
+            float v[4] = {r[0], r[1], r[2], r[3]};
+            if (HASZ) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] *= rbf(silu_f((float)zr[pt][i]));
+            }
+            if (S::STAGE) {
+                // row ln, 16-byte chunk 4 pt + kg, XOR-swizzled by the row
+                const int c = (4 * pt + kg) ^ (ln & (4 * PTW - 1));
+                *reinterpret_cast<float4*>(stg + w * S::STW + ln * (64 * PTW) + 16 * c) =
+                    make_float4(v[0], v[1], v[2], v[3]);
+            } else if (mrow < valid) {
                 const int p0 = 16 * (PTW * pp + pt) + 4 * kg;
-                const f32x4 r = kh ? acc[0][pt] : acc[1][pt];
-                float v[4] = {r[0], r[1], r[2], r[3]};
-                if (a.D) {
-                    const int xoff = mrow * 128 + (((p0 >> 3) ^ xswz(mrow)) * 16) + 2 * (p0 & 7);
-                    const bf16x4 xv = *reinterpret_cast<const bf16x4*>(slot + xoff);
-                    float dv[4];
-                    if (a.D_has_hdim) {
-                        const float4 d4 = *reinterpret_cast<const float4*>(Ds + p0);
-                        dv[0] = d4.x; dv[1] = d4.y; dv[2] = d4.z; dv[3] = d4.w;
-                    } else {
-                        dv[0] = dv[1] = dv[2] = dv[3] = Ds[0];
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) v[i] += dv[i] * (float)xv[i];
-                }
-                if (HASZ) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) v[i] *= rbf(silu_f((float)zr[pt][i]));
-                }
-                *reinterpret_cast<float4*>(op + p0) = make_float4(v[0], v[1], v[2], v[3]);
+                *reinterpret_cast<float4*>(a.out + ((tok0 + mrow) * H + h) * P + p0) =
+                    make_float4(v[0], v[1], v[2], v[3]);
             }
         }
     }
+    if (S::STAGE) lds_barrier();                       // the last head's outputs staged
 }
 
 }  // namespace
