@@ -164,8 +164,9 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
             if (li < 2) wait_vmem<C::WAIT01>();
             else wait_vmem<C::WAIT23>();
             lds_barrier();               // slot s % DEPTH complete, slot (s-1) % DEPTH free
+            if (s % SPC == 0) lds_barrier();   // the compute wavefronts' exchange (before
+                                               // the issue, which would hold it up)
             issue(min(s + DEPTH - 1, S - 1), (s + DEPTH - 1) % DEPTH);
-            if (s % SPC == 0) lds_barrier();   // the compute wavefronts' exchange
         }
         wait_vmem<0>();                  // the tail stages re-loaded into unused slots
         __syncthreads();                 // the final exchange
