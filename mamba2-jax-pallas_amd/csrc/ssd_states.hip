@@ -20,7 +20,10 @@
 // dstate columns of the block (four 16 x 16 tiles) and the positions
 // (KB/2) (w >> 2) .. +KB/2-1 of every stage: the two halves accumulate
 // separate partial states (the recurrence is linear), which are summed
-// through LDS only where the state is written (chunk starts and the end).
+// through LDS only where the state is written (chunk starts and the end):
+// the second half leaves its part in a chunk-parity double buffer at the end
+// of a chunk, and the stage barrier that follows also hands it over, so the
+// exchange costs no barrier of its own.  Each stage has one barrier.
 // The load wavefronts fill the slots with direct global -> LDS loads
 // (global_load_lds_dwordx4), DEPTH - 1 stages ahead of use, and wait for them
 // with explicit vmcnt waits: no load result passes through VGPRs, so nothing
@@ -56,7 +59,7 @@ constexpr int CPR = 8;       // 16-byte chunks per 128-byte tile row
 // takes KB/2 positions (KS MFMA K steps of 32).
 template <int KB>
 struct StCfg {
-    static constexpr int DEPTH = KB == 64 ? 6 : 4;   // LDS stage slots: DEPTH - 1 in flight
+    static constexpr int DEPTH = KB == 64 ? 6 : 3;   // LDS stage slots: DEPTH - 1 in flight
     static constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
     static constexpr int AUXB = KB * 4 + 256;        // weights, 64 copies of the decay
     static constexpr int SLOT = XB + BB + AUXB;
@@ -91,7 +94,10 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
     typedef StCfg<KB> C;
     constexpr int DEPTH = C::DEPTH, XB = C::XB, BB = C::BB, SLOT = C::SLOT, TL = C::TL;
     __shared__ __align__(16) char ring[DEPTH * SLOT];
-    __shared__ __align__(16) f32x4 xchg[4][4][64];   // partial states of the second half
+    // partial states of the second half at chunk starts, double-buffered by
+    // chunk parity: written at the end of a chunk, read after the next stage's
+    // barrier, and not written again before the barrier after that
+    __shared__ __align__(16) f32x4 xchg[2][4][4][64];
     // bf16 state rows of each first-half wavefront on their way to HBM: rows
     // of 64 columns + 8 pad (144 bytes), 16 per wavefront
     __shared__ __align__(16) bf16 pst[4][16][72];
@@ -164,8 +170,6 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
             if (li < 2) wait_vmem<C::WAIT01>();
             else wait_vmem<C::WAIT23>();
             lds_barrier();               // slot s % DEPTH complete, slot (s-1) % DEPTH free
-            if (s % SPC == 0) lds_barrier();   // the compute wavefronts' exchange (before
-                                               // the issue, which would hold it up)
             issue(min(s + DEPTH - 1, S - 1), (s + DEPTH - 1) % DEPTH);
         }
         wait_vmem<0>();                  // the tail stages re-loaded into unused slots
@@ -187,20 +191,20 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
         bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
     }
+    if (kh == 1) {                                   // its part of h_0: zero
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xchg[0][pw][j][lane] = acc[j];
+    }
     for (int s = 0; s < S; ++s) {
         const int k = s % DEPTH;
         const int c = s / SPC, kb = s - c * SPC;
-        lds_barrier();                               // slot k complete (load wavefront)
+        lds_barrier();                               // slot k complete (load wavefront),
+                                                     // at chunk starts the second half's part
         const char* slot = ring + k * SLOT;
         const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
         if (kb == 0) {
             // h_c (sum of the halves) is the state entering chunk c; then both
             // halves h <- scl[c] h
-            if (kh == 1) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) xchg[pw][j][lane] = acc[j];
-            }
-            lds_barrier();
             if (kh == 0) {
                 // round the summed state to bf16, then store whole 128-byte rows:
                 // lane (ln, kg) writes 4 columns of row ln, then reads back 16
@@ -208,7 +212,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
                 bf16* pr = &pst[pw][0][0];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const f32x4 o2 = xchg[pw][j][lane];
+                    const f32x4 o2 = xchg[c & 1][pw][j][lane];
                     const bf16x4 o = {(bf16)(acc[j][0] + o2[0]), (bf16)(acc[j][1] + o2[1]),
                                       (bf16)(acc[j][2] + o2[2]), (bf16)(acc[j][3] + o2[3])};
                     *reinterpret_cast<bf16x4*>(pr + ln * 72 + 16 * j + 4 * kg) = o;
@@ -256,17 +260,17 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
             }
         }
-    }
-    if (kh == 1) {
+        if (kh == 1 && (s + 1) % SPC == 0) {         // the end of chunk c: its part of h_{c+1}
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xchg[pw][j][lane] = acc[j];
+            for (int j = 0; j < 4; ++j) xchg[(c + 1) & 1][pw][j][lane] = acc[j];
+        }
     }
     __syncthreads();
     if (a.fin && kh == 0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int n = NB * nb + 16 * j + 4 * kg;
-            const f32x4 o2 = xchg[pw][j][lane];
+            const f32x4 o2 = xchg[nc & 1][pw][j][lane];
             *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n) =
                 make_float4(acc[j][0] + o2[0], acc[j][1] + o2[1], acc[j][2] + o2[2], acc[j][3] + o2[3]);
         }
