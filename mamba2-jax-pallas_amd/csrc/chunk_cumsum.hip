@@ -6,10 +6,11 @@
 //           previous chunk's (the previous id of chunk 0 is 0)
 // which are the chunk_state scale and the state_passing decay.
 //
-// One workgroup per (batch, chunk, block of 32 heads), 512 threads: lane
-// h = thread & 31 is a head, thread >> 5 one of 16 position segments of the
-// chunk.  Each thread loads its segment's dt (coalesced across the 32 heads),
-// processes it and sums it sequentially in registers; segment totals meet in
+// One workgroup per (batch, chunk, block of 16 heads), 256 threads: thread
+// & 15 is a head, thread >> 4 one of 16 position segments of the chunk.  Each
+// thread loads its segment's dt (coalesced across the 16 heads: dt is
+// [b, L, H], so one head's positions are H elements apart), processes it
+// and sums it sequentially in registers; segment totals meet in
 // LDS and each thread adds the totals of the segments before it.  Outputs are
 // transposed through LDS so that each row [b, h, c, :] is written by
 // consecutive lanes.
@@ -22,7 +23,7 @@
 
 namespace {
 
-constexpr int HB = 32;                 // heads per workgroup
+constexpr int HB = 16;                 // heads per workgroup (256 workgroups at H 128, 32 chunks)
 constexpr int NSEG = 16;               // position segments per chunk
 constexpr int THREADS = HB * NSEG;
 constexpr int QMAX = 256;

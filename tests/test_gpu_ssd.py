@@ -78,6 +78,23 @@ def test_increasing_decay(Q):
     check(got[1], want[1], TOL[cfg.dtype], "final_states")
 
 
+@pytest.mark.parametrize("H,G,Q,dt_f32", [(5, 1, 128, False), (6, 2, 64, True), (3, 3, 128, True)])
+def test_odd_heads_fp32_dt(H, G, Q, dt_f32):
+    """Head counts with odd (t H + h) parity (the bf16 dt word read in halves)
+    and fp32 dt beside bf16 x / B / C; L % Q != 0."""
+    announce("odd heads / fp32 dt", H, G, Q, dt_f32)
+    cfg = dataclasses.replace(configs.CONFIGS["c2"], seqlen=333, nheads=H, ngroups=G, chunk_size=Q)
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, cfg.dtype)
+    if dt_f32:
+        t["dt"] = dev(d["dt"])
+    kw = dict(chunk_size=Q, dt_softplus=True, return_final_states=True)
+    got = mamba_chunk_scan_combined_fwd(**t, **kw)
+    want = O.ssd_combined(io_dtype=cfg.dtype, **d, **kw)
+    check(got[0], want[0], TOL[cfg.dtype], "out")
+    check(got[1], want[1], TOL[cfg.dtype], "final_states")
+
+
 def test_c0_full_fp32():
     announce("c0 full")
     _run_and_check(configs.CONFIGS["c0"])
