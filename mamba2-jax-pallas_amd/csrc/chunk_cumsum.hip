@@ -38,7 +38,7 @@ struct CumsumArgs {
     float* dto;
     float* wts;               // [b, H, nc, Q] or NULL
     float* scl;               // [b, H, nc] or NULL
-    int L, H, Q, nc, softplus;
+    int L, H, Q, nc, softplus, nhb, nblocks;
     float lo, hi;
 };
 
@@ -50,8 +50,12 @@ template <typename TD, int QS, bool VEC>
 __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
     __shared__ float tot[NSEG][HB];
     __shared__ __align__(16) float tile[3][HB][TS];
+    // the head blocks of one (batch, chunk) read the same dt rows: they share
+    // an XCD (and its L2)
+    const int work = xcd_remap(blockIdx.x, a.nblocks);
+    const int hb = work % a.nhb, c = (work / a.nhb) % a.nc, bi = work / (a.nhb * a.nc);
     const int hh = threadIdx.x % HB, seg = threadIdx.x / HB;
-    const int h = blockIdx.x * HB + hh, c = blockIdx.y, bi = blockIdx.z;
+    const int h = hb * HB + hh;
     const bool hok = h < a.H;
     const int Q = a.Q, L = a.L;
     const int qs = (Q + NSEG - 1) / NSEG;
@@ -118,8 +122,8 @@ __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
     }
     __syncthreads();
     float* outs[3] = {a.dA, a.dto, a.wts};
-    const int nh = min(HB, a.H - (int)blockIdx.x * HB);
-    const int64_t row0 = (((int64_t)bi * a.H + blockIdx.x * HB) * a.nc + c) * Q;
+    const int nh = min(HB, a.H - (int)hb * HB);
+    const int64_t row0 = (((int64_t)bi * a.H + hb * HB) * a.nc + c) * Q;
     const int64_t hstride = (int64_t)a.nc * Q;       // between heads' rows
     if (VEC) {
         const int q4n = Q / 4;
@@ -160,7 +164,11 @@ int launch_chunk_cumsum_ex(const m2_chunk_cumsum_args& a, const int32_t* seq_idx
     k.L = (int)a.seqlen; k.H = (int)a.nheads; k.Q = (int)a.chunk_size;
     k.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
     k.softplus = a.dt_softplus; k.lo = a.dt_min; k.hi = a.dt_max;
-    dim3 grid((unsigned)((a.nheads + HB - 1) / HB), (unsigned)k.nc, (unsigned)a.batch);
+    k.nhb = (int)((a.nheads + HB - 1) / HB);
+    const int64_t nblocks = (int64_t)k.nhb * k.nc * a.batch;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_cumsum: too many blocks");
+    k.nblocks = (int)nblocks;
+    const dim3 grid((unsigned)nblocks);
     if (a.dt_dtype != M2_F32 && a.dt_dtype != M2_BF16)
         return set_error(M2_ERR_UNSUPPORTED, "chunk_cumsum: dt dtype %d", a.dt_dtype);
     const int qs = (k.Q + NSEG - 1) / NSEG;
