@@ -97,25 +97,7 @@ M2_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); 
 // use this one so that prefetches and output stores stay in flight.
 M2_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Vector global stores the compiler does not track.  On gfx9-family targets
-// stores and loads share the vmcnt counter, and once both are pending the
-// compiler's wait insertion falls back to vmcnt(0) before the next use of any
-// load: a store inside a prefetch loop would drain every load in flight.
-// Loads still complete in issue order, so waits the compiler computes from
-// its own loads stay correct (they can only wait longer) with these stores
-// pending.
-M2_DEV void store_untracked(float* p, float v) {
-    asm volatile("global_store_dword %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
-M2_DEV void store_untracked(void* p, uint64_t v) {
-    asm volatile("global_store_dwordx2 %0, %1, off" ::"v"(p), "v"(v) : "memory");
-}
-// (a store of more than 8 bytes needs one wait state before a VALU may
-// overwrite its data registers; the compiler cannot see that inside asm)
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
-M2_DEV void store_untracked_x4(void* p, u32x4 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off\n\ts_nop 0" ::"v"(p), "v"(v) : "memory");
-}
 
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
@@ -136,12 +118,16 @@ M2_DEV bf16x4 ds_read_tr(const void* p) {
 // flight (the compiler would wait for those with too small a count).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+// The compiler cannot see that these read their address registers, so they
+// keep the two wait states it puts between a VALU write of an address (a
+// 64-bit add, say) and a global_load_lds reading it: the M0 write and an
+// s_nop.
 M2_DEV void dma16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                  ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
 }
 M2_DEV void dma4(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                  ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
 }
 #pragma clang diagnostic pop

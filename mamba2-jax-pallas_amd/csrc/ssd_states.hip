@@ -94,13 +94,16 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
     typedef StCfg<KB> C;
     constexpr int DEPTH = C::DEPTH, XB = C::XB, BB = C::BB, SLOT = C::SLOT, TL = C::TL;
     __shared__ __align__(16) char ring[DEPTH * SLOT];
-    // partial states of the second half at chunk starts, double-buffered by
-    // chunk parity: written at the end of a chunk, read after the next stage's
-    // barrier, and not written again before the barrier after that
-    __shared__ __align__(16) f32x4 xchg[2][4][4][64];
-    // bf16 state rows of each first-half wavefront on their way to HBM: rows
-    // of 64 columns + 8 pad (144 bytes), 16 per wavefront
-    __shared__ __align__(16) bf16 pst[4][16][72];
+    // partial states at chunk starts: the first half sums column tiles 0, 1,
+    // the second half 2, 3, each taking the other half's part of them from
+    // xchg[parity][the other's wavefront], double-buffered by chunk parity:
+    // written at the end of a chunk, read after the next stage's barrier, and
+    // not written again before the barrier after that
+    __shared__ __align__(16) f32x4 xchg[2][NWAVES][2][64];
+    // the bf16 states entering a chunk on their way to HBM (stored by the load
+    // wavefronts after the next barrier), double-buffered by chunk parity: per
+    // row tile 16 rows of 64 columns + 8 pad (144 bytes)
+    __shared__ __align__(16) bf16 pst[2][4][16][72];
 
     const int work = xcd_remap(blockIdx.x, a.nwork);
     const int nb = work % a.nblk;
@@ -163,6 +166,23 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         if (li == 1) dma4(a.scl + bhc + c, sb + XB + BB + KB * 4);
     };
     if (w >= NWAVES) {
+        // the bf16 state entering chunk c (pst[c & 1], complete one barrier after
+        // the chunk's first stage) to HBM: load wavefront li stores row tile li,
+        // whole 128-byte rows, two 16-byte pieces per lane.  These stores only
+        // make the vmcnt waits below longer (those count the loads issued after
+        // the awaited ones); they are ordinary stores, so the compiler keeps
+        // their address and data registers intact until the hardware has read
+        // them (two wait states after a 16-byte store on gfx950).
+        auto store_pst = [&](int c) {
+            const bf16* pr = &pst[c & 1][li][0][0];
+            bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + 16 * li) * N + NB * nb;
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int row = 8 * half + (lane >> 3), col = 8 * (lane & 7);
+                const u32x4 v = *reinterpret_cast<const u32x4*>(pr + row * 72 + col);
+                *reinterpret_cast<u32x4*>(pp + (int64_t)row * N + col) = v;
+            }
+        };
 #pragma unroll
         for (int i = 0; i < DEPTH - 1; ++i) issue(min(i, S - 1), i);
         for (int s = 0; s < S; ++s) {
@@ -171,9 +191,11 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
             else wait_vmem<C::WAIT23>();
             lds_barrier();               // slot s % DEPTH complete, slot (s-1) % DEPTH free
             issue(min(s + DEPTH - 1, S - 1), (s + DEPTH - 1) % DEPTH);
+            if (s > 0 && (s - 1) % SPC == 0) store_pst((s - 1) / SPC);
         }
         wait_vmem<0>();                  // the tail stages re-loaded into unused slots
         __syncthreads();                 // the final exchange
+        if (SPC == 1) store_pst(nc - 1);
         return;
     }
 
@@ -191,10 +213,23 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
         bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
     }
-    if (kh == 1) {                                   // its part of h_0: zero
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xchg[0][pw][j][lane] = acc[j];
-    }
+    // this wavefront's part of the tiles the other half sums; the sums of its
+    // own two tiles (columns 32 kh .. 32 kh + 31)
+    auto give = [&](int par) {
+        if (kh == 0) {
+            xchg[par][w][0][lane] = acc[2];
+            xchg[par][w][1][lane] = acc[3];
+        } else {
+            xchg[par][w][0][lane] = acc[0];
+            xchg[par][w][1][lane] = acc[1];
+        }
+    };
+    auto take = [&](int par, f32x4& s0, f32x4& s1) {
+        const f32x4 o0 = xchg[par][w ^ 4][0][lane], o1 = xchg[par][w ^ 4][1][lane];
+        s0 = (kh == 0 ? acc[0] : acc[2]) + o0;
+        s1 = (kh == 0 ? acc[1] : acc[3]) + o1;
+    };
+    give(0);                                         // the parts of h_0
     for (int s = 0; s < S; ++s) {
         const int k = s % DEPTH;
         const int c = s / SPC, kb = s - c * SPC;
@@ -205,25 +240,16 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         if (kb == 0) {
             // h_c (sum of the halves) is the state entering chunk c; then both
             // halves h <- scl[c] h
-            if (kh == 0) {
-                // round the summed state to bf16, then store whole 128-byte rows:
-                // lane (ln, kg) writes 4 columns of row ln, then reads back 16
-                // bytes (8 columns) of rows (lane >> 3) and 8 + (lane >> 3)
-                bf16* pr = &pst[pw][0][0];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f32x4 o2 = xchg[c & 1][pw][j][lane];
-                    const bf16x4 o = {(bf16)(acc[j][0] + o2[0]), (bf16)(acc[j][1] + o2[1]),
-                                      (bf16)(acc[j][2] + o2[2]), (bf16)(acc[j][3] + o2[3])};
-                    *reinterpret_cast<bf16x4*>(pr + ln * 72 + 16 * j + 4 * kg) = o;
-                }
-                bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + 16 * pw) * N + NB * nb;
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    const int row = 8 * half + (lane >> 3), col = 8 * (lane & 7);
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(pr + row * 72 + col);
-                    store_untracked_x4(pp + (int64_t)row * N + col, v);
-                }
+            {
+                // round this half's two summed tiles to bf16 into the staging
+                // rows (lane (ln, kg): 4 columns of row ln)
+                f32x4 s0, s1;
+                take(c & 1, s0, s1);
+                bf16* pr = &pst[c & 1][pw][ln][32 * kh + 4 * kg];
+                const bf16x4 o0 = {(bf16)s0[0], (bf16)s0[1], (bf16)s0[2], (bf16)s0[3]};
+                const bf16x4 o1 = {(bf16)s1[0], (bf16)s1[1], (bf16)s1[2], (bf16)s1[3]};
+                *reinterpret_cast<bf16x4*>(pr) = o0;
+                *reinterpret_cast<bf16x4*>(pr + 16) = o1;
             }
             const float sc = aux[KB];
 #pragma unroll
@@ -260,20 +286,15 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
             }
         }
-        if (kh == 1 && (s + 1) % SPC == 0) {         // the end of chunk c: its part of h_{c+1}
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xchg[(c + 1) & 1][pw][j][lane] = acc[j];
-        }
+        if ((s + 1) % SPC == 0) give((c + 1) & 1);  // the end of chunk c: parts of h_{c+1}
     }
     __syncthreads();
-    if (a.fin && kh == 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int n = NB * nb + 16 * j + 4 * kg;
-            const f32x4 o2 = xchg[nc & 1][pw][j][lane];
-            *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n) =
-                make_float4(acc[j][0] + o2[0], acc[j][1] + o2[1], acc[j][2] + o2[2], acc[j][3] + o2[3]);
-        }
+    if (a.fin) {
+        f32x4 s0, s1;
+        take(nc & 1, s0, s1);
+        const int n = NB * nb + 32 * kh + 4 * kg;
+        *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n) = make_float4(s0[0], s0[1], s0[2], s0[3]);
+        *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n + 16) = make_float4(s1[0], s1[1], s1[2], s1[3]);
     }
 }
 
