@@ -34,9 +34,22 @@ PEAK_MFMA_TFLOPS = {"bf16": 2500.0, "f32": 157.3}   # dense
 STAGES = ["chunk_cumsum", "chunk_state", "state_passing", "bmm_chunk", "chunk_scan"]
 
 
+def internal_chunk(cfg):
+    """The chunk size the combined path runs: bf16 chunks of 256 run as chunks of
+    128 when both fused kernels then apply (m2_ssd_combined's internal_args)."""
+    if cfg.dtype == "bf16" and cfg.chunk_size == 256:
+        import dataclasses
+        c = dataclasses.replace(cfg, chunk_size=128)
+        if states_is_fused(c) and scan_is_fused(c):
+            return 128
+    return cfg.chunk_size
+
+
 def stage_work(cfg, with_init=False, with_z=False):
     """Algorithmic (compulsory) HBM bytes and flops per launch of each stage, as
     the combined path runs them (CB and the carried states in the input dtype)."""
+    import dataclasses
+    cfg = dataclasses.replace(cfg, chunk_size=internal_chunk(cfg))
     s = 2 if cfg.dtype == "bf16" else 4
     b, L, H, G, P, N, Q = (cfg.batch, cfg.seqlen, cfg.nheads, cfg.ngroups, cfg.headdim,
                            cfg.dstate, cfg.chunk_size)
@@ -273,7 +286,9 @@ def main(argv=None):
     # launch stream at each kernel boundary; a fused kernel's time lands in the
     # first slot of its group (the other slots of the group are not recorded)
     hev = HipEvents()
-    fs, fc = states_is_fused(cfg), scan_is_fused(cfg)
+    import dataclasses
+    icfg = dataclasses.replace(cfg, chunk_size=internal_chunk(cfg))
+    fs, fc = states_is_fused(icfg), scan_is_fused(icfg)
     keep = [True, True, True, not fs, not fc, True]
     evs = [[hev.new() if k else None for k in keep] for _ in range(K)]
     for _ in range(3):
@@ -295,12 +310,12 @@ def main(argv=None):
     # event slots: cumsum, chunk_state, state_passing, bmm_chunk, chunk_scan
     slots = dict(zip(STAGES, slot_ms))
     stage_ms = {}
-    if states_is_fused(cfg):
+    if fs:
         stage_ms["chunk_cumsum"] = slots["chunk_cumsum"]
         stage_ms[FUSED_STATES] = slots["chunk_state"]
     else:
         stage_ms.update({k: slots[k] for k in STAGES[:3]})
-    if scan_is_fused(cfg):
+    if fc:
         stage_ms["bmm_chunk+chunk_scan"] = slots["chunk_scan"]
     else:
         stage_ms.update({k: slots[k] for k in STAGES[3:]})

@@ -172,6 +172,9 @@ int m2_chunk_state_varlen(const m2_chunk_state_varlen_args* a, void* stream);
  * bmm_chunk -> chunk_scan [-> varlen states]) on one stream, intermediates in
  * the caller's workspace (size from m2_ssd_combined_workspace_size).
  * states_passed is kept in x's dtype; out and the final states are float32.
+ * chunk_size is a tiling choice here as in the reference (the outputs are the
+ * same function of the inputs for every chunk size): bf16 chunks of 256 run
+ * as chunks of 128 when that keeps the whole layer on the fused kernels.
  * Replaces mamba_chunk_scan_combined_fwd (reference kernels/ssd_combined.py:46-203).
  * ------------------------------------------------------------------------- */
 typedef struct {

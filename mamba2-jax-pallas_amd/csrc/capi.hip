@@ -86,16 +86,31 @@ int record(void** ev, int i, hipStream_t s) {
     return M2_OK;
 }
 
+// The combined forward returns only y and the final (and varlen) states: the
+// same function of the inputs for every chunk size (the chunked algorithm is
+// exact; only the rounding points at chunk boundaries move).  bf16 chunks of
+// 256 run as chunks of 128 when that puts both halves of the layer on the
+// fused kernels (the fused scan keeps at most 128 positions of a chunk in LDS).
+m2_ssd_combined_args internal_args(const m2_ssd_combined_args& a0) {
+    m2_ssd_combined_args a = a0;
+    if (a0.dtype == M2_BF16 && a0.chunk_size == 256) {
+        a.chunk_size = 128;
+        if (!m2::states_fused_supported(a) || !m2::scan_fused_supported(a.headdim, a.dstate, 128))
+            a.chunk_size = 256;
+    }
+    return a;
+}
+
 }  // namespace
 
 extern "C" size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a) {
     if (!a || a->chunk_size <= 0 || !m2_dtype_size(a->dtype)) return 0;
-    return layout_of(*a).total;
+    return layout_of(internal_args(*a)).total;
 }
 
 extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
     if (!ap) return m2::set_error(M2_ERR_INVALID, "m2_ssd_combined: NULL args");
-    const m2_ssd_combined_args& a = *ap;
+    const m2_ssd_combined_args a = internal_args(*ap);
     hipStream_t s = (hipStream_t)stream_;
     M2_REQUIRE(a.chunk_size > 0 && a.batch > 0 && a.seqlen > 0, M2_ERR_INVALID,
                "m2_ssd_combined: batch, seqlen and chunk_size must be positive");

@@ -6,7 +6,8 @@
 // with CB = bf16(C B^T) (seq_idx-masked), h_c the bf16 state entering chunk c.
 //
 // One workgroup per (batch, chunk, group) covers every head of the group, so
-// CB is built once and used by all of them.  8 compute wavefronts (+ four that
+// CB is built once and used by all of them (or a slice of them, when fewer
+// than 256 (batch, chunk, group) items would leave CUs idle).  8 compute wavefronts (+ four that
 // only load, below); the chunk's 16-row
 // output tiles are paired (t, Q/16-1-t) so that every pair carries the same
 // causal (triangular) work; the wavefronts of a pair split that work in two
@@ -42,6 +43,7 @@
 //
 // Follows reference ops/ssd_naive.py:189-318 and kernels/chunk_scan_fwd.py
 // :294-322 / kernels/bmm_chunk_fwd.py:353-372 (seq_idx masks).
+#include <algorithm>
 #include <type_traits>
 
 #include "m2_internal.h"
@@ -103,6 +105,7 @@ struct ScanFusedArgs {
     float* out;
     int D_has_hdim;
     int L, H, G, nc, hpg, nwork;
+    int hps, nslice;          // heads per workgroup (a slice of the group's), slices
 };
 
 template <int NS, int QT, bool HASZ>
@@ -153,10 +156,15 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     __shared__ int seqs[Q];
 
     const int L = a.L, H = a.H, G = a.G, nc = a.nc, hpg = a.hpg;
+    // work = ((b nc + chunk) G + group) nslice + slice: the slices of a (chunk,
+    // group), which read the same B / C rows, share an XCD
     const int work = xcd_remap(blockIdx.x, a.nwork);
-    const int g = work % G;
-    const int rest = work / G;
+    const int sl = work % a.nslice;
+    const int g = (work / a.nslice) % G;
+    const int rest = work / (a.nslice * G);
     const int ci = rest % nc, bi = rest / nc;
+    const int h0 = g * hpg + sl * a.hps;                  // this workgroup's heads h0 + j, j < nh
+    const int nh = min(a.hps, hpg - sl * a.hps);
     const int lane = threadIdx.x & 63, w = wave_id();
     const int ln = lane & 15, kg = lane >> 4;
     const int pi = w % NPAIRS, ph = w / NPAIRS;
@@ -191,7 +199,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     const int64_t cq0 = ((int64_t)bi * H * nc + ci) * Q;  // dA / dt row of head 0 (+ h nc Q)
     const int64_t st0 = ((int64_t)bi * nc + ci) * H * P * N;
     auto issue = [&](int j, int k) {
-        const int h = g * hpg + j;
+        const int h = h0 + j;
         const uint32_t sb = ring_lds + k * SLOT;
 #pragma unroll
         for (int uu = 0; uu < S::XL; ++uu) {
@@ -276,7 +284,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     // load wavefront li stores those of compute wavefronts li and li + 4, one
     // 16-byte chunk per lane, 16 PTW (4 PTW with PTW 16 KB rows) per store
     auto store_staged = [&](int j) {
-        const int h = g * hpg + j;
+        const int h = h0 + j;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             const int cw = li + 4 * half;                   // compute wavefront
@@ -295,8 +303,8 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     };
     if (loader) {
 #pragma unroll
-        for (int i = 1; i < R - 1; ++i) issue(min(i, hpg - 1), i);
-        for (int j = 0; j < hpg; ++j) {
+        for (int i = 1; i < R - 1; ++i) issue(min(i, nh - 1), i);
+        for (int j = 0; j < nh; ++j) {
             // head j's loads done (R - 2 later heads may still be in flight;
             // the output stores issued in between only make the wait longer)
             if (li < 2) wait_vmem<S::WAIT01>();
@@ -304,12 +312,12 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
             lds_barrier();                                  // slot j % R complete, slot (j-1) % R free,
                                                             // head j-1's outputs staged
             if (S::STAGE && j > 0) store_staged(j - 1);
-            issue(min(j + R - 1, hpg - 1), (j + R - 1) % R);
+            issue(min(j + R - 1, nh - 1), (j + R - 1) % R);
             lds_barrier();                                  // the compute wavefronts' exchange
         }
         if (S::STAGE) {
             lds_barrier();                                  // the last head's outputs staged
-            store_staged(hpg - 1);
+            store_staged(nh - 1);
         }
         wait_vmem<0>();     // the tail heads re-loaded into unused slots
         return;
@@ -332,14 +340,14 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
             xo[pt] = r0 * 128 + ((ch ^ xswz(r0)) * 16) + 8 * (ln & 1);
         }
     }
-    for (int j = 0; j < hpg; ++j) {
+    for (int j = 0; j < nh; ++j) {
         const int k = j % R;
         lds_barrier();
         const char* slot = ring + k * SLOT;
         const float* dAs = reinterpret_cast<const float*>(slot + XB + SB + ZB);
         const float* dts = dAs + Q;
         const float* Ds = dAs + 2 * Q;
-        const int h = g * hpg + j;
+        const int h = h0 + j;
         const int mrow = 16 * tmine + ln;              // output row of this lane
         bf16x4 zr[PTW];
         if (HASZ) {
@@ -598,14 +606,21 @@ int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const floa
     M2_REQUIRE(a.ngroups > 0 && a.nheads % a.ngroups == 0, M2_ERR_INVALID,
                "scan_fused: nheads %% ngroups != 0");
     const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
-    const int64_t nwork = a.batch * nc * a.ngroups;
+    const int hpg = (int)(a.nheads / a.ngroups);
+    // a group's heads split over enough workgroups to fill the 256 CUs (each
+    // slice builds CB again: cheap next to its heads' work)
+    const int64_t items = a.batch * nc * a.ngroups;
+    int nslice = (int)std::min<int64_t>(hpg, std::max<int64_t>(1, (256 + items - 1) / items));
+    const int hps = (hpg + nslice - 1) / nslice;
+    nslice = (hpg + hps - 1) / hps;
+    const int64_t nwork = items * nslice;
     M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "scan_fused: too many blocks");
     ScanFusedArgs f{};
     f.x = (const bf16*)a.x; f.B = (const bf16*)a.B; f.C = (const bf16*)a.C;
     f.states = (const bf16*)passed; f.dt = dto; f.dA = dA; f.D = a.D; f.z = (const bf16*)a.z;
     f.seq_idx = a.seq_idx; f.out = a.out; f.D_has_hdim = a.D_has_hdim;
     f.L = (int)a.seqlen; f.H = (int)a.nheads; f.G = (int)a.ngroups; f.nc = (int)nc;
-    f.hpg = (int)(a.nheads / a.ngroups); f.nwork = (int)nwork;
+    f.hpg = hpg; f.nwork = (int)nwork; f.hps = hps; f.nslice = nslice;
     void (*kern)(ScanFusedArgs) = nullptr;
     const bool hz = a.z != nullptr;
 #define M2_SF_CASE(NSV, QTV)                                                        \
