@@ -3,9 +3,11 @@
 //
 // Both operands are K-contiguous in HBM ([.., L, G, K] rows), which is exactly
 // the per-lane layout MFMA wants, so every fragment is one 16-byte global load
-// (bf16) straight into VGPRs -- no LDS round trip.  A workgroup owns 64 rows of
-// one (b, c, g) block; each of its 4 wavefronts owns one 16-row tile and all
-// Q/16 column tiles.  Causal and seq_idx masks are applied in the epilogue.
+// (bf16) straight into VGPRs -- no LDS round trip.  A workgroup owns a 64 x 64
+// tile of one (b, c, g) block (so that even a few chunks fill the CUs); each of
+// its 4 wavefronts owns one 16-row tile and the 4 column tiles, with the K
+// loop unrolled so that several steps of loads are in flight.  Causal and
+// seq_idx masks are applied in the epilogue.
 //
 // Follows reference kernels/bmm_chunk_fwd.py:87-154 (product), :348-372
 // (masks; positions past the end carry seq id -1) and ops/ssd_naive.py:189-216.
@@ -22,8 +24,9 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
             int K, int Q, int nc, int causal, int rowblocks, int nblocks) {
     typedef MF<T> M;
     const int work = xcd_remap(blockIdx.x, nblocks);
-    const int rb = work % rowblocks;
-    int rest = work / rowblocks;
+    const int cb = work % rowblocks;                     // 64-column block
+    const int rb = (work / rowblocks) % rowblocks;       // 64-row block
+    int rest = work / (rowblocks * rowblocks);
     const int g = rest % G;
     rest /= G;
     const int c = rest % nc;
@@ -41,9 +44,9 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
     bool bok[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-        const int col = ct * 16 + ln;
+        const int col = cb * 64 + ct * 16 + ln;
         bok[ct] = (c * Q + col) < L && col < Q;
-        bp[ct] = b + ((tbase + col) * G + g) * K + kg * M::KPL;
+        bp[ct] = b + ((tbase + min(col, Q - 1)) * G + g) * K + kg * M::KPL;
     }
     f32x4 acc[CT];
 #pragma unroll
@@ -53,6 +56,7 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
 #pragma unroll
     for (int j = 0; j < M::KPL; ++j) M::set(zf, j, 0.f);
 
+#pragma unroll 8
     for (int k0 = 0; k0 < K; k0 += M::K) {
         const typename M::frag af = arow_ok ? load_frag(ap + k0) : zf;
         typename M::frag bf[CT];
@@ -65,7 +69,7 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
     TO* op = out + ((((int64_t)bi * nc + c) * G + g) * Q) * Q;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-        const int col = ct * 16 + ln;
+        const int col = cb * 64 + ct * 16 + ln;
         if (col >= Q) continue;
         int scol = 0;
         if (seq_idx) scol = (c * Q + col) < L ? seq_idx[tbase + col] : -1;
@@ -88,9 +92,9 @@ int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
     const int Q = (int)a.chunk_size;
     const int nc = (int)((a.seqlen + Q - 1) / Q);
     const int rowblocks = (Q + 63) / 64;
-    const int64_t nblocks = a.batch * nc * a.ngroups * rowblocks;
+    const int64_t nblocks = a.batch * nc * a.ngroups * rowblocks * rowblocks;
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "bmm_chunk: too many blocks");
-    const int ct = Q / 16;
+    const int ct = Q < 64 ? Q / 16 : 4;
 #define M2_BMM_CASE(CTV)                                                                  \
     case CTV:                                                                             \
         k_bmm_chunk<T, TO, CTV><<<(unsigned)nblocks, THREADS, 0, s>>>(                     \
@@ -98,10 +102,7 @@ int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
             (int)a.ngroups, (int)a.k, Q, nc, a.causal, rowblocks, (int)nblocks);          \
         break;
     switch (ct) {
-        M2_BMM_CASE(1) M2_BMM_CASE(2) M2_BMM_CASE(3) M2_BMM_CASE(4) M2_BMM_CASE(5)
-        M2_BMM_CASE(6) M2_BMM_CASE(7) M2_BMM_CASE(8) M2_BMM_CASE(9) M2_BMM_CASE(10)
-        M2_BMM_CASE(11) M2_BMM_CASE(12) M2_BMM_CASE(13) M2_BMM_CASE(14) M2_BMM_CASE(15)
-        M2_BMM_CASE(16)
+        M2_BMM_CASE(1) M2_BMM_CASE(2) M2_BMM_CASE(3) M2_BMM_CASE(4)
         default: return m2::set_error(M2_ERR_UNSUPPORTED, "bmm_chunk: chunk_size %d", Q);
     }
 #undef M2_BMM_CASE

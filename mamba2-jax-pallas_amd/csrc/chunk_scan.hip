@@ -3,7 +3,7 @@
 //          + exp(dA[m]) * C[m,:] @ states^T                        (carried state)
 //          + D x[m,:],   then y *= silu(z[m,:])
 //
-// One workgroup per (b, c, h), 4 wavefronts; the chunk's x rows [Q x P] and
+// One workgroup per (b, c, h), 8 wavefronts; the chunk's x rows [Q x P] and
 // the carried state [P x N] are staged in LDS (16-byte coalesced loads; the
 // state is rounded to x's dtype on the way in).  Each wavefront takes 16-row
 // tiles of the output in a snake order so that the causal (triangular) work
@@ -21,7 +21,9 @@
 
 namespace {
 
-constexpr int THREADS = 256;
+constexpr int THREADS = 512;
+constexpr int NW = THREADS / 64;      // wavefronts: two per SIMD (one workgroup per CU
+                                      // when the fp32 x tile fills the LDS)
 
 template <typename T> struct ScanPad;
 template <> struct ScanPad<bf16> { static constexpr int x = 2; static constexpr int s = 8; };
@@ -146,25 +148,36 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
 
     const int ntiles = Q / 16;
     for (int r = 0;; ++r) {
-        const int t = r * 4 + ((r & 1) ? (3 - w) : w);
+        const int t = r * NW + ((r & 1) ? (NW - 1 - w) : w);
         if (t >= ntiles) break;
         const int m0 = t * 16;
         f32x4 acc[PT];
 #pragma unroll
         for (int pt = 0; pt < PT; ++pt) acc[pt] = zero4();
 
-        // 1. carried state: C[m, :] @ state^T
+        // 1. carried state: C[m, :] @ state^T.  The C fragments of BATCH K
+        // steps are loaded (unconditionally: rows past the end are clamped and
+        // zeroed afterwards) before any is used, so they are in flight together.
         {
             const int m = m0 + ln;
             const bool mok = m < valid;
-            const T* crow = Cbase + (int64_t)m * a.G * N + kg * KPL;
-            for (int k0 = 0; k0 < N; k0 += M::K) {
-                const typename M::frag af = mok ? load_frag(crow + k0) : zf;
+            const T* crow = Cbase + (int64_t)min(m, valid - 1) * a.G * N + kg * KPL;
+            constexpr int BATCH = KPL == 1 ? 8 : 2;
+            for (int k0 = 0; k0 < N; k0 += BATCH * M::K) {
+                typename M::frag cf[BATCH];
 #pragma unroll
-                for (int pt = 0; pt < PT; ++pt) {
-                    const typename M::frag bfr =
-                        load_frag(ss + (pt * 16 + ln) * SS + k0 + kg * KPL);
-                    acc[pt] = M::mma(af, bfr, acc[pt]);
+                for (int u = 0; u < BATCH; ++u) cf[u] = load_frag(crow + min(k0 + u * M::K, N - M::K));
+#pragma unroll
+                for (int u = 0; u < BATCH; ++u) {
+                    // steps past N (N not a multiple of the batch) add zero
+                    const int k = min(k0 + u * M::K, N - M::K);
+                    const typename M::frag af = (mok && k0 + u * M::K < N) ? cf[u] : zf;
+#pragma unroll
+                    for (int pt = 0; pt < PT; ++pt) {
+                        const typename M::frag bfr =
+                            load_frag(ss + (pt * 16 + ln) * SS + k + kg * KPL);
+                        acc[pt] = M::mma(af, bfr, acc[pt]);
+                    }
                 }
             }
             // C @ states has x's dtype as result type in the reference
@@ -179,16 +192,25 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
             }
         }
 
-        // 2. intra-chunk: (cb o decay o dt)[m, k<=m] @ x[k, :]
+        // 2. intra-chunk: (cb o decay o dt)[m, k<=m] @ x[k, :]; the cb values of
+        // BATCH K steps are loaded before any is used
         {
             const int m = m0 + ln;
             const float dAm = dAs[m];
             const TCB* cbrow = cbbase + (int64_t)m * Q;
             const int kend = m0 + 16;
-            for (int k0 = 0; k0 < kend; k0 += M::K) {
+            constexpr int BATCH = KPL == 1 ? 8 : 2;
+            for (int kB = 0; kB < kend; kB += BATCH * M::K) {
+            float cbb[BATCH][KPL];
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u)
+                load_cb<KPL>(cbrow + min(kB + u * M::K + kg * KPL, Q - KPL), cbb[u]);
+#pragma unroll
+            for (int u = 0; u < BATCH; ++u) {
+                const int k0 = kB + u * M::K;
+                if (k0 >= kend) break;
                 const int kb = k0 + kg * KPL;
-                float cbv[KPL];
-                if (kb < Q) load_cb<KPL>(cbrow + kb, cbv);
+                const float* cbv = cbb[u];
                 // the weighted operand is split into bf16 hi + lo parts (x is
                 // exact in bf16): the intra-chunk sum keeps near-fp32 accuracy
                 typename M::frag af, al;
@@ -210,6 +232,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
                     acc[pt] = M::mma(af, bfr, acc[pt]);
                     if constexpr (M::kSplit) acc[pt] = M::mma(al, bfr, acc[pt]);
                 }
+            }
             }
         }
 
