@@ -2,7 +2,7 @@
 //   states[b,c,h][p,n] = sum_q w[q] x[q,p] B[q,n],  w[q] = exp(min(dA[last]-dA[q],0)) dt[q]
 // and its variable-length twin (the final state of each packed sequence).
 //
-// One workgroup per (b, c, h) (per (sequence, h) for varlen), 4 wavefronts.
+// One workgroup per (b, c, h) (per (sequence, h) for varlen), 8 wavefronts.
 // The contraction runs over chunk positions q, the outer (row) dimension of
 // both x [.., L, H, P] and B [.., L, G, N] in HBM, so x and B rows are staged
 // through LDS with coalesced 16-byte loads and the MFMA fragments (8
@@ -10,9 +10,9 @@
 // weight w[q] is applied to the x operand as it is gathered, and for bf16 the
 // weighted operand is split into hi + lo bf16 parts (two MFMAs) so that the
 // states keep near-fp32 accuracy, as the reference's fp32 einsum does.  Positions are
-// processed in blocks of KB rows to bound LDS.  Wavefront w owns all P/16 row
-// tiles and N/64 column tiles: [P x N] fp32 accumulators live in VGPRs and
-// are written once.
+// processed in blocks of KB rows to bound LDS.  Wavefront w owns half of the
+// P/16 row tiles (w >> 2) and N/64 of the 16-column tiles (w & 3): the
+// [P x N] fp32 accumulators live in VGPRs and are written once.
 //
 // Follows reference kernels/chunk_state_fwd.py:104-187 (product), :239-269
 // (scale and seq_idx rule), :448-597 (varlen) and ops/ssd_naive.py:77-128.
@@ -20,7 +20,7 @@
 
 namespace {
 
-constexpr int THREADS = 256;
+constexpr int THREADS = 512;         // 8 wavefronts: two per SIMD
 
 // LDS row padding (elements) so that the 4 k-groups of a fragment gather hit
 // different banks.
@@ -123,16 +123,19 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
         wq[q] = v;
     }
 
-    const int lane = threadIdx.x & 63, w = wave_id();
+    const int lane = threadIdx.x & 63, w8 = wave_id();
+    // wavefront w8: column tiles of group w = w8 & 3, row tiles of half w8 >> 2
+    const int w = w8 & 3, pr0 = (w8 >> 2) * (PT / 2);
     const int ln = lane & 15, kg = lane >> 4;
     const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;   // token of position 0
     const int valid = min(Q, L - c * Q);
     const T* xsrc = reinterpret_cast<const T*>(a.x) + (tok0 * H + h) * P;
     const T* bsrc = reinterpret_cast<const T*>(a.B) + (tok0 * a.G + g) * N;
 
-    f32x4 acc[PT][CTW];
+    constexpr int PTH = PT / 2;          // row tiles per wavefront
+    f32x4 acc[PTH][CTW];
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt)
+    for (int pt = 0; pt < PTH; ++pt)
 #pragma unroll
         for (int j = 0; j < CTW; ++j) acc[pt][j] = zero4();
 
@@ -144,15 +147,15 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
         for (int k0 = 0; k0 < KB; k0 += M::K) {
             // x[q,p] * w[q] is split into bf16 hi + lo parts (x and B are exact
             // in their dtype, so two MFMAs give near-fp32 weighted sums)
-            typename M::frag af[PT], al[PT], bfr[CTW];
+            typename M::frag af[PTH], al[PTH], bfr[CTW];
 #pragma unroll
             for (int j = 0; j < M::KPL; ++j) {
                 const int kl = k0 + kg * M::KPL + j;      // position within the block
                 const bool kok = kl < KB && kb + kl < Q;
                 const float wk = kok ? wq[kb + kl] : 0.f;
 #pragma unroll
-                for (int pt = 0; pt < PT; ++pt) {
-                    const float xv = kok ? to_f32(xs[kl * SX + pt * 16 + ln]) : 0.f;
+                for (int pt = 0; pt < PTH; ++pt) {
+                    const float xv = kok ? to_f32(xs[kl * SX + (pr0 + pt) * 16 + ln]) : 0.f;
                     M::set_split(af[pt], al[pt], j, xv * wk);
                 }
 #pragma unroll
@@ -162,7 +165,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
                 }
             }
 #pragma unroll
-            for (int pt = 0; pt < PT; ++pt)
+            for (int pt = 0; pt < PTH; ++pt)
 #pragma unroll
                 for (int jj = 0; jj < CTW; ++jj) {
                     acc[pt][jj] = M::mma(af[pt], bfr[jj], acc[pt][jj]);
@@ -187,13 +190,13 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
         }
     }
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt)
+    for (int pt = 0; pt < PTH; ++pt)
 #pragma unroll
         for (int jj = 0; jj < CTW; ++jj) {
             const int n = (w * CTW + jj) * 16 + ln;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int p = pt * 16 + kg * 4 + i;
+                const int p = (pr0 + pt) * 16 + kg * 4 + i;
                 float v = acc[pt][jj][i];
                 if (VARLEN) {
                     if (cs16) v += carry_scale * to_f32(cs16[p * N + n]);
