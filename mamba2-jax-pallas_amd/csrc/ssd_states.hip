@@ -237,20 +237,13 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
                                                      // at chunk starts the second half's part
         const char* slot = ring + k * SLOT;
         const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
+        // h_c (sum of the halves) is the state entering chunk c: this half's
+        // two tiles of it are summed, rounded to bf16 and staged after the
+        // stage's MFMA steps are issued (whose latency hides the reads of the
+        // other half's part); both halves continue with h <- scl[c] h
+        f32x4 h0, h1;
         if (kb == 0) {
-            // h_c (sum of the halves) is the state entering chunk c; then both
-            // halves h <- scl[c] h
-            {
-                // round this half's two summed tiles to bf16 into the staging
-                // rows (lane (ln, kg): 4 columns of row ln)
-                f32x4 s0, s1;
-                take(c & 1, s0, s1);
-                bf16* pr = &pst[c & 1][pw][ln][32 * kh + 4 * kg];
-                const bf16x4 o0 = {(bf16)s0[0], (bf16)s0[1], (bf16)s0[2], (bf16)s0[3]};
-                const bf16x4 o1 = {(bf16)s1[0], (bf16)s1[1], (bf16)s1[2], (bf16)s1[3]};
-                *reinterpret_cast<bf16x4*>(pr) = o0;
-                *reinterpret_cast<bf16x4*>(pr + 16) = o1;
-            }
+            take(c & 1, h0, h1);
             const float sc = aux[KB];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -285,6 +278,14 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
             }
+        }
+        if (kb == 0) {
+            // lane (ln, kg): 4 columns of staging row ln
+            bf16* pr = &pst[c & 1][pw][ln][32 * kh + 4 * kg];
+            const bf16x4 o0 = {(bf16)h0[0], (bf16)h0[1], (bf16)h0[2], (bf16)h0[3]};
+            const bf16x4 o1 = {(bf16)h1[0], (bf16)h1[1], (bf16)h1[2], (bf16)h1[3]};
+            *reinterpret_cast<bf16x4*>(pr) = o0;
+            *reinterpret_cast<bf16x4*>(pr + 16) = o1;
         }
         if ((s + 1) % SPC == 0) give((c + 1) & 1);  // the end of chunk c: parts of h_{c+1}
     }
