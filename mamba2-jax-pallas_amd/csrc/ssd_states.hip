@@ -253,28 +253,39 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         // acc += B^T (w x) over this half's KB/2 positions.  In step ks, MFMA k
         // index j < 4 is position (KB/2) kh + 32 ks + 4 kg + j, j >= 4 is 16 more.
         // Lane j < 8 of each row reads the weight of k index j; the row shares them.
+        // every LDS operand of the stage is read first, so that the reads'
+        // latencies overlap (left to itself the scheduler reuses one register
+        // set and waits for each B fragment before its MFMAs)
+        float wl[C::KS];
+        bf16x4 xa[C::KS], xb[C::KS], ba[C::KS][4], bb[C::KS][4];
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-            const float wl = aux[wpos + 32 * ks];
-            const float wv[8] = {row_bcast<0>(wl), row_bcast<1>(wl), row_bcast<2>(wl), row_bcast<3>(wl),
-                                 row_bcast<4>(wl), row_bcast<5>(wl), row_bcast<6>(wl), row_bcast<7>(wl)};
-            bf16x8 xh, xl;
-            {
-                const bf16x4 x0 = ds_read_tr(slot + xo0 + ks * 32 * (2 * P));
-                const bf16x4 x1 = ds_read_tr(slot + xo1 + ks * 32 * (2 * P));
+            wl[ks] = aux[wpos + 32 * ks];
+            xa[ks] = ds_read_tr(slot + xo0 + ks * 32 * (2 * P));
+            xb[ks] = ds_read_tr(slot + xo1 + ks * 32 * (2 * P));
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float v = (float)(j < 4 ? x0[j] : x1[j - 4]) * wv[j];
-                    const bf16 hi = (bf16)v;
-                    xh[j] = hi;
-                    xl[j] = (bf16)(v - (float)hi);
-                }
+            for (int j = 0; j < 4; ++j) {
+                ba[ks][j] = ds_read_tr(slot + bo0[j] + ks * 32 * (2 * NB));
+                bb[ks][j] = ds_read_tr(slot + bo1[j] + ks * 32 * (2 * NB));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+            const float w0 = wl[ks];
+            const float wv[8] = {row_bcast<0>(w0), row_bcast<1>(w0), row_bcast<2>(w0), row_bcast<3>(w0),
+                                 row_bcast<4>(w0), row_bcast<5>(w0), row_bcast<6>(w0), row_bcast<7>(w0)};
+            bf16x8 xh, xl;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = (float)(j < 4 ? xa[ks][j] : xb[ks][j - 4]) * wv[j];
+                const bf16 hi = (bf16)v;
+                xh[j] = hi;
+                xl[j] = (bf16)(v - (float)hi);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const bf16x4 b0 = ds_read_tr(slot + bo0[j] + ks * 32 * (2 * NB));
-                const bf16x4 b1 = ds_read_tr(slot + bo1[j] + ks * 32 * (2 * NB));
-                const bf16x8 bf = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+                const bf16x8 bf = __builtin_shufflevector(ba[ks][j], bb[ks][j], 0, 1, 2, 3, 4, 5, 6, 7);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
             }
