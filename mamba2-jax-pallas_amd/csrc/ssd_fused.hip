@@ -506,14 +506,24 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
             f32x4 ci_[PTW];
 #pragma unroll
             for (int pt = 0; pt < PTW; ++pt) ci_[pt] = zero4();
+            // state fragments in blocks of BR reads, each block read before
+            // its MFMAs are issued (fragment f: head-dim tile f / NS, k step f % NS)
+            constexpr int NF = PTW * NS, BR = (NS >= 8 ? 4 : 8) < NF ? (NS >= 8 ? 4 : 8) : NF;
 #pragma unroll
-            for (int pt = 0; pt < PTW; ++pt) {
-                const int p = 16 * (PTW * pp + pt) + ln;
+            for (int f0 = 0; f0 < NF; f0 += BR) {
+                bf16x8 sfr[BR];
 #pragma unroll
-                for (int ns = 0; ns < NS; ++ns) {
-                    const bf16x8 sfr = *reinterpret_cast<const bf16x8*>(
+                for (int q = 0; q < BR; ++q) {
+                    const int pt = (f0 + q) / NS, ns = (f0 + q) % NS;
+                    const int p = 16 * (PTW * pp + pt) + ln;
+                    sfr[q] = *reinterpret_cast<const bf16x8*>(
                         slot + XB + p * (2 * N) + (((4 * ns + kg) ^ sswz<SCPR>(p)) * 16));
-                    ci_[pt] = mma32(sfr, kh ? cfr[0][ns] : cfr[1][ns], ci_[pt]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < BR; ++q) {
+                    const int pt = (f0 + q) / NS, ns = (f0 + q) % NS;
+                    ci_[pt] = mma32(sfr[q], kh ? cfr[0][ns] : cfr[1][ns], ci_[pt]);
                 }
             }
             const float f = __builtin_amdgcn_exp2f(dAs[mrow] * LOG2E) * (kh ? fmask[0] : fmask[1]);
