@@ -230,6 +230,74 @@ typedef struct {
 } m2_ssu_args;
 int m2_selective_state_update(const m2_ssu_args* a, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Output of a causal_conv1d call: channels [c_begin, next range's c_begin) of
+ * the result go to `ptr`, element (b, c, t) at
+ *   b * stride_batch + (c - c_begin) * stride_dim + t * stride_time
+ * (strides in elements of the result dtype).  One range covers every channel;
+ * three ranges write x, B and C of an SSD layer straight into their own
+ * tensors.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    void*   ptr;
+    int64_t c_begin;
+    int64_t stride_batch, stride_dim, stride_time;
+} m2_conv_out;
+
+/* ---------------------------------------------------------------------------
+ * causal_conv1d: depthwise causal convolution over time, per channel c:
+ *   xm[s] = x[s], zeroed when seq_idx is given and seq_idx[s + j] !=
+ *           seq_idx[s + j - 1] for some 1 <= j < width with s + j < L
+ *   y[t]  = sum_{i < width} weight[c, i] xm[t - width + 1 + i]  (0 before t = 0)
+ *   out   = silu?(y + bias[c])
+ * The result dtype (out_dtype) is bf16 when x, weight and bias (if given) are
+ * all bf16, else f32; a bf16 conv result is rounded before the bias add.
+ * x is addressed through (batch, channel, time) element strides: a contiguous
+ * [b, d, L] array and a [b, L, d] channels-last buffer both work (unit channel
+ * stride and unit time stride are the fast layouts).
+ * Replaces causal_conv1d (reference ops/causal_conv1d.py:18-85, boundary mask
+ * :142-193).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void*    x;              /* [b, d, L] at the strides below, x_dtype */
+    int64_t        x_stride_batch, x_stride_dim, x_stride_time;
+    const void*    weight;         /* [d, width] contiguous, w_dtype          */
+    const void*    bias;           /* [d], bias_dtype, or NULL               */
+    const int32_t* seq_idx;        /* [b, L] contiguous, or NULL             */
+    m2_conv_out    out[3];         /* nout ranges, out[0].c_begin = 0        */
+    int64_t batch, dim, seqlen, width;   /* width 1 .. 8                     */
+    int32_t nout;
+    int32_t x_dtype, w_dtype, bias_dtype, out_dtype;
+    int32_t silu;                  /* 0 / 1 (activation="silu")              */
+} m2_causal_conv1d_args;
+int m2_causal_conv1d(const m2_causal_conv1d_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * causal_conv1d_update (one decode token):
+ *   new_state = concat(conv_state[:, :, 1:], x[:, :, None])
+ *   out = silu?(sum_i new_state[:, :, i] weight[:, i] + bias)
+ * new_state_dtype is bf16 when conv_state and x are bf16, else f32; new_state
+ * may be conv_state (in-place update, same dtype).  The products are bf16
+ * (each rounded, their sum rounded once) when new_state and weight are bf16;
+ * out_dtype is bf16 when those and the bias are bf16, else f32.  The outputs'
+ * stride_dim must be 1 (stride_time is ignored).
+ * Replaces causal_conv1d_update (reference ops/causal_conv1d.py:88-139).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void* x;                 /* [b, d] at x_stride_batch, x_dtype      */
+    int64_t     x_stride_batch;
+    const void* conv_state;        /* [b, d, width] contiguous, state_dtype  */
+    void*       new_state;         /* [b, d, width] contiguous               */
+    const void* weight;            /* [d, width] contiguous, w_dtype         */
+    const void* bias;              /* [d], bias_dtype, or NULL               */
+    m2_conv_out out[3];            /* nout ranges, out[0].c_begin = 0        */
+    int64_t batch, dim, width;     /* width 1 .. 8                           */
+    int32_t nout;
+    int32_t x_dtype, state_dtype, new_state_dtype, w_dtype, bias_dtype, out_dtype;
+    int32_t silu;
+} m2_causal_conv1d_update_args;
+int m2_causal_conv1d_update(const m2_causal_conv1d_update_args* a, void* stream);
+
 /* thread-local message for the last non-zero return code of this thread */
 const char* m2_last_error(void);
 /* M2SSD_ABI_VERSION of the loaded library */

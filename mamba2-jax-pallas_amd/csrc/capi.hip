@@ -42,6 +42,8 @@ M2_ENTRY(m2_bmm_chunk, m2_bmm_chunk_args, launch_bmm_chunk)
 M2_ENTRY(m2_chunk_scan, m2_chunk_scan_args, launch_chunk_scan)
 M2_ENTRY(m2_chunk_state_varlen, m2_chunk_state_varlen_args, launch_chunk_state_varlen)
 M2_ENTRY(m2_selective_state_update, m2_ssu_args, launch_ssu)
+M2_ENTRY(m2_causal_conv1d, m2_causal_conv1d_args, launch_causal_conv1d)
+M2_ENTRY(m2_causal_conv1d_update, m2_causal_conv1d_update_args, launch_causal_conv1d_update)
 
 // ---------------------------------------------------------------------------
 // combined forward

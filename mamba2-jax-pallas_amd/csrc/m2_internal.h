@@ -17,6 +17,8 @@ int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t stream);
 int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t stream);
 int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t stream);
 int launch_ssu(const m2_ssu_args& a, hipStream_t stream);
+int launch_causal_conv1d(const m2_causal_conv1d_args& a, hipStream_t stream);
+int launch_causal_conv1d_update(const m2_causal_conv1d_update_args& a, hipStream_t stream);
 
 // chunk_state_varlen for bf16, head dim 64, dstate % 64 == 0, chunk_size % 32
 // == 0 (<= 256): one workgroup per (sequence, head, 64-column dstate block)

@@ -94,6 +94,27 @@ class SsuArgs(ctypes.Structure):
                 ("dt_bias_has_hdim", _i32), ("dt_softplus", _i32)]
 
 
+class ConvOut(ctypes.Structure):
+    _fields_ = [("ptr", _c_p), ("c_begin", _i64), ("stride_batch", _i64),
+                ("stride_dim", _i64), ("stride_time", _i64)]
+
+
+class CausalConv1dArgs(ctypes.Structure):
+    _fields_ = [("x", _c_p), ("x_stride_batch", _i64), ("x_stride_dim", _i64),
+                ("x_stride_time", _i64), ("weight", _c_p), ("bias", _c_p), ("seq_idx", _c_p),
+                ("out", ConvOut * 3), ("batch", _i64), ("dim", _i64), ("seqlen", _i64),
+                ("width", _i64), ("nout", _i32), ("x_dtype", _i32), ("w_dtype", _i32),
+                ("bias_dtype", _i32), ("out_dtype", _i32), ("silu", _i32)]
+
+
+class CausalConv1dUpdateArgs(ctypes.Structure):
+    _fields_ = [("x", _c_p), ("x_stride_batch", _i64), ("conv_state", _c_p),
+                ("new_state", _c_p), ("weight", _c_p), ("bias", _c_p), ("out", ConvOut * 3),
+                ("batch", _i64), ("dim", _i64), ("width", _i64), ("nout", _i32),
+                ("x_dtype", _i32), ("state_dtype", _i32), ("new_state_dtype", _i32),
+                ("w_dtype", _i32), ("bias_dtype", _i32), ("out_dtype", _i32), ("silu", _i32)]
+
+
 # entry point name -> argument struct (every function declared in m2ssd.h)
 ENTRY_POINTS = {
     "m2_chunk_cumsum": ChunkCumsumArgs,
@@ -104,6 +125,8 @@ ENTRY_POINTS = {
     "m2_chunk_state_varlen": ChunkStateVarlenArgs,
     "m2_ssd_combined": SsdCombinedArgs,
     "m2_selective_state_update": SsuArgs,
+    "m2_causal_conv1d": CausalConv1dArgs,
+    "m2_causal_conv1d_update": CausalConv1dUpdateArgs,
 }
 OTHER_SYMBOLS = ("m2_ssd_combined_workspace_size", "m2_last_error", "m2_abi_version")
 
