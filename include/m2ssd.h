@@ -298,6 +298,30 @@ typedef struct {
 } m2_causal_conv1d_update_args;
 int m2_causal_conv1d_update(const m2_causal_conv1d_update_args* a, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * rms_norm_gated over groups of group_size consecutive elements of each row:
+ *   x' = x * silu(z)                 (z given and !norm_before_gate)
+ *   out = x' / sqrt(mean(x'^2) + eps) * weight
+ *   out = out * silu(z)              (z given and norm_before_gate)
+ * Every intermediate is bf16 exactly when all its operands are (x, z, weight
+ * as they enter it); out_dtype must be that result dtype.  Rows are addressed
+ * through row strides (elements; the last dimension is contiguous), e.g. z as
+ * a slice of the in-projection output.
+ * Replaces rms_norm_gated (reference ops/rms_norm.py:15-92).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void* x;                 /* [rows, hidden] at x_row_stride, x_dtype   */
+    const void* z;                 /* [rows, hidden] at z_row_stride, or NULL   */
+    const void* weight;            /* [hidden], w_dtype                         */
+    void*       out;               /* [rows, hidden] at out_row_stride          */
+    int64_t x_row_stride, z_row_stride, out_row_stride;
+    int64_t rows, hidden, group_size;   /* group_size divides hidden          */
+    float   eps;
+    int32_t x_dtype, z_dtype, w_dtype, out_dtype;
+    int32_t norm_before_gate;      /* 0 / 1                                     */
+} m2_rms_norm_gated_args;
+int m2_rms_norm_gated(const m2_rms_norm_gated_args* a, void* stream);
+
 /* thread-local message for the last non-zero return code of this thread */
 const char* m2_last_error(void);
 /* M2SSD_ABI_VERSION of the loaded library */

@@ -1,0 +1,264 @@
+// rms_norm_gated: RMSNorm over groups of the last dimension with an optional
+// SiLU gate, the step after the SSD in a Mamba2 layer:
+//   x' = x * silu(z)              (gate before the norm: z given, !norm_before_gate)
+//   out = x' / sqrt(mean(x'^2) + eps) * weight
+//   out *= silu(z)                (gate after the norm: z given, norm_before_gate)
+// per row and group of `group_size` consecutive elements.
+//
+// HBM-bound (x, z read once, out written once).  One workgroup per (row,
+// group): NT threads hold E chunks of CW elements each in registers (CW = 4:
+// 16- / 8-byte accesses; CW = 1 for sizes that are not multiples of 4),
+// the sum of squares is reduced over the wavefronts in LDS, and the scaled
+// values are written from the registers.  Groups longer than NT * E are
+// processed in passes (the second pass re-reads x and z from cache).
+// Rounding follows the reference's array dtypes: every intermediate whose
+// JAX dtype is bfloat16 is rounded to bf16 (bf16 only when all its operands
+// are bf16); silu(z) has z's dtype.
+//
+// Follows reference ops/rms_norm.py:15-92.
+#include "m2_internal.h"
+
+namespace {
+
+struct NormArgs {
+    const void* x;
+    const void* z;
+    const void* w;
+    void* out;
+    int64_t x_rs, z_rs, o_rs;     // row strides (elements)
+    int64_t hidden, gs, ngroups;  // ngroups per row
+    float eps;
+    int x_bf16, z_bf16, w_bf16, o_bf16;
+    int gate_first, gate_after;
+    int r_x;                      // the normalised operand (x or x * silu(z)) is bf16
+    int r_w;                      // x_normed * weight is bf16
+    int r_o;                      // the gated output is bf16
+    int vec;                      // 4-element accesses
+};
+
+M2_DEV float rbf(float v) { return (float)(bf16)v; }
+
+// silu(v) = v / (1 + e^-v) from the hardware exp2 / reciprocal (~1 ulp each)
+M2_DEV float silu_fast(float v) {
+    const float e = __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
+    return v * __builtin_amdgcn_rcpf(1.f + e);
+}
+
+// CW consecutive elements at i (one 16- / 8-byte access when CW == 4 and vec)
+template <int CW> M2_DEV void ldc(const void* p, int64_t i, int is_bf16, int vec, float (&o)[CW]) {
+    if constexpr (CW == 1) {
+        o[0] = is_bf16 ? (float)reinterpret_cast<const bf16*>(p)[i] : reinterpret_cast<const float*>(p)[i];
+        return;
+    } else if (is_bf16) {
+        const bf16* q = reinterpret_cast<const bf16*>(p) + i;
+        if (vec) {
+            const bf16x4 r = *reinterpret_cast<const bf16x4*>(q);
+            o[0] = (float)r[0]; o[1] = (float)r[1]; o[2] = (float)r[2]; o[3] = (float)r[3];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = (float)q[k];
+        }
+    } else {
+        const float* q = reinterpret_cast<const float*>(p) + i;
+        if (vec) {
+            const float4 r = *reinterpret_cast<const float4*>(q);
+            o[0] = r.x; o[1] = r.y; o[2] = r.z; o[3] = r.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = q[k];
+        }
+    }
+}
+
+template <int CW> M2_DEV void stc(void* p, int64_t i, int is_bf16, int vec, const float (&v)[CW]) {
+    if constexpr (CW == 1) {
+        if (is_bf16) reinterpret_cast<bf16*>(p)[i] = (bf16)v[0];
+        else reinterpret_cast<float*>(p)[i] = v[0];
+        return;
+    } else if (is_bf16) {
+        bf16* q = reinterpret_cast<bf16*>(p) + i;
+        bf16x4 r;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = (bf16)v[k];
+        if (vec) {
+            *reinterpret_cast<bf16x4*>(q) = r;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q[k] = r[k];
+        }
+    } else {
+        float* q = reinterpret_cast<float*>(p) + i;
+        if (vec) {
+            *reinterpret_cast<float4*>(q) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q[k] = v[k];
+        }
+    }
+}
+
+// the normalised operand of CW elements at group offset i
+template <int CW>
+M2_DEV void operand(const NormArgs& a, const void* xr, const void* zr, int64_t i, float (&v)[CW],
+                    float (&sz)[CW]) {
+    ldc<CW>(xr, i, a.x_bf16, a.vec, v);
+    if (a.gate_first || a.gate_after) {
+        ldc<CW>(zr, i, a.z_bf16, a.vec, sz);
+#pragma unroll
+        for (int k = 0; k < CW; ++k) sz[k] = a.z_bf16 ? rbf(silu_fast(sz[k])) : silu_fast(sz[k]);
+    }
+    if (a.gate_first) {
+#pragma unroll
+        for (int k = 0; k < CW; ++k) v[k] = a.r_x ? rbf(v[k] * sz[k]) : v[k] * sz[k];
+    }
+}
+
+template <int CW>
+M2_DEV void output(const NormArgs& a, void* orow, const void* w, int64_t i, int64_t wi, float inv,
+                   const float (&v)[CW], const float (&sz)[CW]) {
+    float wt[CW], o[CW];
+    ldc<CW>(w, wi, a.w_bf16, a.vec, wt);
+#pragma unroll
+    for (int k = 0; k < CW; ++k) {
+        float xn = v[k] * inv;
+        if (a.r_x) xn = rbf(xn);
+        float y = xn * wt[k];
+        if (a.r_w) y = rbf(y);
+        if (a.gate_after) {
+            y *= sz[k];
+            if (a.r_o) y = rbf(y);
+        }
+        o[k] = y;
+    }
+    stc<CW>(orow, i, a.o_bf16, a.vec, o);
+}
+
+template <int NT>
+M2_DEV float block_sum(float v, float* red) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    if (NT == 64) return v;
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NT / 64; ++j) s += red[j];
+    return s;
+}
+
+// NT threads, E CW-element chunks per thread in registers
+template <int NT, int E, int CW>
+__global__ void __launch_bounds__(NT) k_rms_norm(NormArgs a) {
+    __shared__ float red[NT / 64];
+    const int64_t blk = blockIdx.x;
+    const int64_t row = blk / a.ngroups, g = blk % a.ngroups;
+    const int64_t gofs = g * a.gs;
+    const char* xr = reinterpret_cast<const char*>(a.x) + (row * a.x_rs + gofs) * (a.x_bf16 ? 2 : 4);
+    const char* zr = a.z ? reinterpret_cast<const char*>(a.z) + (row * a.z_rs + gofs) * (a.z_bf16 ? 2 : 4)
+                         : nullptr;
+    char* orow = reinterpret_cast<char*>(a.out) + (row * a.o_rs + gofs) * (a.o_bf16 ? 2 : 4);
+    const int t = threadIdx.x;
+    const int64_t n4 = a.gs / CW;                // chunks in the group
+    const bool resident = n4 <= (int64_t)NT * E;
+
+    float v[E][CW], sz[E][CW];
+    float ss = 0.f;
+    if (resident) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int64_t c = (int64_t)e * NT + t;
+            if (c < n4) {
+                operand<CW>(a, xr, zr, CW * c, v[e], sz[e]);
+#pragma unroll
+                for (int k = 0; k < CW; ++k) ss += a.r_x ? rbf(v[e][k] * v[e][k]) : v[e][k] * v[e][k];
+            }
+        }
+    } else {
+        for (int64_t c = t; c < n4; c += NT) {
+            float vv[CW], zz[CW];
+            operand<CW>(a, xr, zr, CW * c, vv, zz);
+#pragma unroll
+            for (int k = 0; k < CW; ++k) ss += a.r_x ? rbf(vv[k] * vv[k]) : vv[k] * vv[k];
+        }
+    }
+    const float tot = block_sum<NT>(ss, red);
+    float ms = tot / (float)a.gs;
+    if (a.r_x) ms = rbf(ms);
+    float den = ms + a.eps;
+    if (a.r_x) den = rbf(den);
+    float rms = sqrtf(den);
+    if (a.r_x) rms = rbf(rms);
+    const float inv = 1.f / rms;
+    if (resident) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int64_t c = (int64_t)e * NT + t;
+            if (c < n4) output<CW>(a, orow, a.w, CW * c, gofs + CW * c, inv, v[e], sz[e]);
+        }
+    } else {
+        for (int64_t c = t; c < n4; c += NT) {
+            float vv[CW], zz[CW];
+            operand<CW>(a, xr, zr, CW * c, vv, zz);
+            output<CW>(a, orow, a.w, CW * c, gofs + CW * c, inv, vv, zz);
+        }
+    }
+}
+
+bool aligned_to(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+}  // namespace
+
+namespace m2 {
+
+int launch_rms_norm_gated(const m2_rms_norm_gated_args& a, hipStream_t s) {
+    const char* who = "rms_norm_gated";
+    M2_REQUIRE(a.x && a.weight && a.out, M2_ERR_INVALID, "%s: x, weight and out are required", who);
+    M2_REQUIRE(a.rows > 0 && a.hidden > 0 && a.group_size > 0 && a.hidden % a.group_size == 0,
+               M2_ERR_INVALID, "%s: bad sizes (hidden %% group_size must be 0)", who);
+    for (int d : {a.x_dtype, a.w_dtype, a.out_dtype})
+        M2_REQUIRE(d == M2_F32 || d == M2_BF16, M2_ERR_UNSUPPORTED, "%s: dtype %d", who, d);
+    M2_REQUIRE(!a.z || a.z_dtype == M2_F32 || a.z_dtype == M2_BF16, M2_ERR_UNSUPPORTED,
+               "%s: z dtype %d", who, a.z_dtype);
+    const bool zb = a.z && a.z_dtype == M2_BF16;
+    const bool gate_first = a.z && !a.norm_before_gate, gate_after = a.z && a.norm_before_gate;
+    // dtypes of the reference's intermediates (bf16 only when all operands are)
+    const bool xdt_bf = a.x_dtype == M2_BF16 && (!gate_first || zb);
+    const bool wdt_bf = xdt_bf && a.w_dtype == M2_BF16;
+    const bool odt_bf = wdt_bf && (!gate_after || zb);
+    M2_REQUIRE(a.out_dtype == (odt_bf ? M2_BF16 : M2_F32), M2_ERR_INVALID,
+               "%s: out_dtype must be the result dtype %d", who, odt_bf ? M2_BF16 : M2_F32);
+    const int64_t nblocks = a.rows * (a.hidden / a.group_size);
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "%s: too many rows", who);
+
+    NormArgs k{};
+    k.x = a.x; k.z = a.z; k.w = a.weight; k.out = a.out;
+    k.x_rs = a.x_row_stride; k.z_rs = a.z_row_stride; k.o_rs = a.out_row_stride;
+    k.hidden = a.hidden; k.gs = a.group_size; k.ngroups = a.hidden / a.group_size; k.eps = a.eps;
+    k.x_bf16 = a.x_dtype == M2_BF16; k.z_bf16 = zb; k.w_bf16 = a.w_dtype == M2_BF16;
+    k.o_bf16 = odt_bf;
+    k.gate_first = gate_first; k.gate_after = gate_after;
+    k.r_x = xdt_bf; k.r_w = wdt_bf; k.r_o = odt_bf;
+    // 4-element chunks: every row and group start a multiple of 4 elements on
+    // a 4-element-aligned base, as one access each when also aligned
+    const int xs = a.x_dtype == M2_BF16 ? 2 : 4, os = odt_bf ? 2 : 4, ws = a.w_dtype == M2_BF16 ? 2 : 4;
+    bool c4 = a.group_size % 4 == 0 && a.x_row_stride % 4 == 0 && a.out_row_stride % 4 == 0 &&
+              (!a.z || a.z_row_stride % 4 == 0);
+    bool vec = c4 && aligned_to(a.x, 4 * xs) && aligned_to(a.out, 4 * os) && aligned_to(a.weight, 4 * ws);
+    if (a.z) vec = vec && aligned_to(a.z, 4 * (zb ? 2 : 4));
+    k.vec = vec;
+    const dim3 grid((unsigned)nblocks);
+    if (c4) {
+        const int64_t n4 = a.group_size / 4;
+        if (n4 <= 64 * 4) hipLaunchKernelGGL((k_rms_norm<64, 4, 4>), grid, dim3(64), 0, s, k);
+        else if (n4 <= 256 * 2) hipLaunchKernelGGL((k_rms_norm<256, 2, 4>), grid, dim3(256), 0, s, k);
+        else if (n4 <= 256 * 4) hipLaunchKernelGGL((k_rms_norm<256, 4, 4>), grid, dim3(256), 0, s, k);
+        else hipLaunchKernelGGL((k_rms_norm<256, 8, 4>), grid, dim3(256), 0, s, k);
+    } else {
+        if (a.group_size <= 64 * 8) hipLaunchKernelGGL((k_rms_norm<64, 8, 1>), grid, dim3(64), 0, s, k);
+        else hipLaunchKernelGGL((k_rms_norm<256, 16, 1>), grid, dim3(256), 0, s, k);
+    }
+    return check_launch(who);
+}
+
+}  // namespace m2

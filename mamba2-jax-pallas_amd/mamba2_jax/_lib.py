@@ -115,6 +115,14 @@ class CausalConv1dUpdateArgs(ctypes.Structure):
                 ("w_dtype", _i32), ("bias_dtype", _i32), ("out_dtype", _i32), ("silu", _i32)]
 
 
+class RmsNormGatedArgs(ctypes.Structure):
+    _fields_ = [("x", _c_p), ("z", _c_p), ("weight", _c_p), ("out", _c_p),
+                ("x_row_stride", _i64), ("z_row_stride", _i64), ("out_row_stride", _i64),
+                ("rows", _i64), ("hidden", _i64), ("group_size", _i64), ("eps", _f32),
+                ("x_dtype", _i32), ("z_dtype", _i32), ("w_dtype", _i32), ("out_dtype", _i32),
+                ("norm_before_gate", _i32)]
+
+
 # entry point name -> argument struct (every function declared in m2ssd.h)
 ENTRY_POINTS = {
     "m2_chunk_cumsum": ChunkCumsumArgs,
@@ -127,6 +135,7 @@ ENTRY_POINTS = {
     "m2_selective_state_update": SsuArgs,
     "m2_causal_conv1d": CausalConv1dArgs,
     "m2_causal_conv1d_update": CausalConv1dUpdateArgs,
+    "m2_rms_norm_gated": RmsNormGatedArgs,
 }
 OTHER_SYMBOLS = ("m2_ssd_combined_workspace_size", "m2_last_error", "m2_abi_version")
 
