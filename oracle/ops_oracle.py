@@ -7,6 +7,8 @@ checker -- never as a product path.  The product (``mamba2_jax``) runs the HIP
 kernels in ``libm2ssd.so`` and has no CPU path.
 
 NumPy restatement of
+  * ``/root/reference/src/mamba2_jax/modules/mamba2.py:296-549`` (the mixer
+    layer, composed from the pieces below);
   * ``/root/reference/src/mamba2_jax/ops/causal_conv1d.py`` (causal_conv1d
     :18-85, causal_conv1d_update :88-139, _mask_sequence_boundaries :142-193);
   * ``/root/reference/src/mamba2_jax/ops/rms_norm.py:15-92`` (rms_norm_gated).
@@ -26,6 +28,9 @@ How each function is pinned (tests/test_oracle_ops.py):
   rms_norm_gated        the reference tests' closed forms
                         (tests/test_mamba2_ops.py:205-296): plain, gated before
                         and after the norm, grouped; scale invariance
+  mamba2_layer          a composition of the pinned pieces; prefill of T tokens
+                        == T decode steps through the conv update and the
+                        token recurrence (tests/test_oracle_ops.py)
 """
 
 from __future__ import annotations
@@ -196,3 +201,101 @@ def rms_norm_gated(x, weight, z=None, eps=1e-5, group_size=None, norm_before_gat
         dt = promote(dt, z_dtype)
         out = np.asarray(_rf(dt == "bfloat16")(out * silu(z, zb)), np.float64)
     return out, dt
+
+
+# ---------------------------------------------------------------------------
+# Mamba2 mixer layer (reference modules/mamba2.py:296-549), float32 weights
+# ---------------------------------------------------------------------------
+
+def mamba2_layer(p, u, cfg, seq_idx=None, dtype="float32"):
+    """Prefill of one Mamba2 layer from the oracle pieces above and
+    ssd_oracle.ssd_combined: in-projection, conv + SiLU, SSD, gated RMSNorm,
+    MLP bypass, out-projection (reference modules/mamba2.py:296-414).
+
+    p: parameter arrays by reference name; cfg: dict with d_ssm, d_mlp,
+    ngroups, d_state, headdim, nheads, chunk_size, rmsnorm, norm_before_gate,
+    D_has_hdim, dt_limit.  dtype: the parameters' (and so the activations')
+    dtype; with "bfloat16" the projections' outputs, the conv and the SSD's
+    internal casts are rounded to bf16 and the norm output is cast to bf16
+    before the out-projection, as the reference's arrays are.
+    Returns (out, final_states, conv_state).
+    """
+    from .ssd_oracle import ssd_combined
+    bf = dtype == "bfloat16"
+    r = _rf(bf)
+    u = np.asarray(u, np.float64)
+    b, L, _ = u.shape
+    dssm, dmlp, G, N = cfg["d_ssm"], cfg["d_mlp"], cfg["ngroups"], cfg["d_state"]
+    H, P = cfg["nheads"], cfg["headdim"]
+    zx = np.asarray(r(u @ np.asarray(p["in_proj_kernel"], np.float64)), np.float64)
+    if p.get("in_proj_bias") is not None:
+        zx = np.asarray(r(zx + p["in_proj_bias"]), np.float64)
+    o = np.cumsum([0, dmlp, dmlp, dssm, dssm + 2 * G * N, H])
+    z0, x0, z, xBC, dt = (zx[..., o[i]:o[i + 1]] for i in range(5))
+    d_conv = p["conv1d_weight"].shape[1]
+    xT = xBC.transpose(0, 2, 1)
+    conv_state = (xT[:, :, -d_conv:] if L >= d_conv
+                  else np.concatenate([np.zeros((b, xT.shape[1], d_conv - L)), xT], 2))
+    xc, _ = causal_conv1d(xT, p["conv1d_weight"], p.get("conv1d_bias"), "silu", seq_idx,
+                          dtype, dtype, dtype)
+    xc = xc.transpose(0, 2, 1)
+    x = xc[..., :dssm].reshape(b, L, H, P)
+    B = xc[..., dssm:dssm + G * N].reshape(b, L, G, N)
+    C = xc[..., dssm + G * N:].reshape(b, L, G, N)
+    A = -np.exp(np.asarray(p["A_log"], np.float64))
+    D = np.asarray(p["D"], np.float64)
+    if cfg["D_has_hdim"]:
+        D = D.reshape(H, P)
+    zs = None if cfg["rmsnorm"] else z.reshape(b, L, H, P)
+    y, fin = ssd_combined(x, dt, A, B, C, cfg["chunk_size"], D=D, z=zs, dt_bias=p["dt_bias"],
+                          seq_idx=seq_idx, dt_softplus=True, dt_limit=cfg["dt_limit"],
+                          return_final_states=True, io_dtype="bf16" if bf else "f32")
+    y = y.reshape(b, L, dssm)
+    if cfg["rmsnorm"]:
+        y, _ = rms_norm_gated(y, p["norm_weight"], z=z, group_size=dssm // G,
+                              norm_before_gate=cfg["norm_before_gate"], w_dtype=dtype,
+                              z_dtype=dtype)
+    if dmlp > 0:
+        y = np.concatenate([r(silu(z0, bf) * x0), y], -1)
+    y = np.asarray(r(y), np.float64)                  # cast to the out-projection's dtype
+    out = np.asarray(r(y @ np.asarray(p["out_proj_kernel"], np.float64)), np.float64)
+    if p.get("out_proj_bias") is not None:
+        out = np.asarray(r(out + p["out_proj_bias"]), np.float64)
+    return out, fin, conv_state
+
+
+def mamba2_layer_step(p, u_t, conv_state, ssm_state, cfg):
+    """One decode token of the layer (reference modules/mamba2.py:427-549):
+    the conv update, the selective state update (no dt_limit clamp, as the
+    reference's decode), the gated norm and the projections.
+    u_t (b, d_model) -> (out (b, d_model), new conv_state, new ssm_state)."""
+    from .ssd_oracle import selective_state_update
+    u_t = np.asarray(u_t, np.float64)
+    b = u_t.shape[0]
+    dssm, dmlp, G, N = cfg["d_ssm"], cfg["d_mlp"], cfg["ngroups"], cfg["d_state"]
+    H, P = cfg["nheads"], cfg["headdim"]
+    zx = u_t @ np.asarray(p["in_proj_kernel"], np.float64)
+    if p.get("in_proj_bias") is not None:
+        zx = zx + p["in_proj_bias"]
+    o = np.cumsum([0, dmlp, dmlp, dssm, dssm + 2 * G * N, H])
+    z0, x0, z, xBC, dt = (zx[..., o[i]:o[i + 1]] for i in range(5))
+    conv_state, xc, _, _ = causal_conv1d_update(xBC, conv_state, p["conv1d_weight"],
+                                                p.get("conv1d_bias"), "silu")
+    A = -np.exp(np.asarray(p["A_log"], np.float64))
+    D = np.asarray(p["D"], np.float64)
+    if cfg["D_has_hdim"]:
+        D = D.reshape(H, P)
+    zs = None if cfg["rmsnorm"] else z.reshape(b, H, P)
+    ssm_state, y = selective_state_update(
+        ssm_state, xc[:, :dssm].reshape(b, H, P), dt, A, xc[:, dssm:dssm + G * N].reshape(b, G, N),
+        xc[:, dssm + G * N:].reshape(b, G, N), D=D, z=zs, dt_bias=p["dt_bias"], dt_softplus=True)
+    y = y.reshape(b, dssm)
+    if cfg["rmsnorm"]:
+        y, _ = rms_norm_gated(y, p["norm_weight"], z=z, group_size=dssm // G,
+                              norm_before_gate=cfg["norm_before_gate"])
+    if dmlp > 0:
+        y = np.concatenate([z0 / (1 + np.exp(-z0)) * x0, y], -1)
+    out = y @ np.asarray(p["out_proj_kernel"], np.float64)
+    if p.get("out_proj_bias") is not None:
+        out = out + p["out_proj_bias"]
+    return out, conv_state, ssm_state

@@ -1,0 +1,126 @@
+"""The Mamba2 mixer layer (mamba2_jax.modules.Mamba2) on the GPU: in-projection,
+conv + SiLU (split straight into x / B / C), SSD, gated RMSNorm, MLP bypass,
+out-projection -- against the CPU oracle's composition of the same steps, and
+the decode step (conv update + selective state update, states in place)
+against the prefill (reference tests/test_mamba2_vs_torch.py:312-408).
+Tolerance: the BASELINE parity bar, max|err| / rms(reference) <= 1e-3 (fp32
+parameters) or 2e-2 (bf16).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TOL, announce, check, dev, host
+from mamba2_jax.modules import Mamba2, allocate_inference_cache
+from oracle import ops_oracle as X
+
+pytestmark = pytest.mark.gpu
+
+
+def _params(m):
+    return {k: host(v) for k, v in m.named_parameters()}
+
+
+def _cfg(m):
+    return dict(d_ssm=m._d_ssm, d_mlp=m.d_mlp, ngroups=m.ngroups, d_state=m.d_state,
+                headdim=m.headdim, nheads=m.nheads, chunk_size=m.chunk_size, rmsnorm=m.rmsnorm,
+                norm_before_gate=m.norm_before_gate, D_has_hdim=m.D_has_hdim,
+                dt_limit=m.dt_limit)
+
+
+def _randomize(m, seed):
+    """Non-trivial D, norm weight and biases (their inits are ones / zeros)."""
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name in ("D", "norm_weight"):
+            t = getattr(m, name)
+            if t is not None:
+                t.copy_((torch.rand(t.shape, generator=g) + 0.5).to(t))
+        for name in ("conv1d_bias", "in_proj_bias", "out_proj_bias"):
+            t = getattr(m, name)
+            if t is not None:
+                t.copy_((torch.randn(t.shape, generator=g) * 0.1).to(t))
+
+
+VARIANTS = {
+    "plain": {},
+    "mlp+bias+Dhdim": dict(d_ssm=128, bias=True, D_has_hdim=True),
+    "gate-after-norm": dict(norm_before_gate=True),
+    "no-rmsnorm": dict(rmsnorm=False),
+}
+
+
+@pytest.mark.parametrize("variant", list(VARIANTS))
+def test_layer_prefill_fp32(variant):
+    announce("Mamba2 prefill fp32", variant)
+    torch.manual_seed(0)
+    m = Mamba2(d_model=128, d_state=64, headdim=64, ngroups=2, chunk_size=64, seed=1,
+               **VARIANTS[variant])
+    _randomize(m, 2)
+    rng = np.random.default_rng(3)
+    u = rng.standard_normal((2, 100, 128)).astype(np.float32)
+    got = m(dev(u))
+    want, _, _ = X.mamba2_layer(_params(m), u, _cfg(m))
+    check(got, want, TOL["f32"], f"layer out ({variant})")
+
+
+def test_layer_prefill_seq_idx():
+    """packed sequences: seq_idx reaches the conv mask and the SSD."""
+    announce("Mamba2 prefill with seq_idx")
+    m = Mamba2(d_model=128, d_state=64, headdim=64, ngroups=2, chunk_size=64, seed=4)
+    _randomize(m, 5)
+    rng = np.random.default_rng(6)
+    L = 150
+    u = rng.standard_normal((1, L, 128)).astype(np.float32)
+    seq = np.repeat(np.arange(3), [40, 70, 40])[None].astype(np.int32)
+    got = m(dev(u), seq_idx=dev(seq))
+    want, _, _ = X.mamba2_layer(_params(m), u, _cfg(m), seq_idx=seq)
+    check(got, want, TOL["f32"], "layer out (seq_idx)")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_layer_decode_continues_prefill(dtype):
+    """prefill T0 tokens with a cache, then decode T1 tokens one by one: the
+    outputs equal the prefill of all T0 + T1 tokens, and the cache tensors
+    are updated in place."""
+    announce("Mamba2 prefill + decode", dtype)
+    pd = torch.bfloat16 if dtype == "bf16" else torch.float32
+    m = Mamba2(d_model=128, d_state=64, headdim=64, ngroups=2, chunk_size=64, seed=7,
+               param_dtype=pd)
+    _randomize(m, 8)
+    rng = np.random.default_rng(9)
+    b, T0, T1 = 3, 70, 12
+    u = dev(rng.standard_normal((b, T0 + T1, 128)).astype(np.float32), pd)
+    full = m(u)
+    cache = allocate_inference_cache(b, 128, d_state=64, headdim=64, ngroups=2)
+    cs_ptr, ss_ptr = cache["conv_state"].data_ptr(), cache["ssm_state"].data_ptr()
+    out0, cache = m(u[:, :T0], inference_params=cache)
+    assert cache["seqlen_offset"] == T0
+    check(out0, host(full[:, :T0]), 1e-5 if dtype == "f32" else 1e-2, "prefill with cache")
+    outs = []
+    for t in range(T0, T0 + T1):
+        o, cache = m(u[:, t:t + 1], inference_params=cache)
+        outs.append(o)
+    assert cache["seqlen_offset"] == T0 + T1
+    assert cache["conv_state"].data_ptr() == cs_ptr and cache["ssm_state"].data_ptr() == ss_ptr
+    check(torch.cat(outs, 1), host(full[:, T0:]), TOL[dtype], "decode == prefill")
+    if dtype == "f32":
+        want, fin, conv_state = X.mamba2_layer(_params(m), host(u), _cfg(m))
+        check(torch.cat(outs, 1), want[:, T0:], TOL["f32"], "decode vs oracle")
+        check(cache["ssm_state"], fin, TOL["f32"], "final ssm state vs oracle")
+        np.testing.assert_allclose(host(cache["conv_state"]), conv_state, rtol=1e-6, atol=1e-6)
+
+
+def test_layer_nemotron_shape_bf16():
+    """one nemotron-h-8b mixer (d_model 4096, 128 heads x 64, 8 groups,
+    d_state 128, chunk 128) in bf16 over 512 tokens against the oracle."""
+    announce("Mamba2 nemotron-h-8b shape bf16")
+    m = Mamba2(d_model=4096, d_state=128, headdim=64, ngroups=8, chunk_size=128, seed=10,
+               param_dtype=torch.bfloat16)
+    _randomize(m, 11)
+    rng = np.random.default_rng(12)
+    u = rng.standard_normal((1, 512, 4096)).astype(np.float32)
+    got = m(dev(u, torch.bfloat16))
+    want, _, _ = X.mamba2_layer(_params(m), host(dev(u, torch.bfloat16)), _cfg(m), dtype="bfloat16")
+    check(got, want, TOL["bf16"], "layer out (bf16, nemotron-h-8b shape)")

@@ -145,3 +145,54 @@ def test_promote():
     assert X.promote("bfloat16", "bfloat16") == "bfloat16"
     assert X.promote("bfloat16", "float32") == "float32"
     assert X.promote("bfloat16", None) == "bfloat16"
+
+
+def _layer_params(rng, d_model=16, d_state=8, d_conv=4, expand=2, headdim=8, ngroups=2,
+                  d_ssm=None, D_has_hdim=False, bias=False):
+    d_inner = expand * d_model
+    dssm = d_inner if d_ssm is None else d_ssm
+    H = dssm // headdim
+    conv_dim = dssm + 2 * ngroups * d_state
+    d_in_proj = 2 * d_inner + 2 * ngroups * d_state + H
+    p = {"in_proj_kernel": rng.standard_normal((d_model, d_in_proj)) / np.sqrt(d_model),
+         "out_proj_kernel": rng.standard_normal((d_inner, d_model)) / np.sqrt(d_inner),
+         "conv1d_weight": rng.standard_normal((conv_dim, d_conv)) / 2,
+         "conv1d_bias": rng.standard_normal(conv_dim) * 0.1,
+         "dt_bias": np.log(np.expm1(rng.uniform(0.01, 0.1, H))),
+         "A_log": np.log(rng.uniform(1, 16, H)),
+         "D": rng.uniform(0.5, 1.5, dssm if D_has_hdim else H),
+         "norm_weight": rng.uniform(0.5, 1.5, dssm)}
+    if bias:
+        p["in_proj_bias"] = rng.standard_normal(d_in_proj) * 0.1
+        p["out_proj_bias"] = rng.standard_normal(d_model) * 0.1
+    cfg = dict(d_ssm=dssm, d_mlp=d_inner - dssm, ngroups=ngroups, d_state=d_state, headdim=headdim,
+               nheads=H, chunk_size=8, rmsnorm=True, norm_before_gate=False,
+               D_has_hdim=D_has_hdim, dt_limit=(0.0, float("inf")))
+    return p, cfg
+
+
+@pytest.mark.parametrize("variant", ["plain", "mlp+bias+Dhdim", "no-rmsnorm"])
+def test_layer_prefill_equals_decode_steps(variant):
+    """reference tests/test_mamba2_vs_torch.py:312-408: the layer's chunked
+    prefill over T tokens equals T decode steps (conv update + token
+    recurrence) from zero states, output by output, and ends in the same states."""
+    rng = _rng(11)
+    kw = {"plain": {}, "mlp+bias+Dhdim": dict(d_ssm=16, D_has_hdim=True, bias=True),
+          "no-rmsnorm": {}}[variant]
+    p, cfg = _layer_params(rng, **kw)
+    if variant == "no-rmsnorm":
+        cfg["rmsnorm"] = False
+    b, T = 2, 21
+    u = rng.standard_normal((b, T, 16))
+    full, fin, conv_state = X.mamba2_layer(p, u, cfg)
+    cs = np.zeros_like(conv_state)
+    ss = np.zeros((b, cfg["nheads"], cfg["headdim"], cfg["d_state"]))
+    # the chunked path rounds the passed states, CB and C @ states to the
+    # input dtype (float32 here) as the reference does, so agreement is to
+    # ~1e-7 of the output scale
+    scale = np.sqrt(np.mean(full ** 2))
+    for t in range(T):
+        out, cs, ss = X.mamba2_layer_step(p, u[:, t], cs, ss, cfg)
+        assert np.max(np.abs(out - full[:, t])) <= 1e-6 * scale, t
+    assert np.max(np.abs(ss - fin)) <= 1e-6 * np.sqrt(np.mean(fin ** 2))
+    np.testing.assert_array_equal(cs, conv_state)
