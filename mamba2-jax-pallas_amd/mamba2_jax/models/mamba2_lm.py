@@ -1,0 +1,243 @@
+"""The Mamba2 language model on MI355X: prefill, and the token-by-token decode
+loop that consumes the in-place decode kernels (reference
+models/mamba2_lm.py:36-736).
+
+Same config fields, parameter dict structure, call signatures and returns as
+the reference (``__call__(params, input_ids) -> logits``, ``generate``).
+Parameters are torch tensors on the GPU (``init_params`` makes random ones of
+the architecture; loading checkpoint files is not part of this module).
+
+Decode, MI355X-first: every layer's conv and SSM state lives in one
+(n_layer, ...) tensor that the decode kernels update in place, so a step
+allocates no state; the whole step (embedding gather, n_layer x [RMSNorm,
+in-projection, conv update, selective state update, gated norm,
+out-projection, residual], final norm, LM head) is captured once into a HIP
+graph and replayed per token (``generate(..., use_graph=True)``), which
+removes the per-kernel launch cost that dominates a small-batch step.  The
+reference gets the equivalent from jax.jit + lax.scan over layers
+(:667-736).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from ..modules.mamba2 import MixerDims, _lecun_normal, mamba2_block_forward, mamba2_block_step
+from ..ops.rms_norm import rms_norm_gated
+
+
+@dataclass
+class Mamba2Config:
+    """Configuration of a Mamba2 language model (reference :36-83)."""
+    d_model: int = 2048
+    n_layer: int = 48
+    vocab_size: int = 50277
+    pad_vocab_size_multiple: int = 16
+    d_state: int = 128
+    d_conv: int = 4
+    expand: int = 2
+    headdim: int = 64
+    ngroups: int = 1
+    chunk_size: int = 256
+    rmsnorm: bool = True
+    norm_before_gate: bool = False
+    bias: bool = False
+    conv_bias: bool = True
+    D_has_hdim: bool = False
+    tie_embeddings: bool = True
+    residual_in_fp32: bool = True
+    dt_limit: tuple = (0.0, float("inf"))
+
+    @property
+    def vocab_size_padded(self):
+        return math.ceil(self.vocab_size / self.pad_vocab_size_multiple) * self.pad_vocab_size_multiple
+
+    @property
+    def d_inner(self):
+        return self.expand * self.d_model
+
+    @property
+    def nheads(self):
+        return self.d_inner // self.headdim
+
+    @property
+    def conv_dim(self):
+        return self.d_inner + 2 * self.ngroups * self.d_state
+
+    @property
+    def d_in_proj(self):
+        return 2 * self.d_inner + 2 * self.ngroups * self.d_state + self.nheads
+
+    def mixer_dims(self):
+        return MixerDims(d_ssm=self.d_inner, d_mlp=0, ngroups=self.ngroups, d_state=self.d_state,
+                         headdim=self.headdim, nheads=self.nheads, d_conv=self.d_conv,
+                         chunk_size=self.chunk_size, rmsnorm=self.rmsnorm,
+                         norm_before_gate=self.norm_before_gate, D_has_hdim=self.D_has_hdim,
+                         dt_limit=tuple(self.dt_limit))
+
+
+def rms_norm(x, weight, eps=1e-5):
+    """Plain RMSNorm over the last dimension (reference :136-139), as the HIP
+    rms_norm_gated kernel without a gate."""
+    return rms_norm_gated(x, weight, z=None, eps=eps)
+
+
+def init_params(cfg: Mamba2Config, dtype=torch.bfloat16, device=None, seed=0):
+    """Random parameters of the architecture in the reference's dict layout
+    (class docstring of Mamba2LMHeadModel, reference :142-174)."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    g = torch.Generator().manual_seed(seed)
+    emb = (torch.randn((cfg.vocab_size_padded, cfg.d_model), generator=g) * 0.02).to(dev, dtype)
+    layers = []
+    for _ in range(cfg.n_layer):
+        u = torch.rand(cfg.nheads, generator=g, dtype=torch.float64)
+        dt = torch.exp(u * (math.log(0.1) - math.log(0.001)) + math.log(0.001)).clamp(min=1e-4)
+        mixer = {
+            "in_proj_kernel": _lecun_normal((cfg.d_model, cfg.d_in_proj), cfg.d_model, g, dev, dtype),
+            "conv1d_weight": _lecun_normal((cfg.conv_dim, cfg.d_conv), cfg.d_conv, g, dev, dtype),
+            "conv1d_bias": (torch.randn(cfg.conv_dim, generator=g) * 0.02).to(dev, dtype)
+            if cfg.conv_bias else None,
+            "dt_bias": (dt + torch.log(-torch.expm1(-dt))).to(dev, torch.float32),
+            "A_log": torch.log(torch.rand(cfg.nheads, generator=g) * 15 + 1).to(dev, torch.float32),
+            "D": torch.ones(cfg.d_inner if cfg.D_has_hdim else cfg.nheads, device=dev),
+            "norm_weight": torch.ones(cfg.d_inner, device=dev, dtype=dtype) if cfg.rmsnorm else None,
+            # scaled down so that the residual stream stays O(1) over many layers
+            "out_proj_kernel": _lecun_normal((cfg.d_inner, cfg.d_model), cfg.d_inner, g, dev, dtype)
+            / math.sqrt(2 * cfg.n_layer),
+        }
+        if cfg.bias:
+            mixer["in_proj_bias"] = torch.zeros(cfg.d_in_proj, device=dev, dtype=dtype)
+            mixer["out_proj_bias"] = torch.zeros(cfg.d_model, device=dev, dtype=dtype)
+        layers.append({"norm_weight": torch.ones(cfg.d_model, device=dev, dtype=dtype),
+                       "mixer": mixer})
+    return {"embedding": {"weight": emb}, "layers": layers,
+            "norm_f_weight": torch.ones(cfg.d_model, device=dev, dtype=dtype),
+            "lm_head_weight": emb}
+
+
+def _sample_token(logits, generator, temperature=1.0, top_k=50):
+    """Greedy when temperature == 0, else top-k sampling (reference :648-664)."""
+    if temperature == 0:
+        return torch.argmax(logits, dim=-1)
+    logits = logits.float() / temperature
+    if top_k > 0:
+        kth = torch.topk(logits, top_k, dim=-1).values[:, -1:]
+        logits = torch.where(logits < kth, torch.full_like(logits, -1e10), logits)
+    return torch.multinomial(torch.softmax(logits, -1), 1, generator=generator)[:, 0]
+
+
+class DecodeState:
+    """Per-layer decode states stacked over layers, updated in place:
+    conv (n_layer, batch, conv_dim, d_conv) and ssm (n_layer, batch, nheads,
+    headdim, d_state), both float32."""
+
+    def __init__(self, cfg: Mamba2Config, batch: int, device=None):
+        dev = torch.device("cuda") if device is None else torch.device(device)
+        self.conv = torch.zeros((cfg.n_layer, batch, cfg.conv_dim, cfg.d_conv), device=dev)
+        self.ssm = torch.zeros((cfg.n_layer, batch, cfg.nheads, cfg.headdim, cfg.d_state), device=dev)
+
+
+class Mamba2LMHeadModel:
+    """Mamba2 LM for inference over a parameter dict (reference :142-351)."""
+
+    def __init__(self, config: Mamba2Config):
+        self.config = config
+        self._graph = None
+
+    # -- prefill -------------------------------------------------------------
+    def _layers(self, params, x, state=None):
+        cfg = self.config
+        d = cfg.mixer_dims()
+        rdt = torch.float32 if cfg.residual_in_fp32 else x.dtype
+        for i, lp in enumerate(params["layers"]):
+            residual = x.to(rdt)
+            xn = rms_norm(x.float(), lp["norm_weight"])
+            if state is None:
+                out, _, _ = mamba2_block_forward(xn, lp["mixer"], d)
+            else:
+                out, _, _ = mamba2_block_forward(xn, lp["mixer"], d, with_cache=True,
+                                                 conv_state=state.conv[i], ssm_state=state.ssm[i])
+            x = residual + out.to(rdt)
+        return x
+
+    def _head(self, params, x):
+        x = rms_norm(x.float(), params["norm_f_weight"])
+        w = params["lm_head_weight"]
+        return x.to(w.dtype) @ w.t()
+
+    def __call__(self, params, input_ids):
+        """input_ids (batch, seqlen) -> logits (batch, seqlen, vocab_size_padded)."""
+        x = params["embedding"]["weight"][input_ids]
+        return self._head(params, self._layers(params, x))
+
+    def prefill(self, params, input_ids, state: DecodeState):
+        """Prefill that leaves every layer's conv / ssm state in ``state``
+        (reference _forward_with_cache, :304-351); -> logits of the last token."""
+        x = params["embedding"]["weight"][input_ids]
+        return self._head(params, self._layers(params, x, state))[:, -1, :]
+
+    # -- decode ----------------------------------------------------------------
+    def decode_step(self, params, token, state: DecodeState):
+        """token (batch,) -> next-token logits (batch, vocab); states in place
+        (reference _scan_decode_step, :667-736)."""
+        cfg = self.config
+        d = cfg.mixer_dims()
+        rdt = torch.float32 if cfg.residual_in_fp32 else params["embedding"]["weight"].dtype
+        x = params["embedding"]["weight"][token]
+        for i, lp in enumerate(params["layers"]):
+            residual = x.to(rdt)
+            xn = rms_norm(x.float(), lp["norm_weight"])
+            out, _, _ = mamba2_block_step(xn, lp["mixer"], d, state.conv[i], state.ssm[i])
+            x = residual + out.to(rdt)
+        return self._head(params, x)
+
+    def capture_decode(self, params, state: DecodeState, warmup=2):
+        """Capture decode_step into a HIP graph over static token / logits
+        buffers; returns (graph, token_buffer, logits_buffer).  Replaying it
+        advances ``state`` by one token.  The warm-up steps run on copies of
+        the states, which are restored before capture."""
+        batch = state.conv.shape[1]
+        tok = torch.zeros(batch, dtype=torch.long, device=state.conv.device)
+        saved = (state.conv.clone(), state.ssm.clone())
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                self.decode_step(params, tok, state)
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            logits = self.decode_step(params, tok, state)
+        state.conv.copy_(saved[0])
+        state.ssm.copy_(saved[1])
+        return g, tok, logits
+
+    def generate(self, params, input_ids, max_new_tokens: int = 50, temperature: float = 1.0,
+                 top_k: int = 50, rng_key=None, use_graph: bool = True):
+        """Autoregressive generation (reference :219-302) -> (batch,
+        prompt_len + max_new_tokens) token ids.  Batches of any size decode
+        together; rng_key: an int seed or a torch.Generator."""
+        batch = input_ids.shape[0]
+        gen = rng_key if isinstance(rng_key, torch.Generator) else \
+            torch.Generator(device=input_ids.device).manual_seed(0 if rng_key is None else int(rng_key))
+        state = DecodeState(self.config, batch, input_ids.device)
+        logits = self.prefill(params, input_ids, state)
+        ids = [input_ids]
+        graph = self.capture_decode(params, state) if use_graph else None
+        for _ in range(max_new_tokens):
+            nxt = _sample_token(logits, gen, temperature, top_k)
+            ids.append(nxt[:, None])
+            if graph is not None:
+                g, tok, out = graph
+                tok.copy_(nxt)
+                g.replay()
+                logits = out
+            else:
+                logits = self.decode_step(params, nxt, state)
+        return torch.cat(ids, dim=1)
+
+
+__all__ = ["Mamba2Config", "Mamba2LMHeadModel", "DecodeState", "init_params", "rms_norm"]

@@ -24,6 +24,7 @@ them runs in libm2ssd.so:
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 from typing import Optional, Tuple
 
 import torch
@@ -119,96 +120,151 @@ class Mamba2(torch.nn.Module):
         self.D = P(torch.ones(self._d_ssm if D_has_hdim else self.nheads, device=dev, dtype=pd))
         self.norm_weight = P(torch.ones(self._d_ssm, device=dev, dtype=pd)) if rmsnorm else None
 
-    # -- helpers -----------------------------------------------------------
-    def _A(self):
-        return -torch.exp(self.A_log.float())
+    def dims(self):
+        return MixerDims(d_ssm=self._d_ssm, d_mlp=self.d_mlp, ngroups=self.ngroups,
+                         d_state=self.d_state, headdim=self.headdim, nheads=self.nheads,
+                         d_conv=self.d_conv, chunk_size=self.chunk_size, rmsnorm=self.rmsnorm,
+                         norm_before_gate=self.norm_before_gate, D_has_hdim=self.D_has_hdim,
+                         dt_limit=self.dt_limit)
 
-    def _D(self):
-        return self.D.view(self.nheads, self.headdim) if self.D_has_hdim else self.D
+    def params(self):
+        """The parameters by reference name (absent optional ones as None)."""
+        return {k: getattr(self, k) for k in _PARAM_NAMES}
 
-    def _in_proj(self, h):
-        z = h @ self.in_proj_kernel
-        return z if self.in_proj_bias is None else z + self.in_proj_bias
-
-    def _out(self, y, z, z0, x0):
-        """gated RMSNorm, the MLP bypass, out-projection (reference :400-414)."""
-        if self.rmsnorm:
-            y = rms_norm_gated(y, self.norm_weight, z=z, group_size=self._d_ssm // self.ngroups,
-                               norm_before_gate=self.norm_before_gate)
-        if self.d_mlp > 0:
-            y = torch.cat([torch.nn.functional.silu(z0) * x0, y.to(x0.dtype)], dim=-1)
-        y = y.to(self.out_proj_kernel.dtype)
-        out = y @ self.out_proj_kernel
-        return out if self.out_proj_bias is None else out + self.out_proj_bias
-
-    # -- forward -----------------------------------------------------------
     def forward(self, u, seq_idx=None, cu_seqlens=None, inference_params=None):
         """u (batch, seqlen, d_model) -> out (batch, seqlen, d_model), plus the
         new inference_params dict when inference_params is given
         (reference modules/mamba2.py:163-424)."""
         if inference_params is not None and inference_params.get("seqlen_offset", 0) > 0:
-            return self._step(u, inference_params)
-        batch, seqlen, _ = u.shape
-        G, N, H, Pd = self.ngroups, self.d_state, self.nheads, self.headdim
-        zxbcdt = self._in_proj(u.to(self.in_proj_kernel.dtype))
-        z0, x0, z, xBC, dt = _split_last(
-            zxbcdt, [self.d_mlp, self.d_mlp, self._d_ssm, self.conv_dim, self.nheads])
-        new_conv_state = None
-        if inference_params is not None:
-            # the last d_conv inputs of the conv (left-padded with zeros)
-            xT = xBC.transpose(1, 2)
-            if seqlen >= self.d_conv:
-                new_conv_state = xT[:, :, -self.d_conv:]
-            else:
-                new_conv_state = torch.nn.functional.pad(xT, (self.d_conv - seqlen, 0))
-            cs = inference_params.get("conv_state")
-            if cs is not None and tuple(cs.shape) == tuple(new_conv_state.shape):
-                cs.copy_(new_conv_state)
-                new_conv_state = cs
-            else:
-                new_conv_state = new_conv_state.contiguous()
-        # conv + SiLU into x, B, C (contiguous, the SSD's layouts)
-        xs, Bs, Cs = causal_conv1d(xBC.transpose(1, 2), self.conv1d_weight, self.conv1d_bias,
-                                   "silu", seq_idx, split_sizes=(self._d_ssm, G * N, G * N))
-        x = xs.transpose(1, 2).view(batch, seqlen, H, Pd)
-        B = Bs.transpose(1, 2).view(batch, seqlen, G, N)
-        C = Cs.transpose(1, 2).view(batch, seqlen, G, N)
-        z_scan = None if self.rmsnorm else z.reshape(batch, seqlen, H, Pd)
-        return_final = inference_params is not None
-        res = _ssd_combined_fwd(x=x, dt=dt, A=self._A(), B=B, C=C, chunk_size=self.chunk_size,
-                                D=self._D(), z=z_scan, dt_bias=self.dt_bias, dt_softplus=True,
-                                dt_limit=self.dt_limit, seq_idx=seq_idx, cu_seqlens=cu_seqlens,
-                                return_final_states=return_final, return_varlen_states=False)
-        y, final = (res if return_final else (res, None))
-        out = self._out(y.reshape(batch, seqlen, self._d_ssm), z, z0, x0)
+            conv_state, ssm_state = inference_params["conv_state"], inference_params["ssm_state"]
+            out, conv_state, ssm_state = mamba2_block_step(u[:, 0, :], self.params(), self.dims(),
+                                                           conv_state, ssm_state)
+            return out[:, None, :], {"conv_state": conv_state, "ssm_state": ssm_state,
+                                     "seqlen_offset": inference_params["seqlen_offset"] + 1}
         if inference_params is None:
+            out, _, _ = mamba2_block_forward(u, self.params(), self.dims(), seq_idx, cu_seqlens)
             return out
-        ss = inference_params.get("ssm_state")
-        if ss is not None and tuple(ss.shape) == tuple(final.shape) and ss.dtype == final.dtype:
-            ss.copy_(final)
-            final = ss
-        return out, {"conv_state": new_conv_state, "ssm_state": final,
-                     "seqlen_offset": inference_params.get("seqlen_offset", 0) + seqlen}
+        out, conv_state, ssm_state = mamba2_block_forward(
+            u, self.params(), self.dims(), seq_idx, cu_seqlens, with_cache=True,
+            conv_state=inference_params.get("conv_state"),
+            ssm_state=inference_params.get("ssm_state"))
+        return out, {"conv_state": conv_state, "ssm_state": ssm_state,
+                     "seqlen_offset": inference_params.get("seqlen_offset", 0) + u.shape[1]}
 
-    def _step(self, u, inference_params):
-        """One decode token (reference modules/mamba2.py:427-549); the states
-        in inference_params are updated in place."""
-        G, N, H, Pd = self.ngroups, self.d_state, self.nheads, self.headdim
-        zxbcdt = self._in_proj(u[:, 0, :].to(self.in_proj_kernel.dtype))
-        z0, x0, z, xBC, dt = _split_last(
-            zxbcdt, [self.d_mlp, self.d_mlp, self._d_ssm, self.conv_dim, self.nheads])
-        conv_state, ssm_state = inference_params["conv_state"], inference_params["ssm_state"]
-        conv_state, (x, B, C) = causal_conv1d_update(
-            xBC, conv_state, self.conv1d_weight, self.conv1d_bias, "silu",
-            split_sizes=(self._d_ssm, G * N, G * N))
-        batch = u.shape[0]
-        z_step = None if self.rmsnorm else z.reshape(batch, H, Pd)
-        ssm_state, y = selective_state_update(
-            ssm_state, x.view(batch, H, Pd), dt, self._A(), B.view(batch, G, N), C.view(batch, G, N),
-            D=self._D(), z=z_step, dt_bias=self.dt_bias, dt_softplus=True)
-        out = self._out(y.reshape(batch, self._d_ssm), z, z0, x0)
-        return out[:, None, :], {"conv_state": conv_state, "ssm_state": ssm_state,
-                                 "seqlen_offset": inference_params["seqlen_offset"] + 1}
+
+_PARAM_NAMES = ("in_proj_kernel", "in_proj_bias", "conv1d_weight", "conv1d_bias", "dt_bias",
+                "A_log", "D", "norm_weight", "out_proj_kernel", "out_proj_bias")
+
+
+@dataclass(frozen=True)
+class MixerDims:
+    """The sizes and flags one mixer layer's computation needs."""
+    d_ssm: int
+    d_mlp: int
+    ngroups: int
+    d_state: int
+    headdim: int
+    nheads: int
+    d_conv: int
+    chunk_size: int
+    rmsnorm: bool = True
+    norm_before_gate: bool = False
+    D_has_hdim: bool = False
+    dt_limit: Tuple[float, float] = (0.0, float("inf"))
+
+    @property
+    def conv_dim(self):
+        return self.d_ssm + 2 * self.ngroups * self.d_state
+
+
+def _in_proj(h, p):
+    z = h @ p["in_proj_kernel"]
+    return z if p.get("in_proj_bias") is None else z + p["in_proj_bias"]
+
+
+def _mixer_out(y, z, z0, x0, p, d):
+    """gated RMSNorm, the MLP bypass, out-projection (reference :400-414)."""
+    if d.rmsnorm:
+        y = rms_norm_gated(y, p["norm_weight"], z=z, group_size=d.d_ssm // d.ngroups,
+                           norm_before_gate=d.norm_before_gate)
+    if d.d_mlp > 0:
+        y = torch.cat([torch.nn.functional.silu(z0) * x0, y.to(x0.dtype)], dim=-1)
+    y = y.to(p["out_proj_kernel"].dtype)
+    out = y @ p["out_proj_kernel"]
+    return out if p.get("out_proj_bias") is None else out + p["out_proj_bias"]
+
+
+def _A(p):
+    return -torch.exp(p["A_log"].float())
+
+
+def _D(p, d):
+    return p["D"].view(d.nheads, d.headdim) if d.D_has_hdim else p["D"]
+
+
+def mamba2_block_forward(u, p, d, seq_idx=None, cu_seqlens=None, with_cache=False,
+                         conv_state=None, ssm_state=None):
+    """Prefill of one mixer (reference modules/mamba2.py:296-424) from a
+    parameter dict ``p`` (reference names) and MixerDims ``d``.
+
+    -> (out (batch, seqlen, d_model), conv_state, ssm_state); the states are
+    None unless with_cache, and are written into the given tensors when their
+    shapes match (conv_state: the last d_conv conv inputs, left-padded with
+    zeros; ssm_state: the SSD's final states).
+    """
+    batch, seqlen, _ = u.shape
+    G, N, H, Pd = d.ngroups, d.d_state, d.nheads, d.headdim
+    zxbcdt = _in_proj(u.to(p["in_proj_kernel"].dtype), p)
+    z0, x0, z, xBC, dt = _split_last(zxbcdt, [d.d_mlp, d.d_mlp, d.d_ssm, d.conv_dim, d.nheads])
+    new_conv = None
+    if with_cache:
+        xT = xBC.transpose(1, 2)
+        if seqlen >= d.d_conv:
+            new_conv = xT[:, :, -d.d_conv:]
+        else:
+            new_conv = torch.nn.functional.pad(xT, (d.d_conv - seqlen, 0))
+        if conv_state is not None and tuple(conv_state.shape) == tuple(new_conv.shape):
+            conv_state.copy_(new_conv)
+            new_conv = conv_state
+        else:
+            new_conv = new_conv.contiguous()
+    # conv + SiLU into x, B, C (contiguous, the SSD's layouts)
+    xs, Bs, Cs = causal_conv1d(xBC.transpose(1, 2), p["conv1d_weight"], p.get("conv1d_bias"),
+                               "silu", seq_idx, split_sizes=(d.d_ssm, G * N, G * N))
+    x = xs.transpose(1, 2).view(batch, seqlen, H, Pd)
+    B = Bs.transpose(1, 2).view(batch, seqlen, G, N)
+    C = Cs.transpose(1, 2).view(batch, seqlen, G, N)
+    z_scan = None if d.rmsnorm else z.reshape(batch, seqlen, H, Pd)
+    res = _ssd_combined_fwd(x=x, dt=dt, A=_A(p), B=B, C=C, chunk_size=d.chunk_size, D=_D(p, d),
+                            z=z_scan, dt_bias=p["dt_bias"], dt_softplus=True, dt_limit=d.dt_limit,
+                            seq_idx=seq_idx, cu_seqlens=cu_seqlens,
+                            return_final_states=with_cache, return_varlen_states=False)
+    y, final = res if with_cache else (res, None)
+    out = _mixer_out(y.reshape(batch, seqlen, d.d_ssm), z, z0, x0, p, d)
+    if with_cache and ssm_state is not None and tuple(ssm_state.shape) == tuple(final.shape) \
+            and ssm_state.dtype == final.dtype:
+        ssm_state.copy_(final)
+        final = ssm_state
+    return out, new_conv, final
+
+
+def mamba2_block_step(u_t, p, d, conv_state, ssm_state):
+    """One decode token of one mixer (reference modules/mamba2.py:427-549):
+    u_t (batch, d_model) -> (out (batch, d_model), conv_state, ssm_state), the
+    states updated in place (float32 states: no copies)."""
+    G, N, H, Pd = d.ngroups, d.d_state, d.nheads, d.headdim
+    batch = u_t.shape[0]
+    zxbcdt = _in_proj(u_t.to(p["in_proj_kernel"].dtype), p)
+    z0, x0, z, xBC, dt = _split_last(zxbcdt, [d.d_mlp, d.d_mlp, d.d_ssm, d.conv_dim, d.nheads])
+    conv_state, (x, B, C) = causal_conv1d_update(
+        xBC, conv_state, p["conv1d_weight"], p.get("conv1d_bias"), "silu",
+        split_sizes=(d.d_ssm, G * N, G * N))
+    z_step = None if d.rmsnorm else z.reshape(batch, H, Pd)
+    ssm_state, y = selective_state_update(
+        ssm_state, x.view(batch, H, Pd), dt, _A(p), B.view(batch, G, N), C.view(batch, G, N),
+        D=_D(p, d), z=z_step, dt_bias=p["dt_bias"], dt_softplus=True)
+    out = _mixer_out(y.reshape(batch, d.d_ssm), z, z0, x0, p, d)
+    return out, conv_state, ssm_state
 
 
 def allocate_inference_cache(batch_size: int, d_model: int, d_state: int = 128, d_conv: int = 4,
@@ -225,4 +281,5 @@ def allocate_inference_cache(batch_size: int, d_model: int, d_state: int = 128, 
             "seqlen_offset": 0}
 
 
-__all__ = ["_ssd_combined_fwd", "selective_state_update", "Mamba2", "allocate_inference_cache"]
+__all__ = ["_ssd_combined_fwd", "selective_state_update", "Mamba2", "MixerDims",
+           "mamba2_block_forward", "mamba2_block_step", "allocate_inference_cache"]

@@ -299,3 +299,17 @@ def mamba2_layer_step(p, u_t, conv_state, ssm_state, cfg):
     if p.get("out_proj_bias") is not None:
         out = out + p["out_proj_bias"]
     return out, conv_state, ssm_state
+
+
+def mamba2_lm(params, input_ids, mcfg, eps=1e-5):
+    """Logits of the Mamba2 LM (reference models/mamba2_lm.py:178-217) from
+    float32 parameters: embedding, per layer residual + mixer(rmsnorm(x)),
+    final rmsnorm, tied LM head.  params: the reference's nested dict of
+    arrays; mcfg: the mixer cfg of mamba2_layer."""
+    x = np.asarray(params["embedding"]["weight"], np.float64)[np.asarray(input_ids)]
+    for lp in params["layers"]:
+        xn, _ = rms_norm_gated(x, lp["norm_weight"], eps=eps)
+        out, _, _ = mamba2_layer(lp["mixer"], xn, mcfg)
+        x = x + out
+    x, _ = rms_norm_gated(x, params["norm_f_weight"], eps=eps)
+    return x @ np.asarray(params["lm_head_weight"], np.float64).T

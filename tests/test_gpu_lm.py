@@ -1,0 +1,121 @@
+"""The Mamba2 LM (mamba2_jax.models) on the GPU: logits against the CPU
+oracle's composition, prefill + decode against the full forward, HIP-graph
+replays of the decode step against the eager step (every replay checked, with
+eager work and synchronisations between replays), and generation with and
+without the graph (reference models/mamba2_lm.py:178-302, 667-736)."""
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import TOL, announce, check, host
+from mamba2_jax.models import Mamba2Config, Mamba2LMHeadModel, init_params
+from mamba2_jax.models.mamba2_lm import DecodeState
+from oracle import ops_oracle as X
+
+pytestmark = pytest.mark.gpu
+
+CFG = Mamba2Config(d_model=128, n_layer=3, vocab_size=300, d_state=64, headdim=64, ngroups=1,
+                   chunk_size=64)
+
+
+def _np_params(p):
+    f = lambda t: None if t is None else host(t)
+    return {"embedding": {"weight": f(p["embedding"]["weight"])},
+            "layers": [{"norm_weight": f(lp["norm_weight"]),
+                        "mixer": {k: f(v) for k, v in lp["mixer"].items()}} for lp in p["layers"]],
+            "norm_f_weight": f(p["norm_f_weight"]), "lm_head_weight": f(p["lm_head_weight"])}
+
+
+def _mcfg(cfg):
+    d = cfg.mixer_dims()
+    return dict(d_ssm=d.d_ssm, d_mlp=0, ngroups=d.ngroups, d_state=d.d_state, headdim=d.headdim,
+                nheads=d.nheads, chunk_size=d.chunk_size, rmsnorm=d.rmsnorm,
+                norm_before_gate=d.norm_before_gate, D_has_hdim=d.D_has_hdim, dt_limit=d.dt_limit)
+
+
+def _cast(p, dtype):
+    f = lambda t: None if t is None else (t.to(dtype) if t.dtype == torch.bfloat16 else t)
+    return {"embedding": {"weight": f(p["embedding"]["weight"])},
+            "layers": [{"norm_weight": f(lp["norm_weight"]),
+                        "mixer": {k: f(v) for k, v in lp["mixer"].items()}} for lp in p["layers"]],
+            "norm_f_weight": f(p["norm_f_weight"]), "lm_head_weight": f(p["lm_head_weight"])}
+
+
+def _ids(rng, b, L):
+    return torch.from_numpy(rng.integers(0, CFG.vocab_size, (b, L))).cuda()
+
+
+def test_lm_logits_fp32():
+    announce("LM logits fp32")
+    params = init_params(CFG, dtype=torch.float32, seed=1)
+    ids = _ids(np.random.default_rng(2), 2, 90)
+    got = Mamba2LMHeadModel(CFG)(params, ids)
+    want = X.mamba2_lm(_np_params(params), host(ids).astype(np.int64), _mcfg(CFG))
+    check(got, want, TOL["f32"], "logits")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_lm_prefill_then_decode(dtype):
+    announce("LM prefill + decode", dtype)
+    pd = torch.bfloat16 if dtype == "bf16" else torch.float32
+    params = init_params(CFG, dtype=pd, seed=3)
+    m = Mamba2LMHeadModel(CFG)
+    ids = _ids(np.random.default_rng(4), 2, 80)
+    full = m(params, ids)
+    T0 = 70
+    st = DecodeState(CFG, 2)
+    last = m.prefill(params, ids[:, :T0], st)
+    check(last, host(full[:, T0 - 1]), 1e-5 if dtype == "f32" else 2e-2, "prefill logits")
+    outs = [m.decode_step(params, ids[:, t], st) for t in range(T0, 80)]
+    dec = torch.stack(outs[:-1], 1)
+    if dtype == "f32":
+        check(dec, host(full[:, T0:79]), TOL["f32"], "decode logits")
+        return
+    # bf16: prefill and decode round at different points (the chunked SSD's
+    # bf16 passed states and conv outputs vs the decode's f32 conv / SSM
+    # state), and the differences compound over the layers; both are held to
+    # the same float32 run of these (bf16-valued) parameters (the prefill
+    # measured ~5e-2 from it: bf16 projections, conv and SSD over 3 layers),
+    # the decode no further from it than twice the prefill
+    p32 = _cast(params, torch.float32)
+    truth = host(m(p32, ids)[:, T0:79])
+    e_pre = check(full[:, T0:79], truth, 1e-1, "bf16 prefill vs f32")
+    check(dec, truth, max(2 * e_pre, TOL["bf16"]), "bf16 decode vs f32")
+
+
+def test_decode_graph_replays_match_eager():
+    """Every replay of the captured step equals the eager step from the same
+    state; eager work and syncs run between the replays."""
+    announce("LM decode graph replays")
+    params = init_params(CFG, dtype=torch.bfloat16, seed=5)
+    m = Mamba2LMHeadModel(CFG)
+    ids = _ids(np.random.default_rng(6), 3, 40)
+    st_e, st_g = DecodeState(CFG, 3), DecodeState(CFG, 3)
+    m.prefill(params, ids[:, :30], st_e)
+    m.prefill(params, ids[:, :30], st_g)
+    g, tok, out = m.capture_decode(params, st_g)
+    assert torch.equal(st_e.ssm, st_g.ssm) and torch.equal(st_e.conv, st_g.conv)
+    for t in range(30, 40):
+        want = m.decode_step(params, ids[:, t], st_e)
+        torch.cuda.synchronize()
+        tok.copy_(ids[:, t])
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay at token {t}"
+        assert torch.equal(st_g.ssm, st_e.ssm) and torch.equal(st_g.conv, st_e.conv)
+        _ = (torch.randn(1000, device="cuda") * 2).sum().item()   # eager work in between
+
+
+def test_generate_graph_equals_eager():
+    announce("LM generate, graph vs eager")
+    params = init_params(CFG, dtype=torch.float32, seed=7)
+    m = Mamba2LMHeadModel(CFG)
+    ids = _ids(np.random.default_rng(8), 2, 24)
+    a = m.generate(params, ids, max_new_tokens=12, temperature=0, use_graph=True)
+    b = m.generate(params, ids, max_new_tokens=12, temperature=0, use_graph=False)
+    assert a.shape == (2, 36) and torch.equal(a[:, :24], ids)
+    assert torch.equal(a, b)
+    c = m.generate(params, ids, max_new_tokens=8, temperature=1.0, top_k=20, rng_key=3)
+    d = m.generate(params, ids, max_new_tokens=8, temperature=1.0, top_k=20, rng_key=3, use_graph=False)
+    assert torch.equal(c, d)
