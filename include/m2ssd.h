@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define M2SSD_ABI_VERSION 1
+#define M2SSD_ABI_VERSION 2
 
 /* return codes */
 #define M2_OK               0
@@ -304,7 +304,8 @@ int m2_causal_conv1d_update(const m2_causal_conv1d_update_args* a, void* stream)
  *   out = x' / sqrt(mean(x'^2) + eps) * weight
  *   out = out * silu(z)              (z given and norm_before_gate)
  * Every intermediate is bf16 exactly when all its operands are (x, z, weight
- * as they enter it); out_dtype must be that result dtype.  Rows are addressed
+ * as they enter it); out_dtype is that result dtype, or bf16 (the result
+ * rounded at the store, for a bf16 consumer such as a projection).  Rows are addressed
  * through row strides (elements; the last dimension is contiguous), e.g. z as
  * a slice of the in-projection output.
  * Replaces rms_norm_gated (reference ops/rms_norm.py:15-92).
@@ -319,6 +320,10 @@ typedef struct {
     float   eps;
     int32_t x_dtype, z_dtype, w_dtype, out_dtype;
     int32_t norm_before_gate;      /* 0 / 1                                     */
+    float*  residual;              /* [rows, hidden] f32 or NULL: with z == NULL,
+                                      residual += x (stored back) and the sum is
+                                      normalised (a pre-norm block's residual add) */
+    int64_t residual_row_stride;
 } m2_rms_norm_gated_args;
 int m2_rms_norm_gated(const m2_rms_norm_gated_args* a, void* stream);
 

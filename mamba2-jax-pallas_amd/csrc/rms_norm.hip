@@ -11,6 +11,9 @@
 // the sum of squares is reduced over the wavefronts in LDS, and the scaled
 // values are written from the registers.  Groups longer than NT * E are
 // processed in passes (the second pass re-reads x and z from cache).
+// With a residual stream (plain RMSNorm of a pre-norm block) the kernel also
+// does the block's residual add: res = res + x in float32, stored back, and
+// normalises that sum -- one kernel instead of an add and a norm.
 // Rounding follows the reference's array dtypes: every intermediate whose
 // JAX dtype is bfloat16 is rounded to bf16 (bf16 only when all its operands
 // are bf16); silu(z) has z's dtype.
@@ -34,6 +37,8 @@ struct NormArgs {
     int r_w;                      // x_normed * weight is bf16
     int r_o;                      // the gated output is bf16
     int vec;                      // 4-element accesses
+    float* res;                   // residual stream (x += res; res = x), or NULL
+    int64_t r_rs;
 };
 
 M2_DEV float rbf(float v) { return (float)(bf16)v; }
@@ -97,11 +102,24 @@ template <int CW> M2_DEV void stc(void* p, int64_t i, int is_bf16, int vec, cons
     }
 }
 
-// the normalised operand of CW elements at group offset i
+// the normalised operand of CW elements at group offset i; with a residual
+// stream the first pass adds it in float32 and stores the sum back, a second
+// pass (groups longer than the registers hold) reads that sum
 template <int CW>
-M2_DEV void operand(const NormArgs& a, const void* xr, const void* zr, int64_t i, float (&v)[CW],
-                    float (&sz)[CW]) {
-    ldc<CW>(xr, i, a.x_bf16, a.vec, v);
+M2_DEV void operand(const NormArgs& a, const void* xr, const void* zr, float* rr, int64_t i,
+                    float (&v)[CW], float (&sz)[CW], bool second = false) {
+    if (rr && second) {
+        ldc<CW>(rr, i, 0, a.vec, v);
+    } else {
+        ldc<CW>(xr, i, a.x_bf16, a.vec, v);
+        if (rr) {
+            float r[CW];
+            ldc<CW>(rr, i, 0, a.vec, r);
+#pragma unroll
+            for (int k = 0; k < CW; ++k) v[k] += r[k];
+            stc<CW>(rr, i, 0, a.vec, v);
+        }
+    }
     if (a.gate_first || a.gate_after) {
         ldc<CW>(zr, i, a.z_bf16, a.vec, sz);
 #pragma unroll
@@ -114,10 +132,9 @@ M2_DEV void operand(const NormArgs& a, const void* xr, const void* zr, int64_t i
 }
 
 template <int CW>
-M2_DEV void output(const NormArgs& a, void* orow, const void* w, int64_t i, int64_t wi, float inv,
-                   const float (&v)[CW], const float (&sz)[CW]) {
-    float wt[CW], o[CW];
-    ldc<CW>(w, wi, a.w_bf16, a.vec, wt);
+M2_DEV void output(const NormArgs& a, void* orow, int64_t i, float inv, const float (&v)[CW],
+                   const float (&sz)[CW], const float (&wt)[CW]) {
+    float o[CW];
 #pragma unroll
     for (int k = 0; k < CW; ++k) {
         float xn = v[k] * inv;
@@ -158,18 +175,21 @@ __global__ void __launch_bounds__(NT) k_rms_norm(NormArgs a) {
     const char* zr = a.z ? reinterpret_cast<const char*>(a.z) + (row * a.z_rs + gofs) * (a.z_bf16 ? 2 : 4)
                          : nullptr;
     char* orow = reinterpret_cast<char*>(a.out) + (row * a.o_rs + gofs) * (a.o_bf16 ? 2 : 4);
+    float* rr = a.res ? a.res + row * a.r_rs + gofs : nullptr;
     const int t = threadIdx.x;
     const int64_t n4 = a.gs / CW;                // chunks in the group
     const bool resident = n4 <= (int64_t)NT * E;
 
-    float v[E][CW], sz[E][CW];
+    float v[E][CW], sz[E][CW], wt[E][CW];
     float ss = 0.f;
     if (resident) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int64_t c = (int64_t)e * NT + t;
             if (c < n4) {
-                operand<CW>(a, xr, zr, CW * c, v[e], sz[e]);
+                // the weights load with the operands: no second round trip
+                ldc<CW>(a.w, gofs + CW * c, a.w_bf16, a.vec, wt[e]);
+                operand<CW>(a, xr, zr, rr, CW * c, v[e], sz[e]);
 #pragma unroll
                 for (int k = 0; k < CW; ++k) ss += a.r_x ? rbf(v[e][k] * v[e][k]) : v[e][k] * v[e][k];
             }
@@ -177,7 +197,7 @@ __global__ void __launch_bounds__(NT) k_rms_norm(NormArgs a) {
     } else {
         for (int64_t c = t; c < n4; c += NT) {
             float vv[CW], zz[CW];
-            operand<CW>(a, xr, zr, CW * c, vv, zz);
+            operand<CW>(a, xr, zr, rr, CW * c, vv, zz);
 #pragma unroll
             for (int k = 0; k < CW; ++k) ss += a.r_x ? rbf(vv[k] * vv[k]) : vv[k] * vv[k];
         }
@@ -194,13 +214,14 @@ __global__ void __launch_bounds__(NT) k_rms_norm(NormArgs a) {
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int64_t c = (int64_t)e * NT + t;
-            if (c < n4) output<CW>(a, orow, a.w, CW * c, gofs + CW * c, inv, v[e], sz[e]);
+            if (c < n4) output<CW>(a, orow, CW * c, inv, v[e], sz[e], wt[e]);
         }
     } else {
         for (int64_t c = t; c < n4; c += NT) {
-            float vv[CW], zz[CW];
-            operand<CW>(a, xr, zr, CW * c, vv, zz);
-            output<CW>(a, orow, a.w, CW * c, gofs + CW * c, inv, vv, zz);
+            float vv[CW], zz[CW], ww[CW];
+            ldc<CW>(a.w, gofs + CW * c, a.w_bf16, a.vec, ww);
+            operand<CW>(a, xr, zr, rr, CW * c, vv, zz, true);
+            output<CW>(a, orow, CW * c, inv, vv, zz, ww);
         }
     }
 }
@@ -220,14 +241,15 @@ int launch_rms_norm_gated(const m2_rms_norm_gated_args& a, hipStream_t s) {
         M2_REQUIRE(d == M2_F32 || d == M2_BF16, M2_ERR_UNSUPPORTED, "%s: dtype %d", who, d);
     M2_REQUIRE(!a.z || a.z_dtype == M2_F32 || a.z_dtype == M2_BF16, M2_ERR_UNSUPPORTED,
                "%s: z dtype %d", who, a.z_dtype);
+    M2_REQUIRE(!a.residual || !a.z, M2_ERR_INVALID, "%s: a residual stream needs z == NULL", who);
     const bool zb = a.z && a.z_dtype == M2_BF16;
     const bool gate_first = a.z && !a.norm_before_gate, gate_after = a.z && a.norm_before_gate;
     // dtypes of the reference's intermediates (bf16 only when all operands are)
-    const bool xdt_bf = a.x_dtype == M2_BF16 && (!gate_first || zb);
+    const bool xdt_bf = a.x_dtype == M2_BF16 && (!gate_first || zb) && !a.residual;
     const bool wdt_bf = xdt_bf && a.w_dtype == M2_BF16;
     const bool odt_bf = wdt_bf && (!gate_after || zb);
-    M2_REQUIRE(a.out_dtype == (odt_bf ? M2_BF16 : M2_F32), M2_ERR_INVALID,
-               "%s: out_dtype must be the result dtype %d", who, odt_bf ? M2_BF16 : M2_F32);
+    M2_REQUIRE(a.out_dtype == (odt_bf ? M2_BF16 : M2_F32) || a.out_dtype == M2_BF16, M2_ERR_INVALID,
+               "%s: out_dtype must be the result dtype %d or bf16", who, odt_bf ? M2_BF16 : M2_F32);
     const int64_t nblocks = a.rows * (a.hidden / a.group_size);
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "%s: too many rows", who);
 
@@ -236,15 +258,17 @@ int launch_rms_norm_gated(const m2_rms_norm_gated_args& a, hipStream_t s) {
     k.x_rs = a.x_row_stride; k.z_rs = a.z_row_stride; k.o_rs = a.out_row_stride;
     k.hidden = a.hidden; k.gs = a.group_size; k.ngroups = a.hidden / a.group_size; k.eps = a.eps;
     k.x_bf16 = a.x_dtype == M2_BF16; k.z_bf16 = zb; k.w_bf16 = a.w_dtype == M2_BF16;
-    k.o_bf16 = odt_bf;
+    k.o_bf16 = a.out_dtype == M2_BF16;
     k.gate_first = gate_first; k.gate_after = gate_after;
     k.r_x = xdt_bf; k.r_w = wdt_bf; k.r_o = odt_bf;
+    k.res = a.residual; k.r_rs = a.residual_row_stride;
     // 4-element chunks: every row and group start a multiple of 4 elements on
     // a 4-element-aligned base, as one access each when also aligned
-    const int xs = a.x_dtype == M2_BF16 ? 2 : 4, os = odt_bf ? 2 : 4, ws = a.w_dtype == M2_BF16 ? 2 : 4;
+    const int xs = a.x_dtype == M2_BF16 ? 2 : 4, os = k.o_bf16 ? 2 : 4, ws = a.w_dtype == M2_BF16 ? 2 : 4;
     bool c4 = a.group_size % 4 == 0 && a.x_row_stride % 4 == 0 && a.out_row_stride % 4 == 0 &&
-              (!a.z || a.z_row_stride % 4 == 0);
-    bool vec = c4 && aligned_to(a.x, 4 * xs) && aligned_to(a.out, 4 * os) && aligned_to(a.weight, 4 * ws);
+              (!a.z || a.z_row_stride % 4 == 0) && (!a.residual || a.residual_row_stride % 4 == 0);
+    bool vec = c4 && aligned_to(a.x, 4 * xs) && aligned_to(a.out, 4 * os) && aligned_to(a.weight, 4 * ws) &&
+               (!a.residual || aligned_to(a.residual, 16));
     if (a.z) vec = vec && aligned_to(a.z, 4 * (zb ? 2 : 4));
     k.vec = vec;
     const dim3 grid((unsigned)nblocks);

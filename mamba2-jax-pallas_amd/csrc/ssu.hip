@@ -4,9 +4,10 @@
 //   y[p] = sum_n state[p,n] C[n] + D x[p];   y *= silu(z[p])
 //
 // HBM-bound: the state (b*H*P*N fp32) is read and written exactly once.  One
-// workgroup per (batch, head); each thread owns 4 consecutive n (16-byte
-// accesses) of RPT rows p, issuing all RPT state loads before any arithmetic
-// so that RPT x 16 B stay in flight per thread.  The readout over n is a
+// workgroup per (batch, head), or per slice of its rows for small batches
+// (enough workgroups to fill the chip); each thread owns 4 consecutive n
+// (16-byte accesses) of RPT rows p, issuing all RPT state loads before any
+// arithmetic so that RPT x 16 B stay in flight per thread.  The readout over n is a
 // butterfly reduction across the N/4 lanes that share a row.
 //
 // Follows reference ops/selective_state_update.py:68-123.
@@ -28,6 +29,7 @@ struct SsuArgs {
     const float* dt_bias;
     float* out;
     int H, G, P, N;
+    int nsl;                    // workgroups (row slices) per (batch, head)
     int dt_bf16, dt_has_hdim, A_full, D_has_hdim, bias_has_hdim, softplus;
 };
 
@@ -39,7 +41,8 @@ template <typename T> M2_DEV float ld(const void* p, int64_t i) {
 template <typename T, int TPR, int RPT>
 __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
     constexpr int ROWS_PER_PASS = THREADS / TPR;
-    const int bh = blockIdx.x;
+    const int bh = blockIdx.x / a.nsl;
+    const int p0 = (blockIdx.x % a.nsl) * (RPT * ROWS_PER_PASS);   // first row of the slice
     const int bi = bh / a.H, h = bh % a.H;
     const int g = h / (a.H / a.G);
     const int P = a.P, N = a.N;
@@ -56,12 +59,12 @@ __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
     float4 s[RPT];
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-        const int p = r * ROWS_PER_PASS + tr;
+        const int p = p0 + r * ROWS_PER_PASS + tr;
         if (p < P) s[r] = *reinterpret_cast<const float4*>(st + (int64_t)p * N + n0);
     }
 #pragma unroll
     for (int r = 0; r < RPT; ++r) {
-        const int p = r * ROWS_PER_PASS + tr;
+        const int p = p0 + r * ROWS_PER_PASS + tr;
         if (p >= P) continue;
         const int64_t hp = (int64_t)bh * P + p;       // (batch, head, p) index
         float d = a.dt_has_hdim ? (a.dt_bf16 ? ld<bf16>(a.dt, hp) : ld<float>(a.dt, hp))
@@ -101,23 +104,33 @@ __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
 }
 
 template <typename T>
-int launch_typed(const SsuArgs& sa, int64_t nblocks, hipStream_t s) {
+int launch_typed(SsuArgs sa, int64_t nblocks, hipStream_t s) {
     void (*kern)(SsuArgs) = nullptr;
     const int tpr = sa.N / 4;
     const int rows_per_pass = THREADS / tpr;
-    const int rpt = (sa.P + rows_per_pass - 1) / rows_per_pass;
+    const int rpt_full = (sa.P + rows_per_pass - 1) / rows_per_pass;
+    // small batches: split each head's rows over several workgroups so that
+    // the step fills the chip (>= 512 workgroups where the rows allow)
+    int nsl = 1;
+    while (nsl * 2 <= rpt_full && nblocks * nsl < 512) nsl *= 2;
+    const int rpt = (rpt_full + nsl - 1) / nsl;
+    sa.nsl = nsl;
 #define M2_SSU_CASE(TPRV, RPTV) \
     if (tpr == TPRV && rpt <= RPTV && !kern) kern = k_ssu<T, TPRV, RPTV>;
-    M2_SSU_CASE(8, 2) M2_SSU_CASE(8, 4)                       // N = 32
-    M2_SSU_CASE(16, 4) M2_SSU_CASE(16, 8)                     // N = 64
-    M2_SSU_CASE(32, 4) M2_SSU_CASE(32, 8) M2_SSU_CASE(32, 16) // N = 128
-    M2_SSU_CASE(64, 8) M2_SSU_CASE(64, 16) M2_SSU_CASE(64, 32) // N = 256
+    M2_SSU_CASE(8, 1) M2_SSU_CASE(8, 2) M2_SSU_CASE(8, 4)                        // N = 32
+    M2_SSU_CASE(16, 1) M2_SSU_CASE(16, 2) M2_SSU_CASE(16, 4) M2_SSU_CASE(16, 8)  // N = 64
+    M2_SSU_CASE(32, 1) M2_SSU_CASE(32, 2) M2_SSU_CASE(32, 4) M2_SSU_CASE(32, 8)
+    M2_SSU_CASE(32, 16)                                                          // N = 128
+    M2_SSU_CASE(64, 1) M2_SSU_CASE(64, 2) M2_SSU_CASE(64, 4) M2_SSU_CASE(64, 8)
+    M2_SSU_CASE(64, 16) M2_SSU_CASE(64, 32)                                      // N = 256
 #undef M2_SSU_CASE
     if (!kern)
         return m2::set_error(M2_ERR_UNSUPPORTED,
                              "selective_state_update: dstate %d / headdim %d not supported", sa.N,
                              sa.P);
-    kern<<<(unsigned)nblocks, THREADS, 0, s>>>(sa);
+    const int64_t nwg = nblocks * nsl;
+    M2_REQUIRE(nwg < (1ll << 31), M2_ERR_UNSUPPORTED, "selective_state_update: too many blocks");
+    kern<<<(unsigned)nwg, THREADS, 0, s>>>(sa);
     return m2::check_launch("selective_state_update");
 }
 

@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm2ssd.so
 
 M2_F32 = 0
 M2_BF16 = 1
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -120,7 +120,7 @@ class RmsNormGatedArgs(ctypes.Structure):
                 ("x_row_stride", _i64), ("z_row_stride", _i64), ("out_row_stride", _i64),
                 ("rows", _i64), ("hidden", _i64), ("group_size", _i64), ("eps", _f32),
                 ("x_dtype", _i32), ("z_dtype", _i32), ("w_dtype", _i32), ("out_dtype", _i32),
-                ("norm_before_gate", _i32)]
+                ("norm_before_gate", _i32), ("residual", _c_p), ("residual_row_stride", _i64)]
 
 
 # entry point name -> argument struct (every function declared in m2ssd.h)

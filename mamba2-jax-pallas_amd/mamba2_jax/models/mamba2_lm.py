@@ -79,10 +79,12 @@ class Mamba2Config:
                          dt_limit=tuple(self.dt_limit))
 
 
-def rms_norm(x, weight, eps=1e-5):
+def rms_norm(x, weight, eps=1e-5, *, out_dtype=None, residual=None):
     """Plain RMSNorm over the last dimension (reference :136-139), as the HIP
-    rms_norm_gated kernel without a gate."""
-    return rms_norm_gated(x, weight, z=None, eps=eps)
+    rms_norm_gated kernel without a gate; out_dtype=torch.bfloat16 stores the
+    float32 result in bf16 for a bf16 projection; residual (float32, updated
+    in place to residual + x) fuses a pre-norm block's residual add."""
+    return rms_norm_gated(x, weight, z=None, eps=eps, out_dtype=out_dtype, residual=residual)
 
 
 def init_params(cfg: Mamba2Config, dtype=torch.bfloat16, device=None, seed=0):
@@ -145,54 +147,82 @@ class Mamba2LMHeadModel:
 
     def __init__(self, config: Mamba2Config):
         self.config = config
-        self._graph = None
+        self._prep = None
+
+    def _prepared(self, params):
+        """Per-layer mixer dicts with A = -exp(A_log) precomputed (cached per
+        parameter dict), so that a decode step launches no kernels for it."""
+        if self._prep is None or self._prep[0] is not params:
+            mixers = []
+            for lp in params["layers"]:
+                mx = dict(lp["mixer"])
+                mx["A"] = -torch.exp(mx["A_log"].float())
+                mixers.append(mx)
+            self._prep = (params, mixers)
+        return self._prep[1]
+
+    def _run_layers(self, params, x, block):
+        """The residual stack (reference :196-211): per layer x = x +
+        mixer(rmsnorm(x)).  With a float32 residual the add is fused into the
+        next norm (one kernel per layer boundary).  block(i, xn, mixer) runs
+        layer i's mixer.  -> (residual, last mixer output not yet added)."""
+        cfg = self.config
+        layers, mixers = params["layers"], self._prepared(params)
+        if cfg.residual_in_fp32:
+            res = x.float().contiguous()        # a fresh buffer: updated in place
+            out = None
+            for i, (lp, mx) in enumerate(zip(layers, mixers)):
+                dt = mx["in_proj_kernel"].dtype
+                xn = rms_norm(res if out is None else out, lp["norm_weight"], out_dtype=dt,
+                              residual=None if out is None else res)
+                out = block(i, xn, mx)
+            return res, out
+        for i, (lp, mx) in enumerate(zip(layers, mixers)):
+            xn = rms_norm(x.float(), lp["norm_weight"], out_dtype=mx["in_proj_kernel"].dtype)
+            x = x + block(i, xn, mx).to(x.dtype)
+        return x, None
+
+    def _head(self, params, res, out=None):
+        """final norm (with the last residual add) and the tied LM head."""
+        w = params["lm_head_weight"]
+        if out is None:
+            xn = rms_norm(res.float(), params["norm_f_weight"], out_dtype=w.dtype)
+        else:
+            xn = rms_norm(out, params["norm_f_weight"], out_dtype=w.dtype, residual=res)
+        return xn @ w.t()
 
     # -- prefill -------------------------------------------------------------
     def _layers(self, params, x, state=None):
-        cfg = self.config
-        d = cfg.mixer_dims()
-        rdt = torch.float32 if cfg.residual_in_fp32 else x.dtype
-        for i, lp in enumerate(params["layers"]):
-            residual = x.to(rdt)
-            xn = rms_norm(x.float(), lp["norm_weight"])
-            if state is None:
-                out, _, _ = mamba2_block_forward(xn, lp["mixer"], d)
-            else:
-                out, _, _ = mamba2_block_forward(xn, lp["mixer"], d, with_cache=True,
-                                                 conv_state=state.conv[i], ssm_state=state.ssm[i])
-            x = residual + out.to(rdt)
-        return x
+        d = self.config.mixer_dims()
 
-    def _head(self, params, x):
-        x = rms_norm(x.float(), params["norm_f_weight"])
-        w = params["lm_head_weight"]
-        return x.to(w.dtype) @ w.t()
+        def block(i, xn, mx):
+            if state is None:
+                return mamba2_block_forward(xn, mx, d)[0]
+            return mamba2_block_forward(xn, mx, d, with_cache=True, conv_state=state.conv[i],
+                                        ssm_state=state.ssm[i])[0]
+        return self._run_layers(params, x, block)
 
     def __call__(self, params, input_ids):
         """input_ids (batch, seqlen) -> logits (batch, seqlen, vocab_size_padded)."""
         x = params["embedding"]["weight"][input_ids]
-        return self._head(params, self._layers(params, x))
+        return self._head(params, *self._layers(params, x))
 
     def prefill(self, params, input_ids, state: DecodeState):
         """Prefill that leaves every layer's conv / ssm state in ``state``
         (reference _forward_with_cache, :304-351); -> logits of the last token."""
         x = params["embedding"]["weight"][input_ids]
-        return self._head(params, self._layers(params, x, state))[:, -1, :]
+        return self._head(params, *self._layers(params, x, state))[:, -1, :]
 
     # -- decode ----------------------------------------------------------------
     def decode_step(self, params, token, state: DecodeState):
         """token (batch,) -> next-token logits (batch, vocab); states in place
         (reference _scan_decode_step, :667-736)."""
-        cfg = self.config
-        d = cfg.mixer_dims()
-        rdt = torch.float32 if cfg.residual_in_fp32 else params["embedding"]["weight"].dtype
+        d = self.config.mixer_dims()
         x = params["embedding"]["weight"][token]
-        for i, lp in enumerate(params["layers"]):
-            residual = x.to(rdt)
-            xn = rms_norm(x.float(), lp["norm_weight"])
-            out, _, _ = mamba2_block_step(xn, lp["mixer"], d, state.conv[i], state.ssm[i])
-            x = residual + out.to(rdt)
-        return self._head(params, x)
+
+        def block(i, xn, mx):
+            return mamba2_block_step(xn, mx, d, state.conv[i], state.ssm[i])[0]
+        return self._head(params, *self._run_layers(params, x, block))
 
     def capture_decode(self, params, state: DecodeState, warmup=2):
         """Capture decode_step into a HIP graph over static token / logits

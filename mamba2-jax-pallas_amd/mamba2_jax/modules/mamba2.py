@@ -183,10 +183,12 @@ def _in_proj(h, p):
 
 
 def _mixer_out(y, z, z0, x0, p, d):
-    """gated RMSNorm, the MLP bypass, out-projection (reference :400-414)."""
+    """gated RMSNorm, the MLP bypass, out-projection (reference :400-414).
+    Without the MLP bypass the norm stores straight in the projection's dtype."""
     if d.rmsnorm:
         y = rms_norm_gated(y, p["norm_weight"], z=z, group_size=d.d_ssm // d.ngroups,
-                           norm_before_gate=d.norm_before_gate)
+                           norm_before_gate=d.norm_before_gate,
+                           out_dtype=p["out_proj_kernel"].dtype if d.d_mlp == 0 else None)
     if d.d_mlp > 0:
         y = torch.cat([torch.nn.functional.silu(z0) * x0, y.to(x0.dtype)], dim=-1)
     y = y.to(p["out_proj_kernel"].dtype)
@@ -195,7 +197,9 @@ def _mixer_out(y, z, z0, x0, p, d):
 
 
 def _A(p):
-    return -torch.exp(p["A_log"].float())
+    """A = -exp(A_log) (reference :293), or a precomputed p["A"]."""
+    A = p.get("A")
+    return -torch.exp(p["A_log"].float()) if A is None else A
 
 
 def _D(p, d):

@@ -34,13 +34,19 @@ def _bf(*ts):
     return all(t is None or t.dtype == torch.bfloat16 for t in ts)
 
 
-def rms_norm_gated(x, weight, z=None, eps=1e-5, group_size=None, norm_before_gate=True):
+def rms_norm_gated(x, weight, z=None, eps=1e-5, group_size=None, norm_before_gate=True, *,
+                   out_dtype=None, residual=None):
     """-> out, same shape as x.
 
     x (..., hidden); weight (hidden,); z (..., hidden) or None.
     z and not norm_before_gate: out = RMSNorm(x * silu(z)) * weight;
     z and norm_before_gate:     out = RMSNorm(x) * weight * silu(z);
     RMS over groups of group_size trailing elements (None: all of hidden).
+    out_dtype (keyword only, not in the reference): torch.bfloat16 stores the
+    float32 result rounded to bf16 (for a bf16 consumer; no separate cast).
+    residual (keyword only, not in the reference; z must be None): a float32
+    tensor shaped like x, updated in place to residual + x, whose RMSNorm is
+    returned -- a pre-norm block's residual add fused into its norm.
     """
     dev = L.device_of(x, weight, z)
     hidden = int(x.shape[-1])
@@ -56,8 +62,19 @@ def rms_norm_gated(x, weight, z=None, eps=1e-5, group_size=None, norm_before_gat
     rows = int(xr.shape[0])
     gate_first = z is not None and not norm_before_gate
     gate_after = z is not None and norm_before_gate
-    xdt_bf = _bf(xr, zr if gate_first else None)
+    rr = None
+    if residual is not None:
+        L.require(z is None, "residual needs z=None")
+        L.require(residual.dtype == torch.float32 and tuple(residual.shape) == tuple(x.shape)
+                  and residual.is_contiguous() and residual.data_ptr() % 16 == 0,
+                  "residual must be a contiguous, 16-byte aligned float32 tensor shaped like x")
+        rr = residual.view(-1, hidden)
+    # the sum with a float32 residual is float32
+    xdt_bf = _bf(xr, zr if gate_first else None) and rr is None
     odt = torch.bfloat16 if xdt_bf and _bf(w, zr if gate_after else None) else torch.float32
+    if out_dtype is not None:
+        L.require(out_dtype in (odt, torch.bfloat16), f"out_dtype {out_dtype}: the result dtype or bfloat16")
+        odt = out_dtype
     out = torch.empty(tuple(x.shape), dtype=odt, device=dev)
     if rows == 0:
         return out
@@ -68,7 +85,7 @@ def rms_norm_gated(x, weight, z=None, eps=1e-5, group_size=None, norm_before_gat
         out_row_stride=hidden, rows=rows, hidden=hidden, group_size=gs, eps=float(eps),
         x_dtype=L.dtype_code(xr, "x"), z_dtype=L.M2_F32 if zr is None else L.dtype_code(zr, "z"),
         w_dtype=L.dtype_code(w, "weight"), out_dtype=L.dtype_code(out, "out"),
-        norm_before_gate=int(bool(norm_before_gate)))
+        norm_before_gate=int(bool(norm_before_gate)), residual=L.ptr(rr), residual_row_stride=hidden)
     with torch.cuda.device(dev):
         L.call("m2_rms_norm_gated", args, L.stream_of(dev))
     return out

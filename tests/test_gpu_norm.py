@@ -123,3 +123,21 @@ def test_errors():
         rms_norm_gated(x, torch.ones(10, device="cuda"))
     with pytest.raises(ValueError):
         rms_norm_gated(x.cpu(), torch.ones(12))
+
+
+@pytest.mark.parametrize("hidden,xdt", [(2560, "bf16"), (12288, "bf16"), (768, "f32"), (30, "bf16")])
+def test_residual_add_fused(hidden, xdt):
+    """residual (f32, in place) += x, then the RMSNorm of the sum: the
+    reference's pre-norm block (models/mamba2_lm.py:205-211) in one kernel;
+    12288 runs the two-pass path (the second pass must not add again)."""
+    announce("rms_norm with residual", hidden, xdt)
+    rng = np.random.default_rng(hidden)
+    x = _rnd(rng.standard_normal((3, hidden)), T[xdt])
+    res = rng.standard_normal((3, hidden)).astype(np.float32)
+    w = _rnd(rng.uniform(0.5, 1.5, hidden), torch.bfloat16)
+    rt = dev(res)
+    got = rms_norm_gated(dev(x, T[xdt]), dev(w, torch.bfloat16), residual=rt, out_dtype=torch.bfloat16)
+    summed = res.astype(np.float64) + x
+    assert np.array_equal(host(rt), (res + x.astype(np.float32)).astype(np.float64)), "residual += x in f32"
+    want, _ = X.rms_norm_gated(summed.astype(np.float32), w, w_dtype="bfloat16")
+    _close(got, bf16_round(want), True, "add + norm, bf16 store")
