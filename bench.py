@@ -1,6 +1,7 @@
 """Benchmark: one Mamba2 SSD layer forward at the nemotron-h-8b shape on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu-baseline]
+    python bench.py --ops [--lm 130m,2.7b]     (the ops around the SSD, LM decode)
 
 A step is one call of mamba2_jax.kernels.mamba_chunk_scan_combined_fwd on
 synthetic inputs already resident in HBM, returning the output and the final
@@ -224,6 +225,106 @@ def bench_decode(steps=256, warmup=16):
             "bytes_per_step": by}
 
 
+def _graph_time_ms(fn, calls=20, replays=10):
+    """Mean GPU time of fn() from a HIP graph of `calls` back-to-back calls
+    replayed `replays` times (no per-call host overhead in the figure)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (calls * replays)
+
+
+def bench_ops(lm_configs=("130m",)):
+    """The ops on either side of the SSD at the nemotron-h-8b layer shape
+    (causal_conv1d split into x / B / C, gated RMSNorm), the conv decode update
+    at the c4 batch, and the LM decode step (HIP graph) for the given model
+    shapes (random bf16 weights)."""
+    import torch
+    from mamba2_jax.ops import causal_conv1d, causal_conv1d_update, rms_norm_gated
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *shape, dt=torch.bfloat16: torch.randn(shape, generator=g, device=dev).to(dt)
+    out = {}
+    L, H, P, G, N, W = 4096, 128, 64, 8, 128, 4
+    dssm, gn = H * P, G * N
+    D = dssm + 2 * gn
+    dproj = 2 * dssm + 2 * gn + H
+    xbc = rnd(1, L, D)
+    w, b = rnd(D, W), rnd(D)
+    ms = _graph_time_ms(lambda: causal_conv1d(xbc.transpose(1, 2), w, b, "silu",
+                                              split_sizes=(dssm, gn, gn)))
+    by = 2 * 2 * L * D + D * (W + 1) * 2
+    out["causal_conv1d"] = {"workload": f"xBC (1, {L}, {D}) bf16 channels-last, width {W}, silu, "
+                                        "split into x / B / C", "ms": ms, "bytes": by,
+                            "hbm_gbs": by / (ms * 1e-3) / 1e9,
+                            "hbm_frac": by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    y = rnd(1, L, dssm, dt=torch.float32)
+    zx = rnd(1, L, dproj)
+    z = zx[:, :, dssm:2 * dssm]
+    nw = torch.rand(dssm, generator=g, device=dev)
+    ms = _graph_time_ms(lambda: rms_norm_gated(y, nw, z=z, group_size=dssm // G,
+                                               norm_before_gate=False))
+    by = L * dssm * (4 + 2 + 4) + dssm * 4
+    out["rms_norm_gated"] = {"workload": f"y (1, {L}, {dssm}) f32, z bf16 slice of the "
+                                         f"in-projection, groups of {dssm // G}, gate first",
+                             "ms": ms, "bytes": by, "hbm_gbs": by / (ms * 1e-3) / 1e9,
+                             "hbm_frac": by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS}
+    bsz = 64
+    st = torch.randn((bsz, D, W), generator=g, device=dev)
+    xn = rnd(bsz, D)
+    ms = _graph_time_ms(lambda: causal_conv1d_update(xn, st, w, b, "silu"))
+    by = bsz * D * (2 * W * 4 + 2 + 4)
+    out["causal_conv1d_update"] = {"workload": f"batch {bsz}, {D} channels, f32 state in place",
+                                   "ms": ms, "bytes": by, "hbm_gbs": by / (ms * 1e-3) / 1e9}
+    from mamba2_jax.models import Mamba2Config, Mamba2LMHeadModel, init_params
+    from mamba2_jax.models.mamba2_lm import DecodeState
+    shapes = {"130m": Mamba2Config(d_model=768, n_layer=24, vocab_size=50277),
+              "2.7b": Mamba2Config(d_model=2560, n_layer=64, vocab_size=50277)}
+    for name in lm_configs:
+        cfg = shapes[name]
+        params = init_params(cfg, dtype=torch.bfloat16, device=dev)
+        m = Mamba2LMHeadModel(cfg)
+        for bsz in (1, 64):
+            state = DecodeState(cfg, bsz, dev)
+            ids = torch.randint(0, cfg.vocab_size, (bsz, 32), device=dev)
+            m.prefill(params, ids, state)
+            gr, tok, _ = m.capture_decode(params, state)
+            tok.copy_(ids[:, -1])
+            for _ in range(3):
+                gr.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(50):
+                gr.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / 50
+            out[f"lm_decode_{name}_b{bsz}"] = {
+                "workload": f"Mamba2 LM {name} shape (d_model {cfg.d_model}, {cfg.n_layer} "
+                            f"layers), bf16 weights, batch {bsz}, one token per step, HIP graph",
+                "ms_per_token_step": ms, "tokens_per_s": bsz / (ms * 1e-3)}
+            del gr, state
+        del params
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -233,6 +334,10 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=32)
+    ap.add_argument("--ops", action="store_true",
+                    help="instead of the SSD layer: time the ops around it and the LM decode "
+                         "step (one JSON line)")
+    ap.add_argument("--lm", default="130m", help="LM shapes for --ops (comma list: 130m,2.7b)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="run one device copy of this many MiB first (HBM counter calibration)")
     args = ap.parse_args(argv)
@@ -242,6 +347,10 @@ def main(argv=None):
               "this build has no multi-GPU path; the SSD forward shards by head groups with no "
               "communication, so per-GPU throughput is the one-GPU figure.", file=sys.stderr)
         return 2
+
+    if args.ops:
+        print(json.dumps({"ops": bench_ops(tuple(x for x in args.lm.split(",") if x))}))
+        return 0
 
     import numpy as np
     import torch

@@ -28,6 +28,10 @@ STRUCT_NAMES = {
     "ChunkStateVarlenArgs": "m2_chunk_state_varlen_args",
     "SsdCombinedArgs": "m2_ssd_combined_args",
     "SsuArgs": "m2_ssu_args",
+    "ConvOut": "m2_conv_out",
+    "CausalConv1dArgs": "m2_causal_conv1d_args",
+    "CausalConv1dUpdateArgs": "m2_causal_conv1d_update_args",
+    "RmsNormGatedArgs": "m2_rms_norm_gated_args",
 }
 
 
