@@ -327,6 +327,25 @@ typedef struct {
 } m2_rms_norm_gated_args;
 int m2_rms_norm_gated(const m2_rms_norm_gated_args* a, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * skinny_gemm: y[M, N] = x[M, K] w[N, K]^T (+ bias[N]) for M <= 64, bf16 x and w
+ * (K-contiguous rows: the [out, in] layout of a linear layer), float32
+ * accumulation, y in bf16 or f32.  No counterpart operator in the reference
+ * (whose projections are XLA GEMMs, modules/mamba2.py:464-469, :538-541,
+ * models/mamba2_lm.py:699, :734): the decode step's in-/out-projections and LM
+ * head, which are bound by reading the weights once per token.
+ * K and the x / w row strides must be multiples of 8 (16-byte rows).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void* x;                 /* [M, K] at ldx, bf16                       */
+    const void* w;                 /* [N, K] at ldw, bf16                       */
+    const void* bias;              /* [N], bias_dtype, or NULL                  */
+    void*       y;                 /* out [M, N] at ldy, y_dtype                */
+    int64_t M, N, K, ldx, ldw, ldy;
+    int32_t x_dtype, w_dtype, bias_dtype, y_dtype;
+} m2_skinny_gemm_args;
+int m2_skinny_gemm(const m2_skinny_gemm_args* a, void* stream);
+
 /* thread-local message for the last non-zero return code of this thread */
 const char* m2_last_error(void);
 /* M2SSD_ABI_VERSION of the loaded library */

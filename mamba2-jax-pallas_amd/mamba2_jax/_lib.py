@@ -123,6 +123,12 @@ class RmsNormGatedArgs(ctypes.Structure):
                 ("norm_before_gate", _i32), ("residual", _c_p), ("residual_row_stride", _i64)]
 
 
+class SkinnyGemmArgs(ctypes.Structure):
+    _fields_ = [("x", _c_p), ("w", _c_p), ("bias", _c_p), ("y", _c_p), ("M", _i64), ("N", _i64),
+                ("K", _i64), ("ldx", _i64), ("ldw", _i64), ("ldy", _i64), ("x_dtype", _i32),
+                ("w_dtype", _i32), ("bias_dtype", _i32), ("y_dtype", _i32)]
+
+
 # entry point name -> argument struct (every function declared in m2ssd.h)
 ENTRY_POINTS = {
     "m2_chunk_cumsum": ChunkCumsumArgs,
@@ -136,6 +142,7 @@ ENTRY_POINTS = {
     "m2_causal_conv1d": CausalConv1dArgs,
     "m2_causal_conv1d_update": CausalConv1dUpdateArgs,
     "m2_rms_norm_gated": RmsNormGatedArgs,
+    "m2_skinny_gemm": SkinnyGemmArgs,
 }
 OTHER_SYMBOLS = ("m2_ssd_combined_workspace_size", "m2_last_error", "m2_abi_version")
 

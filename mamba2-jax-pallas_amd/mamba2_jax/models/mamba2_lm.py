@@ -26,6 +26,7 @@ from dataclasses import dataclass
 import torch
 
 from ..modules.mamba2 import MixerDims, _lecun_normal, mamba2_block_forward, mamba2_block_step
+from ..ops import linear
 from ..ops.rms_norm import rms_norm_gated
 
 
@@ -150,13 +151,19 @@ class Mamba2LMHeadModel:
         self._prep = None
 
     def _prepared(self, params):
-        """Per-layer mixer dicts with A = -exp(A_log) precomputed (cached per
-        parameter dict), so that a decode step launches no kernels for it."""
+        """Per-layer mixer dicts (cached per parameter dict) with A =
+        -exp(A_log) precomputed, so that a decode step launches no kernels for
+        it, and, for bf16 weights, K-contiguous copies of the projections
+        ([out, in]) for the decode step's skinny GEMM."""
         if self._prep is None or self._prep[0] is not params:
             mixers = []
             for lp in params["layers"]:
                 mx = dict(lp["mixer"])
                 mx["A"] = -torch.exp(mx["A_log"].float())
+                for name in ("in_proj", "out_proj"):
+                    k = mx[name + "_kernel"]
+                    if k.dtype == torch.bfloat16 and k.shape[0] % 8 == 0:
+                        mx[name + "_t"] = k.t().contiguous()
                 mixers.append(mx)
             self._prep = (params, mixers)
         return self._prep[1]
@@ -189,6 +196,8 @@ class Mamba2LMHeadModel:
             xn = rms_norm(res.float(), params["norm_f_weight"], out_dtype=w.dtype)
         else:
             xn = rms_norm(out, params["norm_f_weight"], out_dtype=w.dtype, residual=res)
+        if xn.dim() == 2 and linear.preferred(xn, w):
+            return linear.linear_skinny(xn, w, out_dtype=w.dtype)   # decode: the tied head
         return xn @ w.t()
 
     # -- prefill -------------------------------------------------------------

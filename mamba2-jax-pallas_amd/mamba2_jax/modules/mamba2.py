@@ -30,6 +30,7 @@ from typing import Optional, Tuple
 import torch
 
 from ..kernels.ssd_combined import mamba_chunk_scan_combined_fwd as _hip_fwd
+from ..ops import linear as _lin
 from ..ops.causal_conv1d import causal_conv1d, causal_conv1d_update
 from ..ops.rms_norm import rms_norm_gated
 from ..ops.selective_state_update import selective_state_update
@@ -177,9 +178,19 @@ class MixerDims:
         return self.d_ssm + 2 * self.ngroups * self.d_state
 
 
+def _proj(h, p, name):
+    """h @ p[name + "_kernel"] (+ bias).  A decode-sized h (<= 16 rows) with a
+    K-contiguous bf16 copy p[name + "_t"] ([out, in], prepared by the caller)
+    runs the HIP skinny GEMM; anything else is a torch matmul (hipBLASLt)."""
+    wt, b = p.get(name + "_t"), p.get(name + "_bias")
+    if wt is not None and h.dim() == 2 and _lin.preferred(h, wt):
+        return _lin.linear_skinny(h, wt, b, out_dtype=wt.dtype)
+    z = h @ p[name + "_kernel"]
+    return z if b is None else z + b
+
+
 def _in_proj(h, p):
-    z = h @ p["in_proj_kernel"]
-    return z if p.get("in_proj_bias") is None else z + p["in_proj_bias"]
+    return _proj(h, p, "in_proj")
 
 
 def _mixer_out(y, z, z0, x0, p, d):
@@ -191,9 +202,7 @@ def _mixer_out(y, z, z0, x0, p, d):
                            out_dtype=p["out_proj_kernel"].dtype if d.d_mlp == 0 else None)
     if d.d_mlp > 0:
         y = torch.cat([torch.nn.functional.silu(z0) * x0, y.to(x0.dtype)], dim=-1)
-    y = y.to(p["out_proj_kernel"].dtype)
-    out = y @ p["out_proj_kernel"]
-    return out if p.get("out_proj_bias") is None else out + p["out_proj_bias"]
+    return _proj(y.to(p["out_proj_kernel"].dtype), p, "out_proj")
 
 
 def _A(p):

@@ -32,6 +32,7 @@ STRUCT_NAMES = {
     "CausalConv1dArgs": "m2_causal_conv1d_args",
     "CausalConv1dUpdateArgs": "m2_causal_conv1d_update_args",
     "RmsNormGatedArgs": "m2_rms_norm_gated_args",
+    "SkinnyGemmArgs": "m2_skinny_gemm_args",
 }
 
 
