@@ -325,6 +325,34 @@ def bench_ops(lm_configs=("130m",)):
     return out
 
 
+def bench_fp32_same_shape(cfg, steps=30, warmup=5):
+    """The configuration's shape with fp32 inputs (the reference's published
+    numbers are fp32 runs at the nemotron-h-8b shape, README.md:35)."""
+    import dataclasses
+    import torch
+    from mamba2_jax import configs
+    from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
+    c32 = dataclasses.replace(cfg, dtype="f32")
+    d = configs.make_ssd_inputs(c32)
+    dev = torch.device("cuda")
+    t = lambda a: None if a is None else torch.from_numpy(a).to(dev).float()
+    kw = dict(x=t(d["x"]), dt=t(d["dt"]), A=t(d["A"]), B=t(d["B"]), C=t(d["C"]), D=t(d["D"]),
+              dt_bias=t(d["dt_bias"]), initial_states=t(d["initial_states"]),
+              chunk_size=c32.chunk_size, dt_softplus=True, return_final_states=True)
+    for _ in range(warmup):
+        mamba_chunk_scan_combined_fwd(**kw)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        mamba_chunk_scan_combined_fwd(**kw)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"workload": f"{cfg.name} shape, fp32 inputs (staged kernels)", "ms_per_layer": ms,
+            "tokens_per_s": c32.tokens / (ms * 1e-3)}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -468,6 +496,8 @@ def main(argv=None):
         "reference_published": {"hardware": "H100", "dtype": "fp32", "pallas_ms": 0.94,
                                 "triton_ms": 0.69, "source": "reference README.md:35"},
     }
+    if args.config == "c2":
+        res["fp32_same_shape"] = bench_fp32_same_shape(cfg)
     if not args.no_decode:
         res["decode"] = bench_decode()
     if not args.no_cpu_baseline:
