@@ -125,7 +125,7 @@ int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t s) {
         if (a.out_dtype == M2_F32) return launch_typed<bf16, float>(a, s);
         if (a.out_dtype == M2_BF16) return launch_typed<bf16, bf16>(a, s);
     } else if (a.dtype == M2_F32) {
-        M2_REQUIRE(a.k % 4 == 0, M2_ERR_UNSUPPORTED, "bmm_chunk: f32 needs k %% 4 == 0");
+        M2_REQUIRE(a.k % 32 == 0, M2_ERR_UNSUPPORTED, "bmm_chunk: f32 needs k %% 32 == 0");
         if (a.out_dtype == M2_F32) return launch_typed<float, float>(a, s);
         if (a.out_dtype == M2_BF16) return launch_typed<float, bf16>(a, s);
     }

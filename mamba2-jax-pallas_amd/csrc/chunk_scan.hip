@@ -311,7 +311,7 @@ int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t s) {
         if (a.cb_dtype == M2_F32) return launch_typed<bf16, float>(sa, s);
         if (a.cb_dtype == M2_BF16) return launch_typed<bf16, bf16>(sa, s);
     } else if (a.dtype == M2_F32) {
-        M2_REQUIRE(a.dstate % 4 == 0, M2_ERR_UNSUPPORTED, "chunk_scan: f32 needs dstate %% 4 == 0");
+        M2_REQUIRE(a.dstate % 32 == 0, M2_ERR_UNSUPPORTED, "chunk_scan: f32 needs dstate %% 32 == 0");
         if (a.cb_dtype == M2_F32) return launch_typed<float, float>(sa, s);
         if (a.cb_dtype == M2_BF16) return launch_typed<float, bf16>(sa, s);
     }

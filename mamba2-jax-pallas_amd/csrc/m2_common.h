@@ -43,8 +43,8 @@ M2_DEV float silu_f(float v) { return v / (1.f + expf(-v)); }
 //   A operand: lane l holds row (l & 15), k = (l >> 4) * KPL + j, j < KPL
 //   B operand: lane l holds col (l & 15), same k
 //   D:         lane l holds col (l & 15), rows 4 * (l >> 4) + i, i < 4
-// bf16 inputs use v_mfma_f32_16x16x32_bf16 (K = 32), fp32 inputs use
-// v_mfma_f32_16x16x4_f32 (K = 4) so that fp32 callers keep fp32 operands.
+// bf16 inputs use v_mfma_f32_16x16x32_bf16 (K = 32); fp32 inputs use the same
+// instruction on bf16 hi / lo triples (MF<float> below).
 // ---------------------------------------------------------------------------
 template <typename T> struct MF;
 
@@ -67,22 +67,48 @@ template <> struct MF<bf16> {
     }
 };
 
-template <> struct MF<float> {
-    static constexpr int KPL = 1;
-    static constexpr int K = 4;
-    typedef float frag;
-    static M2_DEV f32x4 mma(frag a, frag b, f32x4 c) {
-        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-    }
-    static M2_DEV void set(frag& f, int, float v) { f = v; }
-    static M2_DEV void set_raw(frag& f, int, float v) { f = v; }
-    static constexpr bool kSplit = false;   // fp32 operands are exact already
-    static M2_DEV void set_split(frag& hi, frag& lo, int, float v) { hi = v; lo = 0.f; }
+// fp32 operands as bf16 triples: v = hi + lo (both bf16, |v - hi - lo| ~ 2^-17 |v|),
+// a.b ~ hi.hi + hi.lo + lo.hi (the dropped lo.lo term is ~2^-16 of the
+// product): three 16x16x32 bf16 MFMAs per K = 32 step, ~16x the fp32 MFMA
+// rate at near-fp32 accuracy, and 8 consecutive k per lane (32-byte loads).
+struct f32x3frag {
+    bf16x8 hi, lo;
 };
 
-// Load KPL consecutive elements (16 B for bf16, 4 B for fp32) as a fragment.
+template <> struct MF<float> {
+    static constexpr int KPL = 8;
+    static constexpr int K = 32;
+    typedef f32x3frag frag;
+    static M2_DEV f32x4 mma(const frag& a, const frag& b, f32x4 c) {
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.lo, b.hi, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.lo, c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.hi, b.hi, c, 0, 0, 0);
+    }
+    static M2_DEV void set(frag& f, int j, float v) {
+        const bf16 h = (bf16)v;
+        f.hi[j] = h;
+        f.lo[j] = (bf16)(v - (float)h);
+    }
+    static M2_DEV void set_raw(frag& f, int j, float v) { set(f, j, v); }
+    // the triple already carries the split: one fragment, no second MFMA pass
+    static constexpr bool kSplit = false;
+    static M2_DEV void set_split(frag& hi, frag& lo, int j, float v) {
+        set(hi, j, v);
+        set(lo, j, 0.f);
+    }
+};
+
+// Load KPL consecutive elements (16 B for bf16, 32 B for fp32) as a fragment.
 M2_DEV bf16x8 load_frag(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
-M2_DEV float load_frag(const float* p) { return *p; }
+M2_DEV f32x3frag load_frag(const float* p) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    f32x3frag f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) MF<float>::set(f, j, v[j]);
+    return f;
+}
 
 M2_DEV f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 

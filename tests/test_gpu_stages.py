@@ -5,7 +5,9 @@ Shapes replay the reference's own stage tests (tests/test_chunk_cumsum_and_state
 tests/test_chunk_scan_and_varlen.py:797-853) with our seeded inputs, plus edge
 cases (L % Q != 0, odd dims, bf16 and fp32).  Tolerances are the benchmark
 contract's: max|err|/rms <= 1e-3 (fp32 inputs), 2e-2 (bf16 inputs); pure fp32
-stages (cumsum, state passing, bmm) are held to 1e-5.
+stages (cumsum, state passing) are held to 1e-5, bmm to 1e-5 for bf16 inputs and
+1e-4 for fp32 inputs (fp32 operands run through the matrix cores as bf16 hi / lo
+triples: ~2^-16 relative error per product).
 """
 
 import math
@@ -174,7 +176,7 @@ def test_bmm_chunk(cfg, dtype):
                         causal=causal)
     assert got.dtype == torch.float32
     want = O.bmm_chunk(a, bb, Q, seq_idx=seq, causal=causal)
-    check(got, want, 1e-5, "CB")
+    check(got, want, 1e-5 if dtype == "bf16" else 1e-4, "CB")
 
 
 def test_bmm_chunk_bf16_output():
