@@ -33,7 +33,7 @@
 namespace {
 
 constexpr int THREADS = 256;
-constexpr int TT = 32;          // tokens per wavefront in k_conv_walk
+constexpr int TT = 16;          // tokens per wavefront in k_conv_walk
 constexpr int GRP = 4;          // tokens per load group (two groups in flight)
 constexpr int MAXW = 8;         // largest conv width
 
