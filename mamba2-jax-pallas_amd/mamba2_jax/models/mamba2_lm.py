@@ -4,8 +4,10 @@ models/mamba2_lm.py:36-736).
 
 Same config fields, parameter dict structure, call signatures and returns as
 the reference (``__call__(params, input_ids) -> logits``, ``generate``).
-Parameters are torch tensors on the GPU (``init_params`` makes random ones of
-the architecture; loading checkpoint files is not part of this module).
+Parameters are torch tensors on the GPU: ``init_params`` makes random ones of
+the architecture, ``load_from_torch_checkpoint`` / ``load_from_pretrained``
+read the HF state-spaces checkpoint format (``pytorch_model.bin`` or
+safetensors, from local files: there is no download).
 
 Decode, MI355X-first: every layer's conv and SSM state lives in one
 (n_layer, ...) tensor that the decode kernels update in place, so a step
@@ -20,7 +22,10 @@ reference gets the equivalent from jax.jit + lax.scan over layers
 
 from __future__ import annotations
 
+import glob
+import json
 import math
+import os
 from dataclasses import dataclass
 
 import torch
@@ -72,12 +77,46 @@ class Mamba2Config:
     def d_in_proj(self):
         return 2 * self.d_inner + 2 * self.ngroups * self.d_state + self.nheads
 
+    @classmethod
+    def from_pretrained(cls, model_name_or_path: str) -> "Mamba2Config":
+        """The config of a local model directory (or its config.json) in the
+        HF state-spaces format (reference :84-113, same key map and defaults).
+        Hub ids are not fetched: there is no network."""
+        path = model_name_or_path
+        if os.path.isdir(path):
+            path = os.path.join(path, "config.json")
+        if not os.path.isfile(path):
+            raise FileNotFoundError(f"{model_name_or_path!r}: no local config.json (hub downloads "
+                                    "are not supported; pass a local model directory)")
+        with open(path) as f:
+            data = json.load(f)
+        ssm = data.get("ssm_cfg", {})
+        return cls(d_model=data.get("d_model", 2048), n_layer=data.get("n_layer", 48),
+                   vocab_size=data.get("vocab_size", 50277),
+                   pad_vocab_size_multiple=data.get("pad_vocab_size_multiple", 16),
+                   d_state=ssm.get("d_state", 128), d_conv=ssm.get("d_conv", 4),
+                   expand=ssm.get("expand", 2), headdim=ssm.get("headdim", 64),
+                   ngroups=ssm.get("ngroups", 1), chunk_size=ssm.get("chunk_size", 256),
+                   rmsnorm=data.get("rms_norm", True),
+                   residual_in_fp32=data.get("residual_in_fp32", True),
+                   tie_embeddings=data.get("tie_embeddings", True))
+
     def mixer_dims(self):
         return MixerDims(d_ssm=self.d_inner, d_mlp=0, ngroups=self.ngroups, d_state=self.d_state,
                          headdim=self.headdim, nheads=self.nheads, d_conv=self.d_conv,
                          chunk_size=self.chunk_size, rmsnorm=self.rmsnorm,
                          norm_before_gate=self.norm_before_gate, D_has_hdim=self.D_has_hdim,
                          dt_limit=tuple(self.dt_limit))
+
+
+# the reference's predefined sizes (:119-125)
+MAMBA2_CONFIGS = {
+    "mamba2-130m": Mamba2Config(d_model=768, n_layer=24),
+    "mamba2-370m": Mamba2Config(d_model=1024, n_layer=48),
+    "mamba2-780m": Mamba2Config(d_model=1536, n_layer=48),
+    "mamba2-1.3b": Mamba2Config(d_model=2048, n_layer=48),
+    "mamba2-2.7b": Mamba2Config(d_model=2560, n_layer=64),
+}
 
 
 def rms_norm(x, weight, eps=1e-5, *, out_dtype=None, residual=None):
@@ -119,6 +158,89 @@ def init_params(cfg: Mamba2Config, dtype=torch.bfloat16, device=None, seed=0):
     return {"embedding": {"weight": emb}, "layers": layers,
             "norm_f_weight": torch.ones(cfg.d_model, device=dev, dtype=dtype),
             "lm_head_weight": emb}
+
+
+def read_state_dict(path):
+    """A checkpoint's tensors on the CPU: ``path`` is a ``pytorch_model.bin``,
+    a ``.safetensors`` file, or a directory holding (possibly sharded)
+    ``*.safetensors`` or ``pytorch_model*.bin`` files.  Only loaders that
+    execute nothing from the file are used (safetensors,
+    ``torch.load(weights_only=True)``)."""
+    if os.path.isdir(path):
+        files = sorted(glob.glob(os.path.join(path, "*.safetensors"))) or \
+            sorted(glob.glob(os.path.join(path, "pytorch_model*.bin")))
+        if not files:
+            raise FileNotFoundError(f"{path}: no *.safetensors or pytorch_model*.bin files")
+    elif os.path.isfile(path):
+        files = [path]
+    else:
+        raise FileNotFoundError(path)
+    sd = {}
+    for f in files:
+        if f.endswith(".safetensors"):
+            from safetensors.torch import load_file
+            sd.update(load_file(f, device="cpu"))
+        else:
+            sd.update(torch.load(f, map_location="cpu", weights_only=True))
+    return sd
+
+
+def load_from_torch_checkpoint(config: Mamba2Config, checkpoint_path, dtype=torch.float32,
+                               device=None):
+    """Parameters in the reference's dict layout from an HF state-spaces
+    checkpoint (reference :530-601, same key map): Linear weights (out, in)
+    become (in, out) kernels, conv1d (ch, 1, k) becomes (ch, k), dt_bias stays
+    float32, everything else takes ``dtype``; the LM head is the embedding
+    when the config ties them.  ``checkpoint_path``: see ``read_state_dict``
+    (the reference reads ``pytorch_model.bin`` only).  ``device``: default
+    cuda.  Linear biases are read when the config has them."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    sd = read_state_dict(checkpoint_path) if isinstance(checkpoint_path, (str, os.PathLike)) \
+        else checkpoint_path
+
+    def t(key, dt=dtype, op=None):
+        v = sd[key]
+        if op is not None:
+            v = op(v)
+        return v.to(dtype=dt).contiguous().to(dev)
+
+    linear_t = lambda v: v.t()
+    params = {"embedding": {"weight": t("backbone.embedding.weight")}, "layers": [],
+              "norm_f_weight": t("backbone.norm_f.weight")}
+    for i in range(config.n_layer):
+        pre = f"backbone.layers.{i}.mixer."
+        mixer = {
+            "in_proj_kernel": t(pre + "in_proj.weight", op=linear_t),
+            "conv1d_weight": t(pre + "conv1d.weight", op=lambda v: v.squeeze(1)),
+            "conv1d_bias": t(pre + "conv1d.bias") if pre + "conv1d.bias" in sd else None,
+            "dt_bias": t(pre + "dt_bias", torch.float32),
+            "A_log": t(pre + "A_log"),
+            "D": t(pre + "D"),
+            "norm_weight": t(pre + "norm.weight") if pre + "norm.weight" in sd else None,
+            "out_proj_kernel": t(pre + "out_proj.weight", op=linear_t),
+        }
+        if config.bias:
+            for name in ("in_proj", "out_proj"):
+                if pre + name + ".bias" in sd:
+                    mixer[name + "_bias"] = t(pre + name + ".bias")
+        params["layers"].append({"norm_weight": t(f"backbone.layers.{i}.norm.weight"),
+                                 "mixer": mixer})
+    params["lm_head_weight"] = params["embedding"]["weight"] if config.tie_embeddings \
+        else t("lm_head.weight")
+    return params
+
+
+def load_from_pretrained(model_name: str, dtype=torch.float32, device=None):
+    """(model, params, config) from a local model directory holding config.json
+    and the weights (reference :604-635, which downloads them from the hub
+    first; there is no network here, so a hub id or short name must be a local
+    directory)."""
+    if not os.path.isdir(model_name):
+        raise FileNotFoundError(f"{model_name!r} is not a local model directory (hub downloads "
+                                "are not supported)")
+    config = Mamba2Config.from_pretrained(model_name)
+    params = load_from_torch_checkpoint(config, model_name, dtype=dtype, device=device)
+    return Mamba2LMHeadModel(config), params, config
 
 
 def _sample_token(logits, generator, temperature=1.0, top_k=50):
@@ -279,4 +401,5 @@ class Mamba2LMHeadModel:
         return torch.cat(ids, dim=1)
 
 
-__all__ = ["Mamba2Config", "Mamba2LMHeadModel", "DecodeState", "init_params", "rms_norm"]
+__all__ = ["Mamba2Config", "Mamba2LMHeadModel", "DecodeState", "MAMBA2_CONFIGS", "init_params",
+           "load_from_pretrained", "load_from_torch_checkpoint", "read_state_dict", "rms_norm"]
