@@ -14,7 +14,8 @@ per-stage table (a second timed pass of K steps with HIP events recorded on the
 launch stream at every kernel boundary), a decode-step measurement (c4: 256 in-place
 selective_state_update steps) and the CPU baseline (the oracle's NumPy
 restatement of the reference's naive path, timed on a bounded head sample on
-this host's cores).
+this host's cores).  At c2 it also times the shape with fp32 inputs and each
+stage operator of the reference's API called on its own (stage_operators).
 """
 
 from __future__ import annotations
@@ -353,6 +354,58 @@ def bench_fp32_same_shape(cfg, steps=30, warmup=5):
             "tokens_per_s": c32.tokens / (ms * 1e-3)}
 
 
+def bench_stage_operators(cfg, calls=10, replays=5):
+    """Each stage operator of the reference's API called on its own at the
+    configuration's shape, as the reference's staged pipeline chains them
+    (kernels/ssd_combined.py:112-170): chunk_cumsum, chunk_state (float32
+    states), state_passing (float32 in, C's dtype out), bmm_chunk (float32 CB),
+    chunk_scan.  Per operator: GPU time from HIP-graph replays and its
+    compulsory HBM bytes (inputs read once, outputs written once)."""
+    import torch
+    from mamba2_jax import configs
+    from mamba2_jax.kernels.bmm_chunk_fwd import bmm_chunk_fwd
+    from mamba2_jax.kernels.chunk_cumsum_fwd import chunk_cumsum_fwd
+    from mamba2_jax.kernels.chunk_scan_fwd import chunk_scan_fwd
+    from mamba2_jax.kernels.chunk_state_fwd import chunk_state_fwd
+    from mamba2_jax.kernels.state_passing_fwd import state_passing_fwd
+    d = configs.make_ssd_inputs(cfg)
+    dev = torch.device("cuda")
+    T = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
+    t = lambda a, dt=None: torch.from_numpy(a).to(dev).to(dt or torch.float32)
+    x, dt, B, C = t(d["x"], T), t(d["dt"], T), t(d["B"], T), t(d["C"], T)
+    A, D, bias = t(d["A"]), t(d["D"]), t(d["dt_bias"])
+    Q, (b, L, H, P), (G, N) = cfg.chunk_size, x.shape, B.shape[2:]
+    nc = -(-L // Q)
+    dA, dto = chunk_cumsum_fwd(dt, A, Q, dt_bias=bias, dt_softplus=True)
+    st = chunk_state_fwd(x, B, dto, dA)
+    passed = state_passing_fwd(st.view(b, nc, H, P * N), dA[:, :, :, -1], chunk_size=Q,
+                               out_dtype=C.dtype)[0].view(b, nc, H, P, N)
+    cb = bmm_chunk_fwd(C, B, Q, output_dtype=torch.float32)
+    s = x.element_size()
+    ops = {
+        "chunk_cumsum": (lambda: chunk_cumsum_fwd(dt, A, Q, dt_bias=bias, dt_softplus=True),
+                         b * L * H * s + 2 * 4 * b * H * nc * Q),
+        "chunk_state": (lambda: chunk_state_fwd(x, B, dto, dA),
+                        b * L * H * P * s + b * L * G * N * s + 2 * 4 * b * H * nc * Q
+                        + 4 * b * nc * H * P * N),
+        "state_passing": (lambda: state_passing_fwd(st.view(b, nc, H, P * N), dA[:, :, :, -1],
+                                                    chunk_size=Q, out_dtype=C.dtype),
+                          4 * b * nc * H * P * N + 4 * b * H * nc + s * b * nc * H * P * N
+                          + 4 * b * H * P * N),
+        "bmm_chunk": (lambda: bmm_chunk_fwd(C, B, Q, output_dtype=torch.float32),
+                      2 * b * L * G * N * s + 4 * b * nc * G * Q * Q),
+        "chunk_scan": (lambda: chunk_scan_fwd(cb, x, dto, dA, C, passed, D=D),
+                       4 * b * nc * G * Q * Q + b * L * H * P * s + 2 * 4 * b * H * nc * Q
+                       + b * L * G * N * s + s * b * nc * H * P * N + 4 * b * L * H * P),
+    }
+    out = {}
+    for name, (fn, by) in ops.items():
+        ms = _graph_time_ms(fn, calls, replays)
+        out[name] = {"ms": ms, "bytes": by, "hbm_gbs": by / ms / 1e6,
+                     "hbm_frac": by / ms / 1e6 / PEAK_HBM_GBS}
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -498,6 +551,7 @@ def main(argv=None):
     }
     if args.config == "c2":
         res["fp32_same_shape"] = bench_fp32_same_shape(cfg)
+        res["stage_operators"] = bench_stage_operators(cfg)
     if not args.no_decode:
         res["decode"] = bench_decode()
     if not args.no_cpu_baseline:
