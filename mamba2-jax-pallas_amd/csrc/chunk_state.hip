@@ -247,6 +247,7 @@ int launch_chunk_state(const m2_chunk_state_args& a, hipStream_t s) {
                M2_ERR_INVALID, "chunk_state: bad sizes (nheads must be a multiple of ngroups)");
     M2_REQUIRE(a.chunk_size % 16 == 0 && a.chunk_size <= 256, M2_ERR_UNSUPPORTED,
                "chunk_state: chunk_size must be a multiple of 16 and <= 256");
+    if (chunk_state_fast_supported(a)) return launch_chunk_state_fast(a, s);
     StateArgs sa{};
     sa.x = a.x; sa.B = a.B; sa.dt = a.dt; sa.dA = a.dA_cumsum; sa.seq_idx = a.seq_idx;
     sa.out = a.states;

@@ -26,6 +26,8 @@ int launch_skinny_gemm(const m2_skinny_gemm_args& a, hipStream_t stream);
 // == 0 (<= 256): one workgroup per (sequence, head, 64-column dstate block)
 bool varlen_states_fast_supported(const m2_chunk_state_varlen_args& a);
 int launch_varlen_states(const m2_chunk_state_varlen_args& a, hipStream_t stream);
+bool chunk_state_fast_supported(const m2_chunk_state_args& a);
+int launch_chunk_state_fast(const m2_chunk_state_args& a, hipStream_t stream);
 
 // fused bmm_chunk + chunk_scan of the combined forward (bf16 inputs)
 bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size);

@@ -1,15 +1,24 @@
-// chunk_state_varlen for bf16 inputs, head dim 64 and dstate a multiple of 64:
-// the final state of each packed sequence s (batch 1) over the chunk c that
-// holds its last token,
+// One-shot state sums for bf16 inputs, head dim 64 and dstate a multiple of
+// 64, in two modes that share the kernel:
+//
+// chunk_state: the state of every chunk c of every batch row,
+//   out[b, c, h] = sum_{q < qhi} w[q] x[q, :]^T B[q, :],  qhi = min(Q, L - c Q)
+//   w[q]         = exp(min(dA[qhi - 1] - dA[q], 0)) dt[q],
+// 0 where seq_idx[q] differs from seq_idx at the chunk's last position (all of
+// the chunk if that is negative);
+//
+// chunk_state_varlen: the final state of each packed sequence s (batch 1)
+// over the chunk c that holds its last token,
 //   out[s, h] = sum_{q in [qlo, qhi)} w[q] x[q, :]^T B[q, :]  (+ carry)
 //   w[q]      = exp(min(dA[qhi - 1] - dA[q], 0)) dt[q]
 //   carry     = exp(dA[qhi - 1]) states[c, h]   when s started before chunk c
 // with q the positions of chunk c, [qlo, qhi) the part of s in it, and
 // states[c] the state entering chunk c.
 //
-// One workgroup per (sequence, head, 64-column dstate block): 6144 at the
-// packed 47b shape, several per CU, so a one-shot kernel hides its latency
-// by occupancy.  The x rows [Q x 64] and the block's B rows [Q x 64] arrive by
+// One workgroup per (chunk or sequence, head, 64-column dstate block): 8192
+// chunk states at the nemotron-h-8b shape, 6144 varlen states at the packed
+// 47b shape, several per CU, so a one-shot kernel hides its latency by
+// occupancy.  The x rows [Q x 64] and the block's B rows [Q x 64] arrive by
 // direct global -> LDS loads (16-byte chunks of each 128-byte row
 // XOR-swizzled, so the transposed reads hit distinct banks); the weights are
 // computed from dA / dt while they are in flight.  Wavefront w owns head-dim
@@ -20,8 +29,8 @@
 // that each output row of 64 fp32 (and its carry row) moves as 16 lanes x 16
 // bytes.
 //
-// Follows reference kernels/chunk_state_fwd.py:448-597 (varlen states) and
-// :239-269 (weights).
+// Follows reference kernels/chunk_state_fwd.py:104-187 (product), :239-269
+// (weights, seq_idx rule) and :448-597 (varlen states).
 #include "m2_internal.h"
 
 namespace {
@@ -45,14 +54,16 @@ __host__ __device__ inline int tiles_bytes(int Q) {
 struct VarlenArgs {
     const bf16* x;
     const bf16* B;
-    const float* dt;        // [H, nc, Q]
-    const float* dA;        // [H, nc, Q]
-    const int32_t* cu;      // [nseq + 1]
-    const void* states;     // [nc, H, P, N]
-    float* out;             // [nseq, H, P, N]
+    const float* dt;        // [b, H, nc, Q]
+    const float* dA;        // [b, H, nc, Q]
+    const int32_t* cu;      // varlen: [nseq + 1]
+    const void* states;     // varlen: [nc, H, P, N]
+    const int32_t* seq;     // chunk mode: [b, L] or NULL
+    float* out;             // varlen: [nseq, H, P, N]; chunk mode: [b, nc, H, P, N]
     int L, H, G, N, Q, nc, nblk, nwork, states_bf16;
 };
 
+template <bool CHUNK>
 __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     extern __shared__ __align__(16) char smem[];
     const int Q = a.Q, H = a.H, N = a.N;
@@ -63,37 +74,47 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
 
     const int work = xcd_remap(blockIdx.x, a.nwork);
     const int nb = work % a.nblk;
-    const int sh = work / a.nblk;
-    const int h = sh % H, s = sh / H;
+    const int sh = work / a.nblk;              // (sequence or batch row x chunk) x H + h
+    const int h = sh % H;
     const int g = h / (H / a.G);
     const int lane = threadIdx.x & 63, w = wave_id();
     const int ln = lane & 15, kg = lane >> 4;
-    float* op = a.out + (((int64_t)s * H + h) * P) * N + NB * nb;
+    float* op = a.out + ((int64_t)sh * P) * N + NB * nb;
 
-    // clamp malformed boundaries into [0, L] so every access stays in bounds
-    const int end = min(max(a.cu[s + 1], 0), a.L);
-    const int start = min(max(a.cu[s], 0), end);
-    if (end <= start) {                         // empty sequence: zero state
-        for (int i = threadIdx.x; i < P * NB / 4; i += THREADS) {
-            const int r = i / (NB / 4), c4 = 4 * (i % (NB / 4));
-            *reinterpret_cast<float4*>(op + (int64_t)r * N + c4) = make_float4(0.f, 0.f, 0.f, 0.f);
+    int c, bi = 0, qlo = 0, qhi;
+    bool carry = false;
+    if (CHUNK) {
+        c = (sh / H) % a.nc;
+        bi = (sh / H) / a.nc;
+        qhi = min(Q, a.L - c * Q);
+    } else {
+        const int s = sh / H;
+        // clamp malformed boundaries into [0, L] so every access stays in bounds
+        const int end = min(max(a.cu[s + 1], 0), a.L);
+        const int start = min(max(a.cu[s], 0), end);
+        if (end <= start) {                     // empty sequence: zero state
+            for (int i = threadIdx.x; i < P * NB / 4; i += THREADS) {
+                const int r = i / (NB / 4), c4 = 4 * (i % (NB / 4));
+                *reinterpret_cast<float4*>(op + (int64_t)r * N + c4) = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            return;
         }
-        return;
+        c = (end - 1) / Q;
+        qlo = max(start - c * Q, 0);
+        qhi = end - c * Q;
+        carry = start < c * Q;
     }
-    const int c = (end - 1) / Q;
-    const int qlo = max(start - c * Q, 0), qhi = end - c * Q;
-    const bool carry = start < c * Q;
 
     // ---- direct loads of the chunk's x rows and the block's B rows: load u
     // (64 lanes x 16 bytes = 8 rows) goes to tile bytes [1024 u, 1024 u + 1024);
-    // rows past the end of the sequence batch are clamped (their weight is 0)
-    const int64_t t0 = (int64_t)c * Q;
+    // rows past the end of the batch row are clamped (their weight is 0)
+    const int64_t t0 = (int64_t)bi * a.L + (int64_t)c * Q, tend = (int64_t)bi * a.L + a.L - 1;
     const bf16* xsrc = a.x + (int64_t)h * P;
     const bf16* bsrc = a.B + (int64_t)g * N + NB * nb;
     const uint32_t xl = lds_addr(xs);
     for (int u = w; u < Q * CPR / 64; u += THREADS / 64) {
         const int gi = 64 * u + lane, r = gi / CPR;
-        const int64_t t = min(t0 + r, (int64_t)a.L - 1);
+        const int64_t t = min(t0 + r, tend);
         const int col = ((gi % CPR) ^ swz(r)) * 8;
         dma16(xsrc + t * H * P + col, xl + 1024 * u);
         dma16(bsrc + t * a.G * N + col, xl + XB + 1024 * u);
@@ -106,7 +127,7 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     const int orr = 16 * w + (lane >> 4), occ = 4 * (lane & 15);
     bf16x4 cv16[4];
     float4 cv32[4];
-    if (carry) {
+    if (!CHUNK && carry) {
 #pragma unroll
         for (int it = 0; it < 4; ++it) {
             const int64_t e = soff + (int64_t)(orr + 4 * it) * N + occ;
@@ -118,11 +139,16 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     }
 
     // ---- weights (while the tiles are in flight)
-    const float* dAp = a.dA + ((int64_t)h * a.nc + c) * Q;
-    const float* dtp = a.dt + ((int64_t)h * a.nc + c) * Q;
+    const float* dAp = a.dA + (((int64_t)bi * H + h) * a.nc + c) * Q;
+    const float* dtp = a.dt + (((int64_t)bi * H + h) * a.nc + c) * Q;
     const float dA_ref = dAp[qhi - 1];
-    for (int q = threadIdx.x; q < Q; q += THREADS)
-        wq[q] = (q >= qlo && q < qhi) ? expf(fminf(dA_ref - dAp[q], 0.f)) * dtp[q] : 0.f;
+    const int32_t* seq = CHUNK && a.seq ? a.seq + t0 : nullptr;
+    const int se = seq ? seq[qhi - 1] : 0;
+    for (int q = threadIdx.x; q < Q; q += THREADS) {
+        float v = (q >= qlo && q < qhi) ? expf(fminf(dA_ref - dAp[q], 0.f)) * dtp[q] : 0.f;
+        if (seq && q < qhi && (se < 0 || seq[q] != se)) v = 0.f;
+        wq[q] = v;
+    }
     wait_vmem<0>();
     __syncthreads();
 
@@ -176,12 +202,12 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         *reinterpret_cast<f32x4*>(orow + ln * OS + 16 * j + 4 * kg) = acc[j];
-    const float cs = carry ? expf(dA_ref) : 0.f;
+    const float cs = !CHUNK && carry ? expf(dA_ref) : 0.f;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int r = orr + 4 * it;
         float4 v = *reinterpret_cast<const float4*>(ot + r * OS + occ);
-        if (carry) {
+        if (!CHUNK && carry) {
             float cv[4];
             if (a.states_bf16) {
 #pragma unroll
@@ -193,6 +219,17 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
         }
         *reinterpret_cast<float4*>(op + (int64_t)r * N + occ) = v;
     }
+}
+
+template <bool CHUNK>
+int launch_k(const VarlenArgs& k, hipStream_t s, const char* who) {
+    const size_t shm = (size_t)tiles_bytes(k.Q) + (size_t)k.Q * 4;
+    if (shm > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(k_varlen_states<CHUNK>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return m2::set_error(M2_ERR_LAUNCH, "%s: cannot reserve %zu B of LDS", who, shm);
+    k_varlen_states<CHUNK><<<(unsigned)k.nwork, THREADS, shm, s>>>(k);
+    return m2::check_launch(who);
 }
 
 }  // namespace
@@ -216,13 +253,28 @@ int launch_varlen_states(const m2_chunk_state_varlen_args& a, hipStream_t s) {
     const int64_t nwork = a.nseq * a.nheads * k.nblk;
     M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "varlen_states: too many workgroups");
     k.nwork = (int)nwork;
-    const size_t shm = (size_t)tiles_bytes(k.Q) + (size_t)k.Q * 4;
-    if (shm > 65536 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k_varlen_states),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
-        return set_error(M2_ERR_LAUNCH, "varlen_states: cannot reserve %zu B of LDS", shm);
-    k_varlen_states<<<(unsigned)k.nwork, THREADS, shm, s>>>(k);
-    return check_launch("varlen_states");
+    return launch_k<false>(k, s, "varlen_states");
+}
+
+bool chunk_state_fast_supported(const m2_chunk_state_args& a) {
+    return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
+           a.chunk_size % 32 == 0 && a.chunk_size <= 256;
+}
+
+int launch_chunk_state_fast(const m2_chunk_state_args& a, hipStream_t s) {
+    M2_REQUIRE(chunk_state_fast_supported(a), M2_ERR_UNSUPPORTED,
+               "chunk_state: unsupported shape / dtype for the one-shot kernel");
+    VarlenArgs k{};
+    k.x = (const bf16*)a.x; k.B = (const bf16*)a.B; k.dt = a.dt; k.dA = a.dA_cumsum;
+    k.seq = a.seq_idx; k.out = a.states;
+    k.L = (int)a.seqlen; k.H = (int)a.nheads; k.G = (int)a.ngroups; k.N = (int)a.dstate;
+    k.Q = (int)a.chunk_size; k.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
+    k.nblk = (int)(a.dstate / NB);
+    const int64_t nwork = a.batch * k.nc * a.nheads * k.nblk;
+    M2_REQUIRE(nwork < (1ll << 31) && a.batch * a.seqlen < (1ll << 31), M2_ERR_UNSUPPORTED,
+               "chunk_state: too many workgroups");
+    k.nwork = (int)nwork;
+    return launch_k<true>(k, s, "chunk_state");
 }
 
 }  // namespace m2
