@@ -295,6 +295,8 @@ int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t s) {
                "chunk_scan: chunk_size must be a multiple of 16 and <= 256");
     M2_REQUIRE(a.states_dtype == M2_F32 || a.states_dtype == M2_BF16, M2_ERR_UNSUPPORTED,
                "chunk_scan: states dtype %d", a.states_dtype);
+    // bf16, headdim 64, no z: the fused scan kernel with CB read in
+    if (scan_fused_cb_supported(a)) return launch_scan_fused_cb(a, s);
     ScanArgs sa{};
     sa.cb = a.cb; sa.x = a.x; sa.dt = a.dt; sa.dA = a.dA_cumsum; sa.C = a.C; sa.states = a.states;
     sa.D = a.D; sa.z = a.z; sa.seq_idx = a.seq_idx; sa.out = a.out; sa.out_x = a.out_x;

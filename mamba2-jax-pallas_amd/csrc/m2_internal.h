@@ -31,6 +31,8 @@ int launch_chunk_state_fast(const m2_chunk_state_args& a, hipStream_t stream);
 
 // fused bmm_chunk + chunk_scan of the combined forward (bf16 inputs)
 bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size);
+bool scan_fused_cb_supported(const m2_chunk_scan_args& a);
+int launch_scan_fused_cb(const m2_chunk_scan_args& a, hipStream_t stream);
 int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const float* dt_out,
                       const void* states_passed, hipStream_t stream);
 

@@ -41,6 +41,13 @@
 //     (A = B rows, B = C rows), so they feed 16x16x16 MFMAs without data
 //     movement; W is split into bf16 hi + lo parts (two MFMAs, near-fp32).
 //
+// The same kernel serves the stage operator chunk_scan (bf16, no z) when CB
+// comes in from bmm_chunk: the CB^T tiles are then read from HBM (fp32 or
+// bf16, rounded to bf16 as the reference's chunk_scan kernel does,
+// kernels/chunk_scan_fwd.py:386-394) with only the causal mask applied, since
+// the seq_idx mask of CB belongs to bmm_chunk (kernels/chunk_scan_fwd.py
+// :295-322 masks C only).
+//
 // Follows reference ops/ssd_naive.py:189-318 and kernels/chunk_scan_fwd.py
 // :294-322 / kernels/bmm_chunk_fwd.py:353-372 (seq_idx masks).
 #include <algorithm>
@@ -102,8 +109,9 @@ struct ScanFusedArgs {
     const float* D;
     const bf16* z;
     const int32_t* seq_idx;
+    const void* cb;        // given CB [b, nc, G, Q, Q] (fp32 or bf16), or NULL: built here
     float* out;
-    int D_has_hdim;
+    int D_has_hdim, cb_bf16;
     int L, H, G, nc, hpg, nwork;
     int hps, nslice;          // heads per workgroup (a slice of the group's), slices
 };
@@ -230,7 +238,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     if (loader) {
         const bf16* Bg = a.B + (tok0 * G + g) * N;
 #pragma unroll
-        for (int uu = 0; uu < S::BL; ++uu) {
+        for (int uu = 0; uu < (a.cb ? 0 : S::BL); ++uu) {
             const int u = li * S::BL + uu;
             const int gi = 64 * u + lane, r = gi / SCPR;
             dma16(Bg + min(r, valid - 1) * rs + 8 * ((gi % SCPR) ^ sswz<SCPR>(r)),
@@ -251,12 +259,27 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
             const int kt = second ? j - t1 - 1 : j;
             const int m = 16 * t + ln;
             f32x4 acc = zero4();
+            if (a.cb) {
+                // row m, columns 16 kt + 4 kg .. + 3 of the given CB
+                const int64_t o = ((((int64_t)bi * nc + ci) * G + g) * Q + m) * Q + 16 * kt + 4 * kg;
+                if (a.cb_bf16) {
+                    const bf16x4 c4 = *reinterpret_cast<const bf16x4*>(
+                        reinterpret_cast<const bf16*>(a.cb) + o);
 #pragma unroll
-            for (int ns = 0; ns < NS; ++ns) {
-                const int r = 16 * kt + ln;
-                const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(
-                    bt + r * (2 * N) + (((4 * ns + kg) ^ sswz<SCPR>(r)) * 16));
-                acc = mma32(bfr, second ? cfr[1][ns] : cfr[0][ns], acc);
+                    for (int i = 0; i < 4; ++i) acc[i] = (float)c4[i];
+                } else {
+                    const float4 c4 = *reinterpret_cast<const float4*>(
+                        reinterpret_cast<const float*>(a.cb) + o);
+                    acc[0] = c4.x; acc[1] = c4.y; acc[2] = c4.z; acc[3] = c4.w;
+                }
+            } else {
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns) {
+                    const int r = 16 * kt + ln;
+                    const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(
+                        bt + r * (2 * N) + (((4 * ns + kg) ^ sswz<SCPR>(r)) * 16));
+                    acc = mma32(bfr, second ? cfr[1][ns] : cfr[0][ns], acc);
+                }
             }
             bf16x4 v4;
 #pragma unroll
@@ -264,7 +287,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                 const int k = 16 * kt + 4 * kg + i;
                 float v = acc[i];
                 if (k > m || m >= valid) v = 0.f;          // causal, k <= m < valid
-                if (a.seq_idx && seqs[m] != seqs[k]) v = 0.f;
+                if (!a.cb && a.seq_idx && seqs[m] != seqs[k]) v = 0.f;
                 v4[i] = (bf16)v;                            // CB is bf16 (reference)
             }
             cbl[pi][j][lane] = v4;
@@ -611,8 +634,12 @@ bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size) {
            (chunk_size == 64 || chunk_size == 128);
 }
 
-int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const float* dto,
-                      const void* passed, hipStream_t s) {
+namespace {
+
+// f: pointers filled in; a: the sizes (batch, seqlen, nheads, ngroups,
+// headdim, dstate, chunk_size); hz: with the z gate
+template <typename Sizes>
+int launch_scan_fused_common(ScanFusedArgs& f, const Sizes& a, bool hz, hipStream_t s) {
     M2_REQUIRE(a.ngroups > 0 && a.nheads % a.ngroups == 0, M2_ERR_INVALID,
                "scan_fused: nheads %% ngroups != 0");
     const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
@@ -625,14 +652,9 @@ int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const floa
     nslice = (hpg + hps - 1) / hps;
     const int64_t nwork = items * nslice;
     M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "scan_fused: too many blocks");
-    ScanFusedArgs f{};
-    f.x = (const bf16*)a.x; f.B = (const bf16*)a.B; f.C = (const bf16*)a.C;
-    f.states = (const bf16*)passed; f.dt = dto; f.dA = dA; f.D = a.D; f.z = (const bf16*)a.z;
-    f.seq_idx = a.seq_idx; f.out = a.out; f.D_has_hdim = a.D_has_hdim;
     f.L = (int)a.seqlen; f.H = (int)a.nheads; f.G = (int)a.ngroups; f.nc = (int)nc;
     f.hpg = hpg; f.nwork = (int)nwork; f.hps = hps; f.nslice = nslice;
     void (*kern)(ScanFusedArgs) = nullptr;
-    const bool hz = a.z != nullptr;
 #define M2_SF_CASE(NSV, QTV)                                                        \
     if (a.dstate == 32 * NSV && a.chunk_size == 16 * QTV)                           \
         kern = hz ? k_scan_fused<NSV, QTV, true> : k_scan_fused<NSV, QTV, false>;
@@ -642,7 +664,34 @@ int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const floa
 #undef M2_SF_CASE
     M2_REQUIRE(kern && a.headdim == P, M2_ERR_UNSUPPORTED, "scan_fused: unsupported sizes");
     kern<<<(unsigned)nwork, THREADS, 0, s>>>(f);
-    return check_launch("scan_fused");
+    return m2::check_launch("scan_fused");
+}
+
+}  // namespace
+
+int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const float* dto,
+                      const void* passed, hipStream_t s) {
+    ScanFusedArgs f{};
+    f.x = (const bf16*)a.x; f.B = (const bf16*)a.B; f.C = (const bf16*)a.C;
+    f.states = (const bf16*)passed; f.dt = dto; f.dA = dA; f.D = a.D; f.z = (const bf16*)a.z;
+    f.seq_idx = a.seq_idx; f.out = a.out; f.D_has_hdim = a.D_has_hdim;
+    return launch_scan_fused_common(f, a, a.z != nullptr, s);
+}
+
+bool scan_fused_cb_supported(const m2_chunk_scan_args& a) {
+    return a.dtype == M2_BF16 && a.states_dtype == M2_BF16 && !a.z && !a.out_x &&
+           (a.cb_dtype == M2_F32 || a.cb_dtype == M2_BF16) &&
+           scan_fused_supported(a.headdim, a.dstate, a.chunk_size);
+}
+
+int launch_scan_fused_cb(const m2_chunk_scan_args& a, hipStream_t s) {
+    M2_REQUIRE(scan_fused_cb_supported(a), M2_ERR_UNSUPPORTED,
+               "chunk_scan: unsupported shape / dtype for the fused kernel");
+    ScanFusedArgs f{};
+    f.x = (const bf16*)a.x; f.C = (const bf16*)a.C; f.states = (const bf16*)a.states;
+    f.dt = a.dt; f.dA = a.dA_cumsum; f.D = a.D; f.seq_idx = a.seq_idx; f.out = a.out;
+    f.D_has_hdim = a.D_has_hdim; f.cb = a.cb; f.cb_bf16 = a.cb_dtype == M2_BF16;
+    return launch_scan_fused_common(f, a, false, s);
 }
 
 }  // namespace m2

@@ -254,6 +254,36 @@ def test_chunk_scan_bf16_cb_and_states():
     check(out, wo, TOL["bf16"], "out")
 
 
+@pytest.mark.parametrize("b,L,H,N,G,Q,Dhp,lens", [
+    (1, 512, 16, 128, 2, 128, False, None),
+    (2, 300, 8, 64, 4, 64, True, None),                  # L % Q != 0, D per head dim
+    (1, 384, 8, 256, 8, 128, False, None),
+    (2, 512, 8, 128, 1, 64, False, [[200, 312], [100, 412]]),
+    (1, 4096, 128, 128, 8, 128, False, None),            # nemotron-h-8b layer shape
+])
+def test_chunk_scan_fused_cb(b, L, H, N, G, Q, Dhp, lens):
+    """bf16 x / C, CB from bmm_chunk (fp32) and bf16 states, no z: the stage
+    operator runs on the fused scan kernel with CB read in (rounded to bf16,
+    causal mask only: the seq_idx mask of CB is bmm_chunk's)."""
+    P = 64
+    announce("chunk_scan fused, CB given", b, L, H, N, G, Q, Dhp, lens)
+    d = _inputs(b, L, H, G, P, N, Q, "bf16", seed=L + N + Q)
+    seq = seq_idx_from_lengths(lens) if lens else None
+    wA, wdt = O.chunk_cumsum(d["dt"], d["A"], Q, d["dt_bias"], True)
+    wA, wdt = wA.astype(np.float32), wdt.astype(np.float32)
+    CB = O.bmm_chunk(d["C"], d["B"], Q, seq_idx=seq).astype(np.float32)
+    nc = math.ceil(L / Q)
+    states = O.bf16_round(0.5 * np.random.default_rng(4).standard_normal((b, nc, H, P, N)))
+    D = np.random.default_rng(5).uniform(0.5, 1.5, (H, P) if Dhp else H).astype(np.float32)
+    out, out_x = chunk_scan_fwd(dev(CB), dev(d["x"], torch.bfloat16), dev(wdt), dev(wA),
+                                dev(d["C"], torch.bfloat16), dev(states, torch.bfloat16),
+                                D=dev(D), seq_idx=dev(seq))
+    assert out_x is None
+    wo, _ = O.chunk_scan(CB, d["x"], wdt, wA, d["C"], states, D=D, seq_idx=seq,
+                         round_fn=O.round_fn_for("bf16"))
+    check(out, wo, TOL["bf16"], "out")
+
+
 def test_chunk_scan_large_decay_is_stable():
     """|dA| inside a chunk far beyond 80: the factored exp(dA_m) * exp(-dA_k) form
     overflows there; the kernel evaluates exp(dA_m - dA_k) directly."""
