@@ -62,27 +62,37 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
         typename M::frag bf[CT];
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) bf[ct] = bok[ct] ? load_frag(bp[ct] + k0) : zf;
+        // transposed product (A = b rows, B = a rows): lane (ln, kg) ends with
+        // row r0 + ln, columns 16 ct + 4 kg + i -- four consecutive outputs
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[ct] = M::mma(af, bf[ct], acc[ct]);
+        for (int ct = 0; ct < CT; ++ct) acc[ct] = M::mma(bf[ct], af, acc[ct]);
     }
 
     TO* op = out + ((((int64_t)bi * nc + c) * G + g) * Q) * Q;
+    const int row = arow;
+    int srow = 0;
+    if (seq_idx) srow = (c * Q + row) < L ? seq_idx[tbase + row] : -1;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-        const int col = cb * 64 + ct * 16 + ln;
-        if (col >= Q) continue;
-        int scol = 0;
-        if (seq_idx) scol = (c * Q + col) < L ? seq_idx[tbase + col] : -1;
+        const int col0 = cb * 64 + ct * 16 + 4 * kg;
+        if (col0 >= Q) continue;
+        float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int row = r0 + kg * 4 + i;
-            float v = acc[ct][i];
-            if (causal && col > row) v = 0.f;
+            const int col = col0 + i;
+            v[i] = acc[ct][i];
+            if (causal && col > row) v[i] = 0.f;
             if (seq_idx) {
-                const int srow = (c * Q + row) < L ? seq_idx[tbase + row] : -1;
-                if (srow != scol) v = 0.f;
+                const int scol = (c * Q + col) < L ? seq_idx[tbase + col] : -1;
+                if (srow != scol) v[i] = 0.f;
             }
-            op[(int64_t)row * Q + col] = from_f32<TO>(v);
+        }
+        TO* dst = op + (int64_t)row * Q + col0;
+        if constexpr (sizeof(TO) == 4) {
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            const bf16x4 o = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+            *reinterpret_cast<bf16x4*>(dst) = o;
         }
     }
 }

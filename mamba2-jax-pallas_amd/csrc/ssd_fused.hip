@@ -151,7 +151,8 @@ struct Shape {
     static_assert(WAIT01 <= 63, "vmcnt range");
 };
 
-template <int NS, int QT, bool HASZ>
+// CBIN: CB given in a.cb (the chunk_scan stage operator) instead of built here
+template <int NS, int QT, bool HASZ, bool CBIN>
 __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     typedef Shape<NS, QT, HASZ> S;
     constexpr int N = S::N, Q = S::Q, NPAIRS = S::NPAIRS, PTW = S::PTW, R = S::R;
@@ -238,7 +239,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
     if (loader) {
         const bf16* Bg = a.B + (tok0 * G + g) * N;
 #pragma unroll
-        for (int uu = 0; uu < (a.cb ? 0 : S::BL); ++uu) {
+        for (int uu = 0; uu < (CBIN ? 0 : S::BL); ++uu) {
             const int u = li * S::BL + uu;
             const int gi = 64 * u + lane, r = gi / SCPR;
             dma16(Bg + min(r, valid - 1) * rs + 8 * ((gi % SCPR) ^ sswz<SCPR>(r)),
@@ -259,7 +260,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
             const int kt = second ? j - t1 - 1 : j;
             const int m = 16 * t + ln;
             f32x4 acc = zero4();
-            if (a.cb) {
+            if (CBIN) {
                 // row m, columns 16 kt + 4 kg .. + 3 of the given CB
                 const int64_t o = ((((int64_t)bi * nc + ci) * G + g) * Q + m) * Q + 16 * kt + 4 * kg;
                 if (a.cb_bf16) {
@@ -287,7 +288,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_fused(ScanFusedArgs a) {
                 const int k = 16 * kt + 4 * kg + i;
                 float v = acc[i];
                 if (k > m || m >= valid) v = 0.f;          // causal, k <= m < valid
-                if (!a.cb && a.seq_idx && seqs[m] != seqs[k]) v = 0.f;
+                if (!CBIN && a.seq_idx && seqs[m] != seqs[k]) v = 0.f;
                 v4[i] = (bf16)v;                            // CB is bf16 (reference)
             }
             cbl[pi][j][lane] = v4;
@@ -637,9 +638,9 @@ bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size) {
 namespace {
 
 // f: pointers filled in; a: the sizes (batch, seqlen, nheads, ngroups,
-// headdim, dstate, chunk_size); hz: with the z gate
+// headdim, dstate, chunk_size); hz: with the z gate; cbin: CB given in f.cb
 template <typename Sizes>
-int launch_scan_fused_common(ScanFusedArgs& f, const Sizes& a, bool hz, hipStream_t s) {
+int launch_scan_fused_common(ScanFusedArgs& f, const Sizes& a, bool hz, bool cbin, hipStream_t s) {
     M2_REQUIRE(a.ngroups > 0 && a.nheads % a.ngroups == 0, M2_ERR_INVALID,
                "scan_fused: nheads %% ngroups != 0");
     const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
@@ -657,7 +658,8 @@ int launch_scan_fused_common(ScanFusedArgs& f, const Sizes& a, bool hz, hipStrea
     void (*kern)(ScanFusedArgs) = nullptr;
 #define M2_SF_CASE(NSV, QTV)                                                        \
     if (a.dstate == 32 * NSV && a.chunk_size == 16 * QTV)                           \
-        kern = hz ? k_scan_fused<NSV, QTV, true> : k_scan_fused<NSV, QTV, false>;
+        kern = cbin ? k_scan_fused<NSV, QTV, false, true>                          \
+                    : hz ? k_scan_fused<NSV, QTV, true, false> : k_scan_fused<NSV, QTV, false, false>;
     M2_SF_CASE(2, 4) M2_SF_CASE(2, 8)
     M2_SF_CASE(4, 4) M2_SF_CASE(4, 8)
     M2_SF_CASE(8, 4) M2_SF_CASE(8, 8)
@@ -675,7 +677,7 @@ int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const floa
     f.x = (const bf16*)a.x; f.B = (const bf16*)a.B; f.C = (const bf16*)a.C;
     f.states = (const bf16*)passed; f.dt = dto; f.dA = dA; f.D = a.D; f.z = (const bf16*)a.z;
     f.seq_idx = a.seq_idx; f.out = a.out; f.D_has_hdim = a.D_has_hdim;
-    return launch_scan_fused_common(f, a, a.z != nullptr, s);
+    return launch_scan_fused_common(f, a, a.z != nullptr, false, s);
 }
 
 bool scan_fused_cb_supported(const m2_chunk_scan_args& a) {
@@ -691,7 +693,7 @@ int launch_scan_fused_cb(const m2_chunk_scan_args& a, hipStream_t s) {
     f.x = (const bf16*)a.x; f.C = (const bf16*)a.C; f.states = (const bf16*)a.states;
     f.dt = a.dt; f.dA = a.dA_cumsum; f.D = a.D; f.seq_idx = a.seq_idx; f.out = a.out;
     f.D_has_hdim = a.D_has_hdim; f.cb = a.cb; f.cb_bf16 = a.cb_dtype == M2_BF16;
-    return launch_scan_fused_common(f, a, false, s);
+    return launch_scan_fused_common(f, a, false, true, s);
 }
 
 }  // namespace m2
