@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define M2SSD_ABI_VERSION 2
+#define M2SSD_ABI_VERSION 3
 
 /* return codes */
 #define M2_OK               0
@@ -345,6 +345,37 @@ typedef struct {
     int32_t x_dtype, w_dtype, bias_dtype, y_dtype;
 } m2_skinny_gemm_args;
 int m2_skinny_gemm(const m2_skinny_gemm_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * skinny_gemm_norm: y = rms_norm_gated(x, norm_weight, z)[M, K] w[N, K]^T
+ * (+ bias) for M <= 4 and M * K <= 32768: m2_skinny_gemm whose input rows are
+ * normalised first, with m2_rms_norm_gated's arithmetic (groups of group_size
+ * <= 8 per row, the optional SiLU gate z before / after the norm, the
+ * reference's rounding points) and stored as bf16 -- done by every
+ * workgroup in its own LDS, so the norm takes no launch and no round trip.
+ * With residual != NULL the result (rounded to y_dtype) is added into the f32
+ * residual rows; y may then be NULL.  No counterpart operator in the
+ * reference: it fuses the pre-norm / gated norm of a decode step into the
+ * projection that follows (reference models/mamba2_lm.py:205-211 and
+ * modules/mamba2.py:536-541), for decode loops that are bound by launch
+ * latency.  Group, stride and base alignment: 4 elements.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void* x;                 /* [M, K] at x_row_stride, x_dtype            */
+    const void* z;                 /* [M, K] at z_row_stride, z_dtype, or NULL   */
+    const void* norm_weight;       /* [K], norm_weight_dtype                     */
+    int64_t x_row_stride, z_row_stride, group_size;
+    float   eps;
+    int32_t x_dtype, z_dtype, norm_weight_dtype, norm_before_gate;
+    const void* w;                 /* [N, K] at ldw, bf16                        */
+    const void* bias;              /* [N], bias_dtype, or NULL                   */
+    void*       y;                 /* out [M, N] at ldy, y_dtype, or NULL        */
+    float*      residual;          /* [M, N] f32 at residual_row_stride, or NULL:
+                                      residual += y                              */
+    int64_t M, N, K, ldw, ldy, residual_row_stride;
+    int32_t w_dtype, bias_dtype, y_dtype;
+} m2_skinny_gemm_norm_args;
+int m2_skinny_gemm_norm(const m2_skinny_gemm_norm_args* a, void* stream);
 
 /* thread-local message for the last non-zero return code of this thread */
 const char* m2_last_error(void);

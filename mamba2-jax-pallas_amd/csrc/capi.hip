@@ -46,6 +46,7 @@ M2_ENTRY(m2_causal_conv1d, m2_causal_conv1d_args, launch_causal_conv1d)
 M2_ENTRY(m2_causal_conv1d_update, m2_causal_conv1d_update_args, launch_causal_conv1d_update)
 M2_ENTRY(m2_rms_norm_gated, m2_rms_norm_gated_args, launch_rms_norm_gated)
 M2_ENTRY(m2_skinny_gemm, m2_skinny_gemm_args, launch_skinny_gemm)
+M2_ENTRY(m2_skinny_gemm_norm, m2_skinny_gemm_norm_args, launch_skinny_gemm_norm)
 
 // ---------------------------------------------------------------------------
 // combined forward

@@ -21,6 +21,7 @@ int launch_causal_conv1d(const m2_causal_conv1d_args& a, hipStream_t stream);
 int launch_causal_conv1d_update(const m2_causal_conv1d_update_args& a, hipStream_t stream);
 int launch_rms_norm_gated(const m2_rms_norm_gated_args& a, hipStream_t stream);
 int launch_skinny_gemm(const m2_skinny_gemm_args& a, hipStream_t stream);
+int launch_skinny_gemm_norm(const m2_skinny_gemm_norm_args& a, hipStream_t stream);
 
 // chunk_state_varlen for bf16, head dim 64, dstate % 64 == 0, chunk_size % 32
 // == 0 (<= 256): one workgroup per (sequence, head, 64-column dstate block)

@@ -10,7 +10,16 @@
 // ~2048 over the chip) split K and meet in LDS, so every weight byte is read
 // once; x (a few KB) comes from the cache.
 // MT = ceil(M / 16) row tiles share each weight fragment.
-#include "m2_internal.h"
+//
+// k_skinny_gemm_norm is the same product for a decode step's first rows
+// (M <= 4) whose x is the output of an RMSNorm (optionally SiLU-gated, over
+// groups): every workgroup normalises the rows itself into LDS (bf16; a few
+// KB read from L2) while its first weight fragments load, so the norm costs no
+// launch and no HBM round trip of its output; the epilogue can add the
+// (output-dtype rounded) result into a float32 residual stream instead of, or
+// besides, storing it -- each output column belongs to one workgroup, so the
+// add needs no synchronisation.
+#include "norm_ops.h"
 
 namespace {
 
@@ -111,6 +120,142 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm(GemmArgs a) {
         }
 }
 
+constexpr int NORM_MAXM = 4;        // rows of the normalising GEMM
+constexpr int NORM_MAXG = 8;        // norm groups per row
+constexpr int NORM_MAXX = 32768;    // normalised elements (M x K) held in LDS
+
+struct NormGemmArgs {
+    m2norm::NormArgs n;     // the rows to normalise (out unused: they go to LDS)
+    const bf16* w;
+    const void* bias;
+    void* y;
+    float* res;
+    int64_t ldw, ldy, r_rs;
+    int M, N, K;
+    int bias_bf16, y_bf16;
+};
+
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) k_skinny_gemm_norm(NormGemmArgs a) {
+    extern __shared__ __align__(16) bf16 xs[];          // [M][K] normalised rows
+    __shared__ f32x4 red[NW - 1][64];
+    __shared__ float part[NW][NORM_MAXM * NORM_MAXG];    // per-wavefront sums of squares
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int n0 = blockIdx.x * 16;
+    const int col = lane & 15, kq = (lane >> 4) * 8;
+    const int nb = min(n0 + col, a.N - 1);
+    const bf16* wr = a.w + (int64_t)nb * a.ldw;
+    const int K = a.K, M = a.M;
+    const int nsteps = (K + 31) / 32;
+    const int per = (nsteps + NW - 1) / NW;
+    const int s0 = w * per, s1 = min(nsteps, s0 + per);
+    const bf16x8 zf = {};
+    bf16x8 ba[UNROLL], bb[UNROLL];
+    auto loadw = [&](bf16x8 (&bf)[UNROLL], int s) {
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int k = (s + u) * 32 + kq;
+            bf[u] = s + u < s1 && k < K ? *reinterpret_cast<const bf16x8*>(wr + k) : zf;
+        }
+    };
+    // the first weight batch is in flight while the rows are normalised
+    loadw(ba, s0);
+
+    // ---- the rows' RMSNorm (as k_rms_norm: same operand / output rounding)
+    const m2norm::NormArgs& na = a.n;
+    const int G = (int)na.ngroups, gs = (int)na.gs, n4 = gs / 4, NT = NW * 64;
+    auto rows = [&](int m, int g, const char*& xr, const char*& zr) {
+        xr = reinterpret_cast<const char*>(na.x) + ((int64_t)m * na.x_rs + (int64_t)g * gs) * (na.x_bf16 ? 2 : 4);
+        zr = na.z ? reinterpret_cast<const char*>(na.z) + ((int64_t)m * na.z_rs + (int64_t)g * gs) * (na.z_bf16 ? 2 : 4)
+                  : nullptr;
+    };
+    for (int m = 0; m < M; ++m)
+        for (int g = 0; g < G; ++g) {
+            const char *xr, *zr;
+            rows(m, g, xr, zr);
+            float ss = 0.f;
+            for (int c = threadIdx.x; c < n4; c += NT) {
+                float v[4], sz[4];
+                m2norm::operand<4>(na, xr, zr, nullptr, 4 * c, v, sz);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) ss += na.r_x ? m2norm::rbf(v[k] * v[k]) : v[k] * v[k];
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            if (lane == 0) part[w][m * G + g] = ss;
+        }
+    __syncthreads();
+    for (int m = 0; m < M; ++m)
+        for (int g = 0; g < G; ++g) {
+            float tot = 0.f;
+#pragma unroll
+            for (int j = 0; j < NW; ++j) tot += part[j][m * G + g];
+            float ms = tot / (float)gs;
+            if (na.r_x) ms = m2norm::rbf(ms);
+            float den = ms + na.eps;
+            if (na.r_x) den = m2norm::rbf(den);
+            float rms = sqrtf(den);
+            if (na.r_x) rms = m2norm::rbf(rms);
+            const float inv = 1.f / rms;
+            const char *xr, *zr;
+            rows(m, g, xr, zr);
+            for (int c = threadIdx.x; c < n4; c += NT) {
+                float v[4], sz[4], wt[4];
+                m2norm::ldc<4>(na.w, (int64_t)g * gs + 4 * c, na.w_bf16, na.vec, wt);
+                m2norm::operand<4>(na, xr, zr, nullptr, 4 * c, v, sz);
+                m2norm::output<4>(na, xs + m * K + g * gs, 4 * c, inv, v, sz, wt);
+            }
+        }
+    __syncthreads();
+
+    // ---- y = x' W^T: A fragments from LDS (rows >= M are zero)
+    f32x4 acc = zero4();
+    auto mma = [&](const bf16x8 (&bf)[UNROLL], int s) {
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int k = (s + u) * 32 + kq;
+            const bf16x8 af = s + u < s1 && k < K && col < M
+                                  ? *reinterpret_cast<const bf16x8*>(xs + col * K + k) : zf;
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[u], acc, 0, 0, 0);
+        }
+    };
+    for (int s = s0; s < s1; s += 2 * UNROLL) {
+        if (s + UNROLL < s1) loadw(bb, s + UNROLL);
+        mma(ba, s);
+        if (s + UNROLL >= s1) break;
+        if (s + 2 * UNROLL < s1) loadw(ba, s + 2 * UNROLL);
+        mma(bb, s + UNROLL);
+    }
+    if (w > 0) red[w - 1][lane] = acc;
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int j = 0; j < NW - 1; ++j) {
+        const f32x4 o = red[j][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += o[i];
+    }
+    const int n = n0 + col;
+    if (n >= a.N) return;
+    float bv = 0.f;
+    if (a.bias)
+        bv = a.bias_bf16 ? (float)reinterpret_cast<const bf16*>(a.bias)[n]
+                         : reinterpret_cast<const float*>(a.bias)[n];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * (lane >> 4) + i;
+        if (m < M) {
+            float v = acc[i] + bv;
+            if (a.y_bf16) v = (float)(bf16)v;        // the output dtype, also for the residual add
+            if (a.y) {
+                if (a.y_bf16) reinterpret_cast<bf16*>(a.y)[(int64_t)m * a.ldy + n] = (bf16)v;
+                else reinterpret_cast<float*>(a.y)[(int64_t)m * a.ldy + n] = v;
+            }
+            if (a.res) a.res[(int64_t)m * a.r_rs + n] += v;
+        }
+    }
+}
+
 template <int MT>
 void launch_mt(const GemmArgs& k, int64_t ngroups, hipStream_t s) {
     // enough wavefronts to keep the weight stream in flight: >= ~2048 over the
@@ -166,6 +311,59 @@ int launch_skinny_gemm(const m2_skinny_gemm_args& a, hipStream_t s) {
     if (a.M <= 16) launch_mt<1>(k, ng, s);
     else if (a.M <= 32) launch_mt<2>(k, ng, s);
     else launch_mt<4>(k, ng, s);
+    return check_launch(who);
+}
+
+int launch_skinny_gemm_norm(const m2_skinny_gemm_norm_args& a, hipStream_t s) {
+    const char* who = "skinny_gemm_norm";
+    M2_REQUIRE(a.x && a.norm_weight && a.w && (a.y || a.residual), M2_ERR_INVALID,
+               "%s: x, norm_weight, w and y or residual are required", who);
+    M2_REQUIRE(a.M >= 1 && a.M <= NORM_MAXM && a.N >= 1 && a.K >= 8 && a.M * a.K <= NORM_MAXX,
+               M2_ERR_UNSUPPORTED, "%s: need 1 <= M <= %d, M * K <= %d (got %lld, %lld)", who,
+               NORM_MAXM, NORM_MAXX, (long long)a.M, (long long)a.K);
+    M2_REQUIRE(a.group_size > 0 && a.K % a.group_size == 0 && a.K / a.group_size <= NORM_MAXG,
+               M2_ERR_UNSUPPORTED, "%s: K / group_size must be a whole number <= %d", who, NORM_MAXG);
+    M2_REQUIRE(a.K % 8 == 0 && a.ldw % 8 == 0 && a.ldw >= a.K && aligned16(a.w) && a.w_dtype == M2_BF16,
+               M2_ERR_UNSUPPORTED, "%s: w must be bf16 [N, K] with 16-byte aligned rows", who);
+    M2_REQUIRE(!a.y || ((a.y_dtype == M2_BF16 || a.y_dtype == M2_F32) && a.ldy >= a.N),
+               M2_ERR_UNSUPPORTED, "%s: y dtype %d", who, a.y_dtype);
+    M2_REQUIRE(!a.bias || a.bias_dtype == M2_BF16 || a.bias_dtype == M2_F32, M2_ERR_UNSUPPORTED,
+               "%s: bias dtype %d", who, a.bias_dtype);
+    M2_REQUIRE(!a.residual || a.residual_row_stride >= a.N, M2_ERR_INVALID,
+               "%s: residual row stride", who);
+    M2_REQUIRE(a.N < (1ll << 31), M2_ERR_UNSUPPORTED, "%s: too large", who);
+    // the norm as m2_rms_norm_gated sees it, storing bf16 (the LDS rows)
+    m2_rms_norm_gated_args na{};
+    na.x = a.x; na.z = a.z; na.weight = a.norm_weight;
+    na.out = reinterpret_cast<void*>(16);         // not written: a 16-byte aligned stand-in
+    na.x_row_stride = a.x_row_stride; na.z_row_stride = a.z_row_stride; na.out_row_stride = a.K;
+    na.rows = a.M; na.hidden = a.K; na.group_size = a.group_size; na.eps = a.eps;
+    na.x_dtype = a.x_dtype; na.z_dtype = a.z_dtype; na.w_dtype = a.norm_weight_dtype;
+    na.out_dtype = M2_BF16; na.norm_before_gate = a.norm_before_gate;
+    NormGemmArgs k{};
+    bool c4;
+    if (int rc = prepare_norm(na, k.n, c4)) return rc;
+    M2_REQUIRE(c4 && k.n.vec, M2_ERR_UNSUPPORTED,
+               "%s: the rows need 4-element aligned groups, strides and bases", who);
+    k.n.out = nullptr;
+    k.w = reinterpret_cast<const bf16*>(a.w); k.bias = a.bias; k.y = a.y; k.res = a.residual;
+    k.ldw = a.ldw; k.ldy = a.ldy; k.r_rs = a.residual_row_stride;
+    k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
+    // y_dtype is the rounding of the result also when only the residual is written
+    M2_REQUIRE(a.y_dtype == M2_BF16 || a.y_dtype == M2_F32, M2_ERR_UNSUPPORTED, "%s: y dtype %d",
+               who, a.y_dtype);
+    k.bias_bf16 = a.bias_dtype == M2_BF16; k.y_bf16 = a.y_dtype == M2_BF16;
+    const int64_t ng = (a.N + 15) / 16;
+    const int nsteps = (int)((a.K + 31) / 32);
+    const size_t shm = (size_t)a.M * a.K * 2;
+    const dim3 grid((unsigned)ng);
+    // as the plain product: enough wavefronts to keep the weight stream in flight
+    if (ng * 4 >= 2048 || nsteps < 8 * 2 * UNROLL)
+        hipLaunchKernelGGL((k_skinny_gemm_norm<4>), grid, dim3(4 * 64), shm, s, k);
+    else if (ng * 8 >= 2048 || nsteps < 16 * 2 * UNROLL)
+        hipLaunchKernelGGL((k_skinny_gemm_norm<8>), grid, dim3(8 * 64), shm, s, k);
+    else
+        hipLaunchKernelGGL((k_skinny_gemm_norm<16>), grid, dim3(16 * 64), shm, s, k);
     return check_launch(who);
 }
 

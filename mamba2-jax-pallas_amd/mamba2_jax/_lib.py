@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm2ssd.so
 
 M2_F32 = 0
 M2_BF16 = 1
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -129,6 +129,16 @@ class SkinnyGemmArgs(ctypes.Structure):
                 ("w_dtype", _i32), ("bias_dtype", _i32), ("y_dtype", _i32)]
 
 
+class SkinnyGemmNormArgs(ctypes.Structure):
+    _fields_ = [("x", _c_p), ("z", _c_p), ("norm_weight", _c_p), ("x_row_stride", _i64),
+                ("z_row_stride", _i64), ("group_size", _i64), ("eps", ctypes.c_float),
+                ("x_dtype", _i32), ("z_dtype", _i32), ("norm_weight_dtype", _i32),
+                ("norm_before_gate", _i32), ("w", _c_p), ("bias", _c_p), ("y", _c_p),
+                ("residual", _c_p), ("M", _i64), ("N", _i64), ("K", _i64), ("ldw", _i64),
+                ("ldy", _i64), ("residual_row_stride", _i64), ("w_dtype", _i32),
+                ("bias_dtype", _i32), ("y_dtype", _i32)]
+
+
 # entry point name -> argument struct (every function declared in m2ssd.h)
 ENTRY_POINTS = {
     "m2_chunk_cumsum": ChunkCumsumArgs,
@@ -143,6 +153,7 @@ ENTRY_POINTS = {
     "m2_causal_conv1d_update": CausalConv1dUpdateArgs,
     "m2_rms_norm_gated": RmsNormGatedArgs,
     "m2_skinny_gemm": SkinnyGemmArgs,
+    "m2_skinny_gemm_norm": SkinnyGemmNormArgs,
 }
 OTHER_SYMBOLS = ("m2_ssd_combined_workspace_size", "m2_last_error", "m2_abi_version")
 

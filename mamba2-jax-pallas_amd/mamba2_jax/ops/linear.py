@@ -56,4 +56,73 @@ def linear_skinny(x, w, bias=None, out_dtype=torch.bfloat16):
     return y
 
 
-__all__ = ["linear_skinny", "supported"]
+NORM_MAX_ROWS = 4
+NORM_MAX_ELEMS = 32768      # M * K normalised elements held in LDS
+NORM_MAX_GROUPS = 8
+
+
+def _rows4(t):
+    """t (M, K) as rows with unit last stride, 4-element row stride and a
+    16-byte aligned base (views such as a slice of the in-projection output
+    qualify), or None."""
+    if t.stride(1) != 1 or (t.shape[0] > 1 and t.stride(0) % 4) or t.data_ptr() % 16:
+        return None
+    return t
+
+
+def norm_supported(x, w, z=None, group_size=None):
+    """True when linear_norm can take these operands."""
+    if not (w.dtype == torch.bfloat16 and x.dim() == 2 and w.dim() == 2 and x.is_cuda and w.is_cuda):
+        return False
+    M, K = x.shape
+    gs = K if group_size is None else int(group_size)
+    return (1 <= M <= NORM_MAX_ROWS and M * K <= NORM_MAX_ELEMS and w.shape[1] == K and K % 8 == 0
+            and gs % 4 == 0 and K % gs == 0 and K // gs <= NORM_MAX_GROUPS
+            and x.dtype in (torch.float32, torch.bfloat16) and _rows4(x) is not None
+            and (z is None or (tuple(z.shape) == (M, K) and z.dtype in (torch.float32, torch.bfloat16)
+                               and _rows4(z) is not None)))
+
+
+def linear_norm(x, norm_weight, w, z=None, group_size=None, eps=1e-5, norm_before_gate=True,
+                bias=None, out_dtype=torch.bfloat16, residual=None, store=True):
+    """y = rms_norm_gated(x, norm_weight, z, eps, group_size, norm_before_gate)
+    @ w.T (+ bias) in one kernel (m2_skinny_gemm_norm): x (M <= 4, K), w (N, K)
+    bf16.  The normalised rows are bf16, as rms_norm_gated(..., out_dtype=
+    torch.bfloat16) gives them.  residual (M, N) float32: the result (rounded
+    to out_dtype) is added into it in place; with store=False y is not
+    written and None is returned."""
+    dev = L.device_of(x, norm_weight, w, z, bias, residual)
+    L.require(norm_supported(x, w, z, group_size),
+              f"linear_norm: x {tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}: need M <= "
+              f"{NORM_MAX_ROWS}, M * K <= {NORM_MAX_ELEMS}, bf16 w, 4-element aligned rows")
+    M, K = x.shape
+    N = w.shape[0]
+    gs = K if group_size is None else int(group_size)
+    nw = L.dev_contig(norm_weight if norm_weight.dtype in (torch.float32, torch.bfloat16)
+                      else norm_weight.float())
+    w = L.dev_contig(w)
+    b = None if bias is None else L.dev_contig(bias if bias.dtype in (torch.float32, torch.bfloat16)
+                                               else bias.float())
+    if residual is not None:
+        L.require(residual.dtype == torch.float32 and tuple(residual.shape) == (M, N)
+                  and residual.stride(1) == 1, "residual must be float32 (M, N) with unit last stride")
+    L.require(store or residual is not None, "linear_norm: nothing to write")
+    L.require(out_dtype in (torch.float32, torch.bfloat16), f"out_dtype {out_dtype}")
+    y = torch.empty((M, N), dtype=out_dtype, device=dev) if store else None
+    args = L.SkinnyGemmNormArgs(
+        x=L.ptr(x), z=L.ptr(z), norm_weight=L.ptr(nw),
+        x_row_stride=x.stride(0) if M > 1 else K,
+        z_row_stride=(z.stride(0) if M > 1 else K) if z is not None else 0, group_size=gs,
+        eps=float(eps), x_dtype=L.dtype_code(x, "x"),
+        z_dtype=L.M2_F32 if z is None else L.dtype_code(z, "z"),
+        norm_weight_dtype=L.dtype_code(nw, "norm_weight"), norm_before_gate=int(bool(norm_before_gate)),
+        w=L.ptr(w), bias=L.ptr(b), y=L.ptr(y), residual=L.ptr(residual), M=M, N=N, K=K, ldw=K,
+        ldy=N, residual_row_stride=0 if residual is None else (residual.stride(0) if M > 1 else N),
+        w_dtype=L.M2_BF16, bias_dtype=L.M2_F32 if b is None else L.dtype_code(b, "bias"),
+        y_dtype=L.M2_BF16 if out_dtype == torch.bfloat16 else L.M2_F32)
+    with torch.cuda.device(dev):
+        L.call("m2_skinny_gemm_norm", args, L.stream_of(dev))
+    return y
+
+
+__all__ = ["linear_norm", "linear_skinny", "norm_supported", "supported"]

@@ -33,6 +33,7 @@ STRUCT_NAMES = {
     "CausalConv1dUpdateArgs": "m2_causal_conv1d_update_args",
     "RmsNormGatedArgs": "m2_rms_norm_gated_args",
     "SkinnyGemmArgs": "m2_skinny_gemm_args",
+    "SkinnyGemmNormArgs": "m2_skinny_gemm_norm_args",
 }
 
 

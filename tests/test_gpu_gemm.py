@@ -51,3 +51,75 @@ def test_strided_x_and_errors():
                          ldw=512, ldy=96, x_dtype=L.M2_F32, w_dtype=L.M2_BF16, y_dtype=L.M2_F32)
     with pytest.raises(L.M2Error):
         L.call("m2_skinny_gemm", a, 0)
+
+
+# ---------------------------------------------------------------------------
+# m2_skinny_gemm_norm: the rows normalised in the GEMM's prologue
+# ---------------------------------------------------------------------------
+
+from mamba2_jax.ops.linear import linear_norm  # noqa: E402
+from mamba2_jax.ops.rms_norm import rms_norm_gated  # noqa: E402
+
+NORM_CASES = [
+    # M, K, N, x dtype, gated (z slice), group_size, norm_before_gate, bias
+    (1, 2560, 10576, "f32", False, None, True, False),     # 2.7b pre-norm + in-projection
+    (4, 768, 3352, "f32", False, None, True, True),
+    (1, 5120, 2560, "f32", True, None, False, False),      # 2.7b gated norm + out-projection
+    (3, 8192, 4096, "f32", True, 1024, False, False),      # nemotron-h-8b: 8 groups
+    (2, 1536, 768, "bf16", True, 768, True, True),
+    (4, 64, 40, "bf16", False, 16, True, False),
+]
+
+
+@pytest.mark.parametrize("case", NORM_CASES, ids=[f"{c[0]}x{c[1]}x{c[2]}-{c[3]}-z{int(c[4])}-g{c[5]}"
+                                                   f"-nbg{int(c[6])}-b{int(c[7])}" for c in NORM_CASES])
+def test_skinny_gemm_norm(case):
+    """against the two-kernel composition it replaces (rms_norm_gated storing
+    bf16, then the skinny GEMM): the normalised rows may differ by one bf16 ulp
+    where the two kernels' sums of squares round differently, so the bound is
+    2^-7 of each product's magnitude sum |x'| |w| plus 1e-5 of the RMS;
+    with a residual, residual_after == residual_before + y exactly."""
+    M, K, N, xdt, gated, gs, nbg, hasb = case
+    announce("skinny_gemm_norm", case)
+    g = torch.Generator(device="cuda").manual_seed(M + K + N)
+    T = {"f32": torch.float32, "bf16": torch.bfloat16}[xdt]
+    x = (torch.randn((M, K), generator=g, device="cuda") * 3).to(T)
+    z = None
+    if gated:
+        wide = torch.randn((M, K + 2 * K + 16), generator=g, device="cuda").to(torch.bfloat16)
+        z = wide[:, 8:8 + K]                                  # a strided slice, as in the layer
+    nw = torch.rand(K, generator=g, device="cuda").add(0.5).to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g, device="cuda") / K ** 0.5).to(torch.bfloat16)
+    b = torch.randn(N, generator=g, device="cuda").to(torch.bfloat16) if hasb else None
+    res = torch.randn((M, N), generator=g, device="cuda")
+    res0 = res.clone()
+    y = linear_norm(x, nw, w, z=z, group_size=gs, norm_before_gate=nbg, bias=b, residual=res)
+    xn = rms_norm_gated(x, nw, z=z, group_size=gs, norm_before_gate=nbg, out_dtype=torch.bfloat16)
+    ref = xn.float() @ w.float().t() + (0 if b is None else b.float())
+    mag = xn.float().abs() @ w.float().abs().t()
+    err = (y.float() - ref).abs()
+    rms = ref.pow(2).mean().sqrt().item()
+    tol = 2.0 ** -7 * mag + 2.0 ** -8 * ref.abs() + 1e-5 * rms
+    print(f"  max err {err.max().item():.3e}, rms {rms:.3e}", flush=True)
+    assert bool((err <= tol).all()), f"{int((err > tol).sum())} values beyond tolerance"
+    assert torch.equal(res, res0 + y.float()), "residual += y"
+    # residual only (no y): the same sums
+    res2 = res0.clone()
+    assert linear_norm(x, nw, w, z=z, group_size=gs, norm_before_gate=nbg, bias=b, residual=res2,
+                       store=False) is None
+    assert torch.equal(res2, res)
+
+
+def test_skinny_gemm_norm_limits():
+    w = torch.zeros((16, 64), device="cuda", dtype=torch.bfloat16)
+    nw = torch.ones(64, device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):                    # 5 rows
+        linear_norm(torch.zeros((5, 64), device="cuda"), nw, w)
+    with pytest.raises(AssertionError):                    # 16 groups
+        linear_norm(torch.zeros((1, 64), device="cuda"), nw, w, group_size=4)
+    a = L.SkinnyGemmNormArgs(x=w.data_ptr(), norm_weight=nw.data_ptr(), w=w.data_ptr(), y=0,
+                             residual=0, M=1, N=16, K=64, ldw=64, ldy=16, group_size=64,
+                             x_dtype=L.M2_BF16, norm_weight_dtype=L.M2_BF16, w_dtype=L.M2_BF16,
+                             y_dtype=L.M2_BF16)
+    with pytest.raises(L.M2Error):                          # neither y nor residual
+        L.call("m2_skinny_gemm_norm", a, 0)
