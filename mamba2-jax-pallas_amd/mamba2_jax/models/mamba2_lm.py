@@ -30,7 +30,8 @@ from dataclasses import dataclass
 
 import torch
 
-from ..modules.mamba2 import MixerDims, _lecun_normal, mamba2_block_forward, mamba2_block_step
+from ..modules.mamba2 import (MixerDims, _lecun_normal, block_step_fusable, mamba2_block_forward,
+                              mamba2_block_step, mamba2_block_step_fused)
 from ..ops import linear
 from ..ops.rms_norm import rms_norm_gated
 
@@ -271,6 +272,9 @@ class Mamba2LMHeadModel:
     def __init__(self, config: Mamba2Config):
         self.config = config
         self._prep = None
+        # decode steps of <= 4 rows run the norms inside the projections
+        # (mamba2_block_step_fused) when the parameters allow it
+        self.fuse_decode = True
 
     def _prepared(self, params):
         """Per-layer mixer dicts (cached per parameter dict) with A =
@@ -345,11 +349,30 @@ class Mamba2LMHeadModel:
         return self._head(params, *self._layers(params, x, state))[:, -1, :]
 
     # -- decode ----------------------------------------------------------------
+    def _fusable(self, params, batch):
+        cfg = self.config
+        w = params["lm_head_weight"]
+        return (self.fuse_decode and cfg.residual_in_fp32 and w.dtype == torch.bfloat16
+                and w.dim() == 2 and w.shape[1] % 8 == 0 and w.is_cuda
+                and all(block_step_fusable(mx, cfg.mixer_dims(), batch, cfg.d_model)
+                        for mx in self._prepared(params)))
+
     def decode_step(self, params, token, state: DecodeState):
         """token (batch,) -> next-token logits (batch, vocab); states in place
-        (reference _scan_decode_step, :667-736)."""
+        (reference _scan_decode_step, :667-736).  Up to 4 rows with bf16
+        projections: each layer's norms run inside its projections
+        (mamba2_block_step_fused; 4 kernels per layer), the final norm inside
+        the LM head."""
         d = self.config.mixer_dims()
         x = params["embedding"]["weight"][token]
+        if self._fusable(params, x.shape[0]):
+            res = x.float().contiguous()
+            if res.data_ptr() == x.data_ptr():
+                res = res.clone()
+            for i, (lp, mx) in enumerate(zip(params["layers"], self._prepared(params))):
+                mamba2_block_step_fused(res, lp["norm_weight"], mx, d, state.conv[i], state.ssm[i])
+            w = params["lm_head_weight"]
+            return linear.linear_norm(res, params["norm_f_weight"], w, out_dtype=w.dtype)
 
         def block(i, xn, mx):
             return mamba2_block_step(xn, mx, d, state.conv[i], state.ssm[i])[0]

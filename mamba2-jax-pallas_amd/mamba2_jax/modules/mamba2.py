@@ -280,6 +280,45 @@ def mamba2_block_step(u_t, p, d, conv_state, ssm_state):
     return out, conv_state, ssm_state
 
 
+def block_step_fusable(p, d, batch, d_model):
+    """True when mamba2_block_step_fused can run this mixer at this batch: bf16
+    projections with their [out, in] copies, the gated norm (no MLP bypass),
+    and rows the normalising GEMM takes (<= 4 rows, 4-element aligned)."""
+    return (d.rmsnorm and d.d_mlp == 0 and p.get("in_proj_t") is not None
+            and p.get("out_proj_t") is not None and batch <= _lin.NORM_MAX_ROWS
+            and batch * max(d_model, d.d_ssm) <= _lin.NORM_MAX_ELEMS and d_model % 8 == 0
+            and d.d_ssm % 8 == 0 and (d.d_ssm // d.ngroups) % 4 == 0
+            and d.ngroups <= _lin.NORM_MAX_GROUPS and (2 * d.d_ssm + 2 * d.ngroups * d.d_state
+                                                        + d.nheads) % 4 == 0)
+
+
+def mamba2_block_step_fused(res, norm_weight, p, d, conv_state, ssm_state, eps=1e-5):
+    """One decode token of a pre-norm residual block, res += mixer(rmsnorm(res))
+    (reference models/mamba2_lm.py:205-211 around modules/mamba2.py:427-549),
+    in four kernels: the block's RMSNorm runs in the in-projection's prologue,
+    the gated norm in the out-projection's, whose epilogue adds the output
+    (rounded to bf16, the projection's dtype) into res.  res (batch, d_model)
+    float32 and the states are updated in place; block_step_fusable must hold.
+    The results equal mamba2_block_step's around rms_norm up to the rounding
+    of the norms' sums of squares (summed in another order)."""
+    G, N, H, Pd = d.ngroups, d.d_state, d.nheads, d.headdim
+    batch = res.shape[0]
+    zxbcdt = _lin.linear_norm(res, norm_weight, p["in_proj_t"], eps=eps, bias=p.get("in_proj_bias"),
+                              out_dtype=p["in_proj_t"].dtype)
+    _, _, z, xBC, dt = _split_last(zxbcdt, [0, 0, d.d_ssm, d.conv_dim, d.nheads])
+    conv_state, (x, B, C) = causal_conv1d_update(
+        xBC, conv_state, p["conv1d_weight"], p.get("conv1d_bias"), "silu",
+        split_sizes=(d.d_ssm, G * N, G * N))
+    ssm_state, y = selective_state_update(
+        ssm_state, x.view(batch, H, Pd), dt, _A(p), B.view(batch, G, N), C.view(batch, G, N),
+        D=_D(p, d), dt_bias=p["dt_bias"], dt_softplus=True)
+    _lin.linear_norm(y.view(batch, d.d_ssm), p["norm_weight"], p["out_proj_t"], z=z,
+                     group_size=d.d_ssm // G, norm_before_gate=d.norm_before_gate,
+                     bias=p.get("out_proj_bias"), out_dtype=p["out_proj_t"].dtype, residual=res,
+                     store=False)
+    return res, conv_state, ssm_state
+
+
 def allocate_inference_cache(batch_size: int, d_model: int, d_state: int = 128, d_conv: int = 4,
                              expand: int = 2, headdim: int = 64, d_ssm: Optional[int] = None,
                              ngroups: int = 1, dtype=torch.float32, device=None):
@@ -295,4 +334,5 @@ def allocate_inference_cache(batch_size: int, d_model: int, d_state: int = 128, 
 
 
 __all__ = ["_ssd_combined_fwd", "selective_state_update", "Mamba2", "MixerDims",
-           "mamba2_block_forward", "mamba2_block_step", "allocate_inference_cache"]
+           "mamba2_block_forward", "mamba2_block_step", "mamba2_block_step_fused",
+           "block_step_fusable", "allocate_inference_cache"]

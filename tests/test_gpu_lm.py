@@ -119,3 +119,27 @@ def test_generate_graph_equals_eager():
     c = m.generate(params, ids, max_new_tokens=8, temperature=1.0, top_k=20, rng_key=3)
     d = m.generate(params, ids, max_new_tokens=8, temperature=1.0, top_k=20, rng_key=3, use_graph=False)
     assert torch.equal(c, d)
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_fused_decode_matches_unfused(batch):
+    """The decode step with the norms inside the projections
+    (mamba2_block_step_fused, batch <= 4) against the separate norm kernels:
+    the two differ only where a norm's sum of squares rounds differently
+    (another summation order), so logits and states stay within the bf16
+    bar over ten steps."""
+    announce("LM fused decode vs unfused", batch)
+    params = init_params(CFG, dtype=torch.bfloat16, seed=9)
+    fused, plain = Mamba2LMHeadModel(CFG), Mamba2LMHeadModel(CFG)
+    plain.fuse_decode = False
+    assert fused._fusable(params, batch) and not plain._fusable(params, batch)
+    ids = _ids(np.random.default_rng(10), batch, 40)
+    st_f, st_p = DecodeState(CFG, batch), DecodeState(CFG, batch)
+    fused.prefill(params, ids[:, :30], st_f)
+    plain.prefill(params, ids[:, :30], st_p)
+    for t in range(30, 40):
+        lf = fused.decode_step(params, ids[:, t], st_f)
+        lp = plain.decode_step(params, ids[:, t], st_p)
+        check(lf, host(lp), TOL["bf16"], f"logits, token {t}")
+    check(st_f.ssm, host(st_p.ssm), TOL["bf16"], "ssm states")
+    check(st_f.conv, host(st_p.conv), TOL["bf16"], "conv states")
