@@ -110,6 +110,29 @@ M2_DEV f32x3frag load_frag(const float* p) {
     return f;
 }
 
+// Two floats rounded to bf16 (RNE) and packed, a in the low half
+// (v_cvt_pk_bf16_f32).
+M2_DEV uint32_t pk_bf16(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+}
+// a ~= hi + lo, b likewise, each part bf16 (packed pairs); the hi values are
+// unpacked with bit operations (a bf16 is the high half of its float)
+M2_DEV void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
+    hi = pk_bf16(a, b);
+    lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
+}
+M2_DEV bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u4;
+    const u4 v = {a, b, c, d};
+    return __builtin_bit_cast(bf16x8, v);
+}
+// the two bf16 of a packed pair as floats
+M2_DEV float bf16_lo(uint32_t d) { return __uint_as_float(d << 16); }
+M2_DEV float bf16_hi(uint32_t d) { return __uint_as_float(d & 0xffff0000u); }
+
 M2_DEV f32x4 zero4() { f32x4 z = {0.f, 0.f, 0.f, 0.f}; return z; }
 
 // Index of the calling wavefront in its workgroup, as a scalar: branches and

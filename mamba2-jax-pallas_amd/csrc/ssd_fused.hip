@@ -73,25 +73,6 @@ M2_DEV f32x4 mma32(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 M2_DEV float rbf(float v) { return (float)(bf16)v; }
 
-// Two floats rounded to bf16 (RNE) and packed, a in the low half
-// (v_cvt_pk_bf16_f32).
-M2_DEV uint32_t pk_bf16(float a, float b) {
-    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-    typedef float f2 __attribute__((ext_vector_type(2)));
-    const f2 v = {a, b};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
-}
-// a ~= hi + lo, b likewise, each part bf16 (packed pairs); the hi values are
-// unpacked with bit operations (a bf16 is the high half of its float)
-M2_DEV void split2(float a, float b, uint32_t& hi, uint32_t& lo) {
-    hi = pk_bf16(a, b);
-    lo = pk_bf16(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u));
-}
-M2_DEV bf16x8 as_bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    const u32x4 v = {a, b, c, d};
-    return __builtin_bit_cast(bf16x8, v);
-}
-
 // 16-byte chunk swizzles.  x rows are 128 bytes and read as chunk pairs by
 // 16-lane groups (4 rows each) or as single 8-byte halves: an even mask keeps
 // pairs together.  State / B rows (CPR chunks) are read 16 bytes per lane by

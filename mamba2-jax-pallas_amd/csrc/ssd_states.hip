@@ -275,14 +275,15 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
             const float w0 = wl[ks];
             const float wv[8] = {row_bcast<0>(w0), row_bcast<1>(w0), row_bcast<2>(w0), row_bcast<3>(w0),
                                  row_bcast<4>(w0), row_bcast<5>(w0), row_bcast<6>(w0), row_bcast<7>(w0)};
-            bf16x8 xh, xl;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float v = (float)(j < 4 ? xa[ks][j] : xb[ks][j - 4]) * wv[j];
-                const bf16 hi = (bf16)v;
-                xh[j] = hi;
-                xl[j] = (bf16)(v - (float)hi);
-            }
+            // w x of the lane's 8 k indices as packed bf16 hi / lo pairs
+            typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+            const u2 pa = __builtin_bit_cast(u2, xa[ks]), pb = __builtin_bit_cast(u2, xb[ks]);
+            uint32_t h[4], l[4];
+            split2(bf16_lo(pa[0]) * wv[0], bf16_hi(pa[0]) * wv[1], h[0], l[0]);
+            split2(bf16_lo(pa[1]) * wv[2], bf16_hi(pa[1]) * wv[3], h[1], l[1]);
+            split2(bf16_lo(pb[0]) * wv[4], bf16_hi(pb[0]) * wv[5], h[2], l[2]);
+            split2(bf16_lo(pb[1]) * wv[6], bf16_hi(pb[1]) * wv[7], h[3], l[3]);
+            const bf16x8 xh = as_bf16x8(h[0], h[1], h[2], h[3]), xl = as_bf16x8(l[0], l[1], l[2], l[3]);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const bf16x8 bf = __builtin_shufflevector(ba[ks][j], bb[ks][j], 0, 1, 2, 3, 4, 5, 6, 7);
