@@ -63,6 +63,7 @@ STATE_CFGS = [
     (1, 256, 256, 64, 256, 8, 256),
     (2, 200, 8, 32, 128, 2, 64),     # L % Q != 0, headdim 32
     (2, 200, 8, 64, 128, 2, 64),     # L % Q != 0, batch 2, one-shot bf16 kernel
+    (1, 100, 8, 64, 128, 2, 32),     # chunk 32, L % Q != 0
     (1, 4096, 128, 64, 128, 8, 128), # nemotron-h-8b layer shape
 ]
 
