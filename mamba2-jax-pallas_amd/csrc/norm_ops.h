@@ -142,6 +142,7 @@ namespace m2 {
 // The norm's arguments for these sizes and dtypes (rounding flags as the
 // reference's dtype promotion gives them; k.vec set when every access can be
 // 4 elements wide); c4: the sizes allow 4-element chunks.  Checks the
-// arguments as m2_rms_norm_gated does.
-int prepare_norm(const m2_rms_norm_gated_args& a, m2norm::NormArgs& k, bool& c4);
+// arguments as m2_rms_norm_gated does; to_lds: the caller writes the rows to
+// its own LDS (a.out is not used and may be NULL).
+int prepare_norm(const m2_rms_norm_gated_args& a, m2norm::NormArgs& k, bool& c4, bool to_lds);
 }  // namespace m2

@@ -110,9 +110,10 @@ using m2norm::NormArgs;
 static bool aligned_to(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 
-int prepare_norm(const m2_rms_norm_gated_args& a, NormArgs& k, bool& c4) {
+int prepare_norm(const m2_rms_norm_gated_args& a, NormArgs& k, bool& c4, bool to_lds) {
     const char* who = "rms_norm_gated";
-    M2_REQUIRE(a.x && a.weight && a.out, M2_ERR_INVALID, "%s: x, weight and out are required", who);
+    M2_REQUIRE(a.x && a.weight && (a.out || to_lds), M2_ERR_INVALID,
+               "%s: x, weight and out are required", who);
     M2_REQUIRE(a.rows > 0 && a.hidden > 0 && a.group_size > 0 && a.hidden % a.group_size == 0,
                M2_ERR_INVALID, "%s: bad sizes (hidden %% group_size must be 0)", who);
     for (int d : {a.x_dtype, a.w_dtype, a.out_dtype})
@@ -142,7 +143,8 @@ int prepare_norm(const m2_rms_norm_gated_args& a, NormArgs& k, bool& c4) {
     const int xs = a.x_dtype == M2_BF16 ? 2 : 4, os = k.o_bf16 ? 2 : 4, ws = a.w_dtype == M2_BF16 ? 2 : 4;
     c4 = a.group_size % 4 == 0 && a.x_row_stride % 4 == 0 && a.out_row_stride % 4 == 0 &&
          (!a.z || a.z_row_stride % 4 == 0) && (!a.residual || a.residual_row_stride % 4 == 0);
-    bool vec = c4 && aligned_to(a.x, 4 * xs) && aligned_to(a.out, 4 * os) && aligned_to(a.weight, 4 * ws) &&
+    bool vec = c4 && aligned_to(a.x, 4 * xs) && (to_lds || aligned_to(a.out, 4 * os)) &&
+               aligned_to(a.weight, 4 * ws) &&
                (!a.residual || aligned_to(a.residual, 16));
     if (a.z) vec = vec && aligned_to(a.z, 4 * (zb ? 2 : 4));
     k.vec = vec;
@@ -153,7 +155,7 @@ int launch_rms_norm_gated(const m2_rms_norm_gated_args& a, hipStream_t s) {
     const char* who = "rms_norm_gated";
     NormArgs k;
     bool c4;
-    if (int rc = prepare_norm(a, k, c4)) return rc;
+    if (int rc = prepare_norm(a, k, c4, false)) return rc;
     const int64_t nblocks = a.rows * (a.hidden / a.group_size);
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "%s: too many rows", who);
     const dim3 grid((unsigned)nblocks);

@@ -335,14 +335,13 @@ int launch_skinny_gemm_norm(const m2_skinny_gemm_norm_args& a, hipStream_t s) {
     // the norm as m2_rms_norm_gated sees it, storing bf16 (the LDS rows)
     m2_rms_norm_gated_args na{};
     na.x = a.x; na.z = a.z; na.weight = a.norm_weight;
-    na.out = reinterpret_cast<void*>(16);         // not written: a 16-byte aligned stand-in
     na.x_row_stride = a.x_row_stride; na.z_row_stride = a.z_row_stride; na.out_row_stride = a.K;
     na.rows = a.M; na.hidden = a.K; na.group_size = a.group_size; na.eps = a.eps;
     na.x_dtype = a.x_dtype; na.z_dtype = a.z_dtype; na.w_dtype = a.norm_weight_dtype;
     na.out_dtype = M2_BF16; na.norm_before_gate = a.norm_before_gate;
     NormGemmArgs k{};
     bool c4;
-    if (int rc = prepare_norm(na, k.n, c4)) return rc;
+    if (int rc = prepare_norm(na, k.n, c4, true)) return rc;
     M2_REQUIRE(c4 && k.n.vec, M2_ERR_UNSUPPORTED,
                "%s: the rows need 4-element aligned groups, strides and bases", who);
     k.n.out = nullptr;
