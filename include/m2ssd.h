@@ -374,6 +374,13 @@ typedef struct {
                                       residual += y                              */
     int64_t M, N, K, ldw, ldy, residual_row_stride;
     int32_t w_dtype, bias_dtype, y_dtype;
+    /* with_conv: the decode conv update (m2_causal_conv1d_update) of output
+       columns [conv_begin, conv_begin + conv.dim), run on each column once it
+       is computed (rounded to y_dtype); conv.x is not read, conv.batch == M,
+       conv.width 4, f32 conv_state updated in place (new_state == conv_state) */
+    int32_t with_conv;
+    int64_t conv_begin;
+    m2_causal_conv1d_update_args conv;
 } m2_skinny_gemm_norm_args;
 int m2_skinny_gemm_norm(const m2_skinny_gemm_norm_args* a, void* stream);
 

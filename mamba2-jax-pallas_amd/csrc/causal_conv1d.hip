@@ -28,20 +28,17 @@
 // (causal_conv1d_update) and :142-193 (the sequence-boundary mask).
 #include <type_traits>
 
-#include "m2_internal.h"
+#include "conv_ops.h"
 
 namespace {
+
+using namespace m2conv;
 
 constexpr int THREADS = 256;
 constexpr int TT = 16;          // tokens per wavefront in k_conv_walk
 constexpr int GRP = 4;          // tokens per load group (two groups in flight)
 constexpr int MAXW = 8;         // largest conv width
 
-struct Outs {
-    void* ptr[3];
-    int64_t c_begin[3], sb[3], sd[3], st[3];
-    int n;
-};
 
 struct ConvArgs {
     const void* x;
@@ -59,20 +56,7 @@ struct ConvArgs {
     int64_t nwork, ncv, nrun;   // work decomposition
 };
 
-M2_DEV float rbf(float v) { return (float)(bf16)v; }
 
-// silu(v) = v / (1 + e^-v) from the hardware base-2 exponential and
-// reciprocal (each ~1 ulp; the e^-v argument is rounded once, a relative
-// error below |v| 2^-24): a few instructions instead of a full-precision exp
-// and division, which dominated this HBM-bound kernel's issue time.  Limits:
-// e^-v = inf gives v * 0 = 0, e^-v = 0 gives v.
-M2_DEV float silu_fast(float v) {
-    const float e = __builtin_amdgcn_exp2f(v * -1.4426950408889634f);
-    return v * __builtin_amdgcn_rcpf(1.f + e);
-}
-M2_DEV float ldf(const void* p, int64_t i, int is_bf16) {
-    return is_bf16 ? (float)reinterpret_cast<const bf16*>(p)[i] : reinterpret_cast<const float*>(p)[i];
-}
 
 // the reference's mask: keep x[s] iff seq[s] == seq[s + 1] == ... == seq[s + K - 1]
 // (positions past the end compare equal)
@@ -362,20 +346,6 @@ __global__ void __launch_bounds__(THREADS) k_conv_cf(ConvArgs a) {
 // ---------------------------------------------------------------------------
 // decode
 // ---------------------------------------------------------------------------
-struct UpdArgs {
-    const void* x;
-    int64_t xsb;
-    const void* state;
-    void* nstate;
-    const void* w;
-    const void* bias;
-    Outs o;
-    int64_t B, D;
-    int x_bf16, w_bf16, bias_bf16, out_bf16;
-    int round_prod;             // products and their sum are bf16
-    int round_bias;
-    int silu;
-};
 
 template <typename TS, typename TN, int K>
 __global__ void __launch_bounds__(THREADS) k_conv_update(UpdArgs a) {
@@ -395,23 +365,7 @@ __global__ void __launch_bounds__(THREADS) k_conv_update(UpdArgs a) {
         s[i] = to_f32(v);
         np[i] = v;
     }
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < K; ++i) {
-        const float p = s[i] * ldf(a.w, c * K + i, a.w_bf16);
-        acc += a.round_prod ? rbf(p) : p;
-    }
-    if (a.round_prod) acc = rbf(acc);
-    if (a.bias) acc += ldf(a.bias, c, a.bias_bf16);
-    if (a.round_bias) acc = rbf(acc);
-    if (a.silu) acc = silu_fast(acc);
-    int r = 0;
-#pragma unroll
-    for (int j = 1; j < 3; ++j)
-        if (j < a.o.n && c >= a.o.c_begin[j]) r = j;
-    const int64_t o = b * a.o.sb[r] + (c - a.o.c_begin[r]);
-    if (a.out_bf16) reinterpret_cast<bf16*>(a.o.ptr[r])[o] = (bf16)acc;
-    else reinterpret_cast<float*>(a.o.ptr[r])[o] = acc;
+    conv_store(a, b, c, conv_channel<K>(a, s, c));
 }
 
 // ---------------------------------------------------------------------------
@@ -569,9 +523,9 @@ int launch_causal_conv1d(const m2_causal_conv1d_args& a, hipStream_t s) {
     return check_launch(who);
 }
 
-int launch_causal_conv1d_update(const m2_causal_conv1d_update_args& a, hipStream_t s) {
+int prepare_conv_update(const m2_causal_conv1d_update_args& a, UpdArgs& k, bool x_given) {
     const char* who = "causal_conv1d_update";
-    M2_REQUIRE(a.x && a.conv_state && a.new_state && a.weight, M2_ERR_INVALID,
+    M2_REQUIRE((a.x || x_given) && a.conv_state && a.new_state && a.weight, M2_ERR_INVALID,
                "%s: x, conv_state, new_state and weight are required", who);
     M2_REQUIRE(a.batch > 0 && a.dim > 0, M2_ERR_INVALID, "%s: bad sizes", who);
     M2_REQUIRE(a.width >= 1 && a.width <= MAXW, M2_ERR_UNSUPPORTED,
@@ -589,7 +543,7 @@ int launch_causal_conv1d_update(const m2_causal_conv1d_update_args& a, hipStream
     const int rdt = pdt == M2_BF16 && (!a.bias || a.bias_dtype == M2_BF16) ? M2_BF16 : M2_F32;
     M2_REQUIRE(a.out_dtype == rdt, M2_ERR_INVALID, "%s: out_dtype must be the result dtype %d",
                who, rdt);
-    UpdArgs k{};
+    k = UpdArgs{};
     int rc = take_outs(a.out, a.nout, a.dim, k.o, who);
     if (rc) return rc;
     for (int j = 0; j < a.nout; ++j)
@@ -599,6 +553,14 @@ int launch_causal_conv1d_update(const m2_causal_conv1d_update_args& a, hipStream
     k.x_bf16 = a.x_dtype == M2_BF16; k.w_bf16 = a.w_dtype == M2_BF16;
     k.bias_bf16 = a.bias_dtype == M2_BF16; k.out_bf16 = rdt == M2_BF16;
     k.round_prod = pdt == M2_BF16; k.round_bias = a.bias && rdt == M2_BF16; k.silu = a.silu != 0;
+    return M2_OK;
+}
+
+int launch_causal_conv1d_update(const m2_causal_conv1d_update_args& a, hipStream_t s) {
+    const char* who = "causal_conv1d_update";
+    UpdArgs k;
+    if (int rc = prepare_conv_update(a, k, false)) return rc;
+    const int nsdt = a.state_dtype == M2_BF16 && a.x_dtype == M2_BF16 ? M2_BF16 : M2_F32;
     const int64_t n = a.batch * a.dim;
     M2_REQUIRE((n + THREADS - 1) / THREADS < (1ll << 31), M2_ERR_UNSUPPORTED, "%s: too many workgroups", who);
     const dim3 grid((unsigned)((n + THREADS - 1) / THREADS));

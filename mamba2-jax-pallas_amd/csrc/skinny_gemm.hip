@@ -19,6 +19,7 @@
 // (output-dtype rounded) result into a float32 residual stream instead of, or
 // besides, storing it -- each output column belongs to one workgroup, so the
 // add needs no synchronisation.
+#include "conv_ops.h"
 #include "norm_ops.h"
 
 namespace {
@@ -125,6 +126,8 @@ constexpr int NORM_MAXG = 8;        // norm groups per row
 constexpr int NORM_MAXX = 32768;    // normalised elements (M x K) held in LDS
 
 struct NormGemmArgs {
+    m2conv::UpdArgs cv;     // conv update of columns [conv_lo, conv_lo + cv.D) (CONV)
+    int64_t conv_lo;
     m2norm::NormArgs n;     // the rows to normalise (out unused: they go to LDS)
     const bf16* w;
     const void* bias;
@@ -135,7 +138,7 @@ struct NormGemmArgs {
     int bias_bf16, y_bf16;
 };
 
-template <int NW>
+template <int NW, bool CONV>
 __global__ void __launch_bounds__(NW * 64) k_skinny_gemm_norm(NormGemmArgs a) {
     extern __shared__ __align__(16) bf16 xs[];          // [M][K] normalised rows
     __shared__ f32x4 red[NW - 1][64];
@@ -247,6 +250,17 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm_norm(NormGemmArgs a) {
         if (m < M) {
             float v = acc[i] + bv;
             if (a.y_bf16) v = (float)(bf16)v;        // the output dtype, also for the residual add
+            if (CONV && n >= a.conv_lo && n < a.conv_lo + a.cv.D) {
+                // the decode conv update of this column's channel (width 4, f32
+                // state in place): each (row, channel) belongs to this lane only
+                const int64_t c = n - a.conv_lo;
+                float* st = reinterpret_cast<float*>(a.cv.nstate) + ((int64_t)m * a.cv.D + c) * 4;
+                const float4 o = *reinterpret_cast<const float4*>(st);
+                const float sv[4] = {o.y, o.z, o.w, v};
+                *reinterpret_cast<float4*>(st) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+                m2conv::conv_store(a.cv, m, c, m2conv::conv_channel<4>(a.cv, sv, c));
+                continue;
+            }
             if (a.y) {
                 if (a.y_bf16) reinterpret_cast<bf16*>(a.y)[(int64_t)m * a.ldy + n] = (bf16)v;
                 else reinterpret_cast<float*>(a.y)[(int64_t)m * a.ldy + n] = v;
@@ -354,15 +368,31 @@ int launch_skinny_gemm_norm(const m2_skinny_gemm_norm_args& a, hipStream_t s) {
     k.bias_bf16 = a.bias_dtype == M2_BF16; k.y_bf16 = a.y_dtype == M2_BF16;
     const int64_t ng = (a.N + 15) / 16;
     const int nsteps = (int)((a.K + 31) / 32);
+    k.conv_lo = -1;
+    if (a.with_conv) {
+        const m2_causal_conv1d_update_args& c = a.conv;
+        M2_REQUIRE(c.width == 4 && c.state_dtype == M2_F32 && c.new_state == c.conv_state &&
+                       c.batch == a.M && a.conv_begin >= 0 && a.conv_begin + c.dim <= a.N &&
+                       c.x_dtype == a.y_dtype && aligned16(c.conv_state),
+                   M2_ERR_UNSUPPORTED, "%s: the conv update needs width 4, an f32 state updated in "
+                   "place, batch M, x_dtype == y_dtype and columns inside N", who);
+        if (int rc = prepare_conv_update(c, k.cv, true)) return rc;
+        k.conv_lo = a.conv_begin;
+    }
     const size_t shm = (size_t)a.M * a.K * 2;
     const dim3 grid((unsigned)ng);
+    const bool cv = a.with_conv;
     // as the plain product: enough wavefronts to keep the weight stream in flight
-    if (ng * 4 >= 2048 || nsteps < 8 * 2 * UNROLL)
-        hipLaunchKernelGGL((k_skinny_gemm_norm<4>), grid, dim3(4 * 64), shm, s, k);
-    else if (ng * 8 >= 2048 || nsteps < 16 * 2 * UNROLL)
-        hipLaunchKernelGGL((k_skinny_gemm_norm<8>), grid, dim3(8 * 64), shm, s, k);
-    else
-        hipLaunchKernelGGL((k_skinny_gemm_norm<16>), grid, dim3(16 * 64), shm, s, k);
+    if (ng * 4 >= 2048 || nsteps < 8 * 2 * UNROLL) {
+        if (cv) hipLaunchKernelGGL((k_skinny_gemm_norm<4, true>), grid, dim3(4 * 64), shm, s, k);
+        else hipLaunchKernelGGL((k_skinny_gemm_norm<4, false>), grid, dim3(4 * 64), shm, s, k);
+    } else if (ng * 8 >= 2048 || nsteps < 16 * 2 * UNROLL) {
+        if (cv) hipLaunchKernelGGL((k_skinny_gemm_norm<8, true>), grid, dim3(8 * 64), shm, s, k);
+        else hipLaunchKernelGGL((k_skinny_gemm_norm<8, false>), grid, dim3(8 * 64), shm, s, k);
+    } else {
+        if (cv) hipLaunchKernelGGL((k_skinny_gemm_norm<16, true>), grid, dim3(16 * 64), shm, s, k);
+        else hipLaunchKernelGGL((k_skinny_gemm_norm<16, false>), grid, dim3(16 * 64), shm, s, k);
+    }
     return check_launch(who);
 }
 

@@ -136,7 +136,8 @@ class SkinnyGemmNormArgs(ctypes.Structure):
                 ("norm_before_gate", _i32), ("w", _c_p), ("bias", _c_p), ("y", _c_p),
                 ("residual", _c_p), ("M", _i64), ("N", _i64), ("K", _i64), ("ldw", _i64),
                 ("ldy", _i64), ("residual_row_stride", _i64), ("w_dtype", _i32),
-                ("bias_dtype", _i32), ("y_dtype", _i32)]
+                ("bias_dtype", _i32), ("y_dtype", _i32), ("with_conv", _i32),
+                ("conv_begin", _i64), ("conv", CausalConv1dUpdateArgs)]
 
 
 # entry point name -> argument struct (every function declared in m2ssd.h)

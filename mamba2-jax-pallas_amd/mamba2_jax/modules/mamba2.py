@@ -31,7 +31,7 @@ import torch
 
 from ..kernels.ssd_combined import mamba_chunk_scan_combined_fwd as _hip_fwd
 from ..ops import linear as _lin
-from ..ops.causal_conv1d import causal_conv1d, causal_conv1d_update
+from ..ops.causal_conv1d import causal_conv1d, causal_conv1d_update, update_from_columns
 from ..ops.rms_norm import rms_norm_gated
 from ..ops.selective_state_update import selective_state_update
 from ..ops.ssd_naive import mamba_chunk_scan_combined_naive
@@ -303,12 +303,21 @@ def mamba2_block_step_fused(res, norm_weight, p, d, conv_state, ssm_state, eps=1
     of the norms' sums of squares (summed in another order)."""
     G, N, H, Pd = d.ngroups, d.d_state, d.nheads, d.headdim
     batch = res.shape[0]
-    zxbcdt = _lin.linear_norm(res, norm_weight, p["in_proj_t"], eps=eps, bias=p.get("in_proj_bias"),
-                              out_dtype=p["in_proj_t"].dtype)
-    _, _, z, xBC, dt = _split_last(zxbcdt, [0, 0, d.d_ssm, d.conv_dim, d.nheads])
-    conv_state, (x, B, C) = causal_conv1d_update(
-        xBC, conv_state, p["conv1d_weight"], p.get("conv1d_bias"), "silu",
-        split_sizes=(d.d_ssm, G * N, G * N))
+    odt = p["in_proj_t"].dtype
+    if conv_state.dtype == torch.float32 and conv_state.is_contiguous() and d.d_conv == 4:
+        # the conv update runs in the in-projection's epilogue on the xBC columns
+        cargs, (x, B, C) = update_from_columns(conv_state, p["conv1d_weight"], p.get("conv1d_bias"),
+                                               "silu", x_dtype=odt, split_sizes=(d.d_ssm, G * N, G * N))
+        zxbcdt = _lin.linear_norm(res, norm_weight, p["in_proj_t"], eps=eps, bias=p.get("in_proj_bias"),
+                                  out_dtype=odt, conv_update=(cargs, d.d_ssm))
+        _, _, z, _, dt = _split_last(zxbcdt, [0, 0, d.d_ssm, d.conv_dim, d.nheads])
+    else:
+        zxbcdt = _lin.linear_norm(res, norm_weight, p["in_proj_t"], eps=eps,
+                                  bias=p.get("in_proj_bias"), out_dtype=odt)
+        _, _, z, xBC, dt = _split_last(zxbcdt, [0, 0, d.d_ssm, d.conv_dim, d.nheads])
+        conv_state, (x, B, C) = causal_conv1d_update(
+            xBC, conv_state, p["conv1d_weight"], p.get("conv1d_bias"), "silu",
+            split_sizes=(d.d_ssm, G * N, G * N))
     ssm_state, y = selective_state_update(
         ssm_state, x.view(batch, H, Pd), dt, _A(p), B.view(batch, G, N), C.view(batch, G, N),
         D=_D(p, d), dt_bias=p["dt_bias"], dt_softplus=True)

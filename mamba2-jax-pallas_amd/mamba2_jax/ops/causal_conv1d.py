@@ -114,6 +114,42 @@ def causal_conv1d(x, weight, bias=None, activation=None, seq_idx=None, *, split_
     return parts[0] if split_sizes is None else tuple(parts)
 
 
+def update_from_columns(conv_state, weight, bias=None, activation=None, *, x_dtype=torch.bfloat16,
+                        split_sizes=None):
+    """The arguments of an in-place decode conv update whose new inputs are
+    produced by another kernel (the in-projection's epilogue, see
+    ops.linear.linear_norm): -> (CausalConv1dUpdateArgs with x unset, out
+    parts).  conv_state (batch, d, width) float32 contiguous."""
+    dev = L.device_of(conv_state, weight, bias)
+    L.require(conv_state.dim() == 3 and conv_state.dtype == torch.float32 and conv_state.is_contiguous(),
+              "conv_state must be a contiguous float32 (batch, d, width) tensor")
+    batch, dim, width = (int(v) for v in conv_state.shape)
+    w, kw = _weight(weight, dim)
+    L.require(kw == width, f"weight width {kw} != conv_state width {width}")
+    if bias is not None:
+        L.require(tuple(bias.shape) == (dim,), f"bias.shape={tuple(bias.shape)}")
+    b_c = _float_tensor(bias, "bias")
+    nsdt = _result_dtype(torch.float32, x_dtype)
+    odt = _result_dtype(nsdt, w.dtype, None if b_c is None else b_c.dtype)
+    sizes = _splits(dim, split_sizes)
+    parts, outs, c0 = [], (L.ConvOut * 3)(), 0
+    for j, dj in enumerate(sizes):
+        part = torch.empty((batch, dj), dtype=odt, device=dev)
+        outs[j] = L.ConvOut(L.ptr(part), c0, part.stride(0), 1, 0)
+        parts.append(part)
+        c0 += dj
+    args = L.CausalConv1dUpdateArgs(
+        x=None, x_stride_batch=0, conv_state=L.ptr(conv_state), new_state=L.ptr(conv_state),
+        weight=L.ptr(w), bias=L.ptr(b_c), out=outs, batch=batch, dim=dim, width=width,
+        nout=len(sizes), x_dtype=L.M2_BF16 if x_dtype == torch.bfloat16 else L.M2_F32,
+        state_dtype=L.M2_F32, new_state_dtype=L.M2_F32, w_dtype=L.dtype_code(w, "weight"),
+        bias_dtype=L.M2_F32 if b_c is None else L.dtype_code(b_c, "bias"),
+        out_dtype=L.dtype_code(parts[0], "out"), silu=int(activation == "silu"))
+    # keep the converted operands alive as long as the arguments
+    args._keep = (w, b_c)
+    return args, (parts[0] if split_sizes is None else tuple(parts))
+
+
 def causal_conv1d_update(x_new, conv_state, weight, bias=None, activation=None, *,
                          inplace=True, split_sizes=None):
     """-> (new_conv_state (batch, d, width), out (batch, d)) (out: a tuple of
@@ -163,4 +199,4 @@ def causal_conv1d_update(x_new, conv_state, weight, bias=None, activation=None, 
     return new_state, (parts[0] if split_sizes is None else tuple(parts))
 
 
-__all__ = ["causal_conv1d", "causal_conv1d_update"]
+__all__ = ["causal_conv1d", "causal_conv1d_update", "update_from_columns"]

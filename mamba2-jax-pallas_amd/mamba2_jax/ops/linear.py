@@ -84,13 +84,16 @@ def norm_supported(x, w, z=None, group_size=None):
 
 
 def linear_norm(x, norm_weight, w, z=None, group_size=None, eps=1e-5, norm_before_gate=True,
-                bias=None, out_dtype=torch.bfloat16, residual=None, store=True):
+                bias=None, out_dtype=torch.bfloat16, residual=None, store=True, conv_update=None):
     """y = rms_norm_gated(x, norm_weight, z, eps, group_size, norm_before_gate)
     @ w.T (+ bias) in one kernel (m2_skinny_gemm_norm): x (M <= 4, K), w (N, K)
     bf16.  The normalised rows are bf16, as rms_norm_gated(..., out_dtype=
     torch.bfloat16) gives them.  residual (M, N) float32: the result (rounded
     to out_dtype) is added into it in place; with store=False y is not
-    written and None is returned."""
+    written and None is returned.  conv_update = (args, begin): the decode
+    conv update (ops.causal_conv1d.update_from_columns) of output columns
+    [begin, begin + args.dim), run on them in the epilogue (width 4, float32
+    state in place); those columns of y are then not written."""
     dev = L.device_of(x, norm_weight, w, z, bias, residual)
     L.require(norm_supported(x, w, z, group_size),
               f"linear_norm: x {tuple(x.shape)} {x.dtype}, w {tuple(w.shape)} {w.dtype}: need M <= "
@@ -120,6 +123,11 @@ def linear_norm(x, norm_weight, w, z=None, group_size=None, eps=1e-5, norm_befor
         ldy=N, residual_row_stride=0 if residual is None else (residual.stride(0) if M > 1 else N),
         w_dtype=L.M2_BF16, bias_dtype=L.M2_F32 if b is None else L.dtype_code(b, "bias"),
         y_dtype=L.M2_BF16 if out_dtype == torch.bfloat16 else L.M2_F32)
+    if conv_update is not None:
+        cargs, begin = conv_update
+        L.require(int(cargs.batch) == M and 0 <= begin and begin + int(cargs.dim) <= N,
+                  "conv_update: batch M and columns inside N")
+        args.with_conv, args.conv_begin, args.conv = 1, int(begin), cargs
     with torch.cuda.device(dev):
         L.call("m2_skinny_gemm_norm", args, L.stream_of(dev))
     return y

@@ -123,3 +123,31 @@ def test_skinny_gemm_norm_limits():
                              y_dtype=L.M2_BF16)
     with pytest.raises(L.M2Error):                          # neither y nor residual
         L.call("m2_skinny_gemm_norm", a, 0)
+
+
+@pytest.mark.parametrize("M,bias", [(1, True), (4, False)])
+def test_skinny_gemm_norm_conv_epilogue(M, bias):
+    """The decode conv update run in the in-projection's epilogue equals the
+    projection followed by causal_conv1d_update (same rounding of the new
+    inputs, same conv arithmetic): outputs and the in-place state bit for bit."""
+    from mamba2_jax.ops.causal_conv1d import causal_conv1d_update, update_from_columns
+    announce("skinny_gemm_norm + conv update", M, bias)
+    g = torch.Generator(device="cuda").manual_seed(M + 100)
+    K, d_ssm, GN, H = 768, 1536, 128, 24
+    conv_dim, N = d_ssm + 2 * GN, 2 * d_ssm + 2 * GN + H
+    x = torch.randn((M, K), generator=g, device="cuda")
+    nw = torch.rand(K, generator=g, device="cuda").add(0.5).to(torch.bfloat16)
+    w = (torch.randn((N, K), generator=g, device="cuda") / K ** 0.5).to(torch.bfloat16)
+    cw = (torch.randn((conv_dim, 4), generator=g, device="cuda") * 0.5).to(torch.bfloat16)
+    cb = torch.randn(conv_dim, generator=g, device="cuda").to(torch.bfloat16) if bias else None
+    st0 = torch.randn((M, conv_dim, 4), generator=g, device="cuda")
+    st_a, st_b = st0.clone(), st0.clone()
+    split = (d_ssm, GN, GN)
+    y = linear_norm(x, nw, w)
+    st_b, want = causal_conv1d_update(y[:, d_ssm:d_ssm + conv_dim], st_b, cw, cb, "silu", split_sizes=split)
+    cargs, got = update_from_columns(st_a, cw, cb, "silu", split_sizes=split)
+    y2 = linear_norm(x, nw, w, conv_update=(cargs, d_ssm))
+    for a_, b_ in zip(got, want):
+        assert torch.equal(a_, b_)
+    assert torch.equal(st_a, st_b)
+    assert torch.equal(y2[:, :d_ssm], y[:, :d_ssm]) and torch.equal(y2[:, -H:], y[:, -H:])
