@@ -348,7 +348,7 @@ int m2_skinny_gemm(const m2_skinny_gemm_args* a, void* stream);
 
 /* ---------------------------------------------------------------------------
  * skinny_gemm_norm: y = rms_norm_gated(x, norm_weight, z)[M, K] w[N, K]^T
- * (+ bias) for M <= 4 and M * K <= 32768: m2_skinny_gemm whose input rows are
+ * (+ bias) for M <= 16 and M * K <= 32768: m2_skinny_gemm whose input rows are
  * normalised first, with m2_rms_norm_gated's arithmetic (groups of group_size
  * <= 8 per row, the optional SiLU gate z before / after the norm, the
  * reference's rounding points) and stored as bf16 -- done by every

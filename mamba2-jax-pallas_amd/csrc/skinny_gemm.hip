@@ -12,7 +12,7 @@
 // MT = ceil(M / 16) row tiles share each weight fragment.
 //
 // k_skinny_gemm_norm is the same product for a decode step's first rows
-// (M <= 4) whose x is the output of an RMSNorm (optionally SiLU-gated, over
+// (M <= 16, M * K <= 32768) whose x is the output of an RMSNorm (optionally SiLU-gated, over
 // groups): every workgroup normalises the rows itself into LDS (bf16; a few
 // KB read from L2) while its first weight fragments load, so the norm costs no
 // launch and no HBM round trip of its output; the epilogue can add the
@@ -121,7 +121,7 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm(GemmArgs a) {
         }
 }
 
-constexpr int NORM_MAXM = 4;        // rows of the normalising GEMM
+constexpr int NORM_MAXM = 16;       // rows of the normalising GEMM (one row tile)
 constexpr int NORM_MAXG = 8;        // norm groups per row
 constexpr int NORM_MAXX = 32768;    // normalised elements (M x K) held in LDS
 

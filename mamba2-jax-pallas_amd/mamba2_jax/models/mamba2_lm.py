@@ -272,7 +272,7 @@ class Mamba2LMHeadModel:
     def __init__(self, config: Mamba2Config):
         self.config = config
         self._prep = None
-        # decode steps of <= 4 rows run the norms inside the projections
+        # small decode batches (block_step_fusable) run the norms inside the projections
         # (mamba2_block_step_fused) when the parameters allow it
         self.fuse_decode = True
 
@@ -359,7 +359,7 @@ class Mamba2LMHeadModel:
 
     def decode_step(self, params, token, state: DecodeState):
         """token (batch,) -> next-token logits (batch, vocab); states in place
-        (reference _scan_decode_step, :667-736).  Up to 4 rows with bf16
+        (reference _scan_decode_step, :667-736).  Small batches (up to 16 rows of at most 32768 normalised elements) with bf16
         projections: each layer's norms run inside its projections
         (mamba2_block_step_fused; 4 kernels per layer), the final norm inside
         the LM head."""

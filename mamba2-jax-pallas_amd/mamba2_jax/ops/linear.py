@@ -56,7 +56,7 @@ def linear_skinny(x, w, bias=None, out_dtype=torch.bfloat16):
     return y
 
 
-NORM_MAX_ROWS = 4
+NORM_MAX_ROWS = 16
 NORM_MAX_ELEMS = 32768      # M * K normalised elements held in LDS
 NORM_MAX_GROUPS = 8
 
@@ -86,7 +86,7 @@ def norm_supported(x, w, z=None, group_size=None):
 def linear_norm(x, norm_weight, w, z=None, group_size=None, eps=1e-5, norm_before_gate=True,
                 bias=None, out_dtype=torch.bfloat16, residual=None, store=True, conv_update=None):
     """y = rms_norm_gated(x, norm_weight, z, eps, group_size, norm_before_gate)
-    @ w.T (+ bias) in one kernel (m2_skinny_gemm_norm): x (M <= 4, K), w (N, K)
+    @ w.T (+ bias) in one kernel (m2_skinny_gemm_norm): x (M <= 16, M * K <= 32768), w (N, K)
     bf16.  The normalised rows are bf16, as rms_norm_gated(..., out_dtype=
     torch.bfloat16) gives them.  residual (M, N) float32: the result (rounded
     to out_dtype) is added into it in place; with store=False y is not

@@ -68,6 +68,8 @@ NORM_CASES = [
     (3, 8192, 4096, "f32", True, 1024, False, False),      # nemotron-h-8b: 8 groups
     (2, 1536, 768, "bf16", True, 768, True, True),
     (4, 64, 40, "bf16", False, 16, True, False),
+    (16, 768, 3352, "f32", False, None, True, False),     # 130m pre-norm, batch 16
+    (11, 1536, 768, "f32", True, 768, False, True),       # 130m-like gated norm, 2 groups
 ]
 
 
@@ -113,8 +115,8 @@ def test_skinny_gemm_norm(case):
 def test_skinny_gemm_norm_limits():
     w = torch.zeros((16, 64), device="cuda", dtype=torch.bfloat16)
     nw = torch.ones(64, device="cuda", dtype=torch.bfloat16)
-    with pytest.raises(AssertionError):                    # 5 rows
-        linear_norm(torch.zeros((5, 64), device="cuda"), nw, w)
+    with pytest.raises(AssertionError):                    # 17 rows
+        linear_norm(torch.zeros((17, 64), device="cuda"), nw, w)
     with pytest.raises(AssertionError):                    # 16 groups
         linear_norm(torch.zeros((1, 64), device="cuda"), nw, w, group_size=4)
     a = L.SkinnyGemmNormArgs(x=w.data_ptr(), norm_weight=nw.data_ptr(), w=w.data_ptr(), y=0,
