@@ -301,7 +301,7 @@ def bench_ops(lm_configs=("130m",)):
         cfg = shapes[name]
         params = init_params(cfg, dtype=torch.bfloat16, device=dev)
         m = Mamba2LMHeadModel(cfg)
-        for bsz in (1, 64):
+        for bsz in (1, 16, 64):
             state = DecodeState(cfg, bsz, dev)
             ids = torch.randint(0, cfg.vocab_size, (bsz, 32), device=dev)
             m.prefill(params, ids, state)

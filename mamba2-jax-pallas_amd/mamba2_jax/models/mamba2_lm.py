@@ -359,7 +359,7 @@ class Mamba2LMHeadModel:
 
     def decode_step(self, params, token, state: DecodeState):
         """token (batch,) -> next-token logits (batch, vocab); states in place
-        (reference _scan_decode_step, :667-736).  Small batches (up to 16 rows of at most 32768 normalised elements) with bf16
+        (reference _scan_decode_step, :667-736).  Batches of up to 2 rows with bf16
         projections: each layer's norms run inside its projections
         (mamba2_block_step_fused; 4 kernels per layer), the final norm inside
         the LM head."""

@@ -283,10 +283,10 @@ def mamba2_block_step(u_t, p, d, conv_state, ssm_state):
 def block_step_fusable(p, d, batch, d_model):
     """True when mamba2_block_step_fused can run this mixer at this batch: bf16
     projections with their [out, in] copies, the gated norm (no MLP bypass),
-    and rows the normalising GEMM takes (<= 16 rows of <= 32768 elements in all,
-    4-element aligned)."""
+    and rows the normalising GEMM takes and runs faster than the separate
+    kernels (<= 2 rows, 4-element aligned)."""
     return (d.rmsnorm and d.d_mlp == 0 and p.get("in_proj_t") is not None
-            and p.get("out_proj_t") is not None and batch <= _lin.NORM_MAX_ROWS
+            and p.get("out_proj_t") is not None and batch <= _lin.NORM_PREFERRED_ROWS
             and batch * max(d_model, d.d_ssm) <= _lin.NORM_MAX_ELEMS and d_model % 8 == 0
             and d.d_ssm % 8 == 0 and (d.d_ssm // d.ngroups) % 4 == 0
             and d.ngroups <= _lin.NORM_MAX_GROUPS and (2 * d.d_ssm + 2 * d.ngroups * d.d_state

@@ -57,6 +57,11 @@ def linear_skinny(x, w, bias=None, out_dtype=torch.bfloat16):
 
 
 NORM_MAX_ROWS = 16
+# rows up to which the decode layer prefers the normalising projections: each
+# workgroup normalises every row itself, one row after another, so the
+# prologue's latency grows with the rows (measured on MI355X, 130m shapes:
+# 1 row 4.7 us fused vs 6.7 us norm + skinny GEMM; 4 rows 9.1 vs 7.4 us)
+NORM_PREFERRED_ROWS = 2
 NORM_MAX_ELEMS = 32768      # M * K normalised elements held in LDS
 NORM_MAX_GROUPS = 8
 

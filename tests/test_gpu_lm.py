@@ -121,7 +121,7 @@ def test_generate_graph_equals_eager():
     assert torch.equal(c, d)
 
 
-@pytest.mark.parametrize("batch", [1, 4, 16])
+@pytest.mark.parametrize("batch", [1, 2])
 def test_fused_decode_matches_unfused(batch):
     """The decode step with the norms inside the projections
     (mamba2_block_step_fused, batch <= 4) against the separate norm kernels:
