@@ -207,13 +207,13 @@ def bench_decode(steps=256, warmup=16):
     A, D, bias = f(d["A"]), f(d["D"]), f(d["dt_bias"])
     for t in range(warmup):
         selective_state_update(state, xs[t], dts[t], A, Bs[t], Cs[t], D=D, z=zs[t],
-                               dt_bias=bias, dt_softplus=True)
+                               dt_bias=bias, dt_softplus=True, inplace=True)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for t in range(steps):
         selective_state_update(state, xs[t], dts[t], A, Bs[t], Cs[t], D=D, z=zs[t],
-                               dt_bias=bias, dt_softplus=True)
+                               dt_bias=bias, dt_softplus=True, inplace=True)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
@@ -289,7 +289,7 @@ def bench_ops(lm_configs=("130m",)):
     bsz = 64
     st = torch.randn((bsz, D, W), generator=g, device=dev)
     xn = rnd(bsz, D)
-    ms = _graph_time_ms(lambda: causal_conv1d_update(xn, st, w, b, "silu"))
+    ms = _graph_time_ms(lambda: causal_conv1d_update(xn, st, w, b, "silu", inplace=True))
     by = bsz * D * (2 * W * 4 + 2 + 4)
     out["causal_conv1d_update"] = {"workload": f"batch {bsz}, {D} channels, f32 state in place",
                                    "ms": ms, "bytes": by, "hbm_gbs": by / (ms * 1e-3) / 1e9}

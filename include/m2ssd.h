@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define M2SSD_ABI_VERSION 3
+#define M2SSD_ABI_VERSION 4
 
 /* return codes */
 #define M2_OK               0
@@ -207,13 +207,15 @@ size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a);
 int m2_ssd_combined(const m2_ssd_combined_args* a, void* stream);
 
 /* ---------------------------------------------------------------------------
- * selective_state_update (one decode token, state updated IN PLACE):
- * dt' = softplus?(dt + dt_bias); state = state * exp(dt' A) + dt' x B^T;
- * out = state @ C + D x; out *= silu(z).
+ * selective_state_update (one decode token):
+ * dt' = softplus?(dt + dt_bias); new = state * exp(dt' A) + dt' x B^T;
+ * out = new @ C + D x; out *= silu(z).
+ * new goes to new_state, or back into state when new_state is NULL (or
+ * equal to state): the in-place update of a decode loop that owns its state.
  * Replaces selective_state_update (reference ops/selective_state_update.py:22-123).
  * ------------------------------------------------------------------------- */
 typedef struct {
-    float*       state;        /* [b, H, P, N], updated in place         */
+    float*       state;        /* [b, H, P, N] (read; written when in place) */
     const void*  x;            /* [b, H, P], dtype                       */
     const void*  dt;           /* [b, H] or [b, H, P], dt_dtype          */
     const float* A;            /* [H] or [H, P, N]                       */
@@ -227,6 +229,7 @@ typedef struct {
     int32_t dtype, dt_dtype;
     int32_t dt_has_hdim, A_full, D_has_hdim, dt_bias_has_hdim;
     int32_t dt_softplus;
+    float*       new_state;    /* [b, H, P, N] result, or NULL: into state */
 } m2_ssu_args;
 int m2_selective_state_update(const m2_ssu_args* a, void* stream);
 

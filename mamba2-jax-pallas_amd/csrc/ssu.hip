@@ -1,7 +1,8 @@
-// selective_state_update: one decode token, fp32 state updated in place
+// selective_state_update: one decode token on an fp32 state
 //   dt' = softplus?(dt + dt_bias)
-//   state[p,n] = state[p,n] * exp(dt' A) + dt' x[p] B[n]
-//   y[p] = sum_n state[p,n] C[n] + D x[p];   y *= silu(z[p])
+//   new[p,n] = state[p,n] * exp(dt' A) + dt' x[p] B[n]
+//   y[p] = sum_n new[p,n] C[n] + D x[p];   y *= silu(z[p])
+// new goes to a separate tensor or back into state (in place).
 //
 // HBM-bound: the state (b*H*P*N fp32) is read and written exactly once.  One
 // workgroup per (batch, head), or per slice of its rows for small batches
@@ -18,7 +19,8 @@ namespace {
 constexpr int THREADS = 256;
 
 struct SsuArgs {
-    float* state;
+    const float* state;         // read
+    float* new_state;           // written (may equal state)
     const void* x;
     const void* dt;
     const float* A;
@@ -48,7 +50,8 @@ __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
     const int P = a.P, N = a.N;
     const int tr = threadIdx.x / TPR;           // row within a pass
     const int n0 = (threadIdx.x % TPR) * 4;
-    float* st = a.state + (int64_t)bh * P * N;
+    const float* st = a.state + (int64_t)bh * P * N;
+    float* nst = a.new_state + (int64_t)bh * P * N;
 
     float Bv[4], Cv[4];
 #pragma unroll
@@ -90,7 +93,7 @@ __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
                 part += v[j] * Cv[j];
             }
         }
-        *reinterpret_cast<float4*>(st + (int64_t)p * N + n0) = make_float4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<float4*>(nst + (int64_t)p * N + n0) = make_float4(v[0], v[1], v[2], v[3]);
 #pragma unroll
         for (int off = TPR / 2; off > 0; off >>= 1) part += __shfl_xor(part, off, TPR);
         if (threadIdx.x % TPR == 0) {
@@ -117,6 +120,9 @@ int launch_typed(SsuArgs sa, int64_t nblocks, hipStream_t s) {
     sa.nsl = nsl;
 #define M2_SSU_CASE(TPRV, RPTV) \
     if (tpr == TPRV && rpt <= RPTV && !kern) kern = k_ssu<T, TPRV, RPTV>;
+    M2_SSU_CASE(1, 1) M2_SSU_CASE(1, 2) M2_SSU_CASE(1, 4)                        // N = 4
+    M2_SSU_CASE(2, 1) M2_SSU_CASE(2, 2) M2_SSU_CASE(2, 4)                        // N = 8
+    M2_SSU_CASE(4, 1) M2_SSU_CASE(4, 2) M2_SSU_CASE(4, 4)                        // N = 16
     M2_SSU_CASE(8, 1) M2_SSU_CASE(8, 2) M2_SSU_CASE(8, 4)                        // N = 32
     M2_SSU_CASE(16, 1) M2_SSU_CASE(16, 2) M2_SSU_CASE(16, 4) M2_SSU_CASE(16, 8)  // N = 64
     M2_SSU_CASE(32, 1) M2_SSU_CASE(32, 2) M2_SSU_CASE(32, 4) M2_SSU_CASE(32, 8)
@@ -152,7 +158,8 @@ int launch_ssu(const m2_ssu_args& a, hipStream_t s) {
     const int64_t nblocks = a.batch * a.nheads;
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "selective_state_update: too many blocks");
     SsuArgs sa{};
-    sa.state = a.state; sa.x = a.x; sa.dt = a.dt; sa.A = a.A; sa.B = a.B; sa.C = a.C; sa.D = a.D;
+    sa.state = a.state; sa.new_state = a.new_state ? a.new_state : a.state;
+    sa.x = a.x; sa.dt = a.dt; sa.A = a.A; sa.B = a.B; sa.C = a.C; sa.D = a.D;
     sa.z = a.z; sa.dt_bias = a.dt_bias; sa.out = a.out;
     sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.P = (int)a.headdim; sa.N = (int)a.dstate;
     sa.dt_bf16 = a.dt_dtype == M2_BF16; sa.dt_has_hdim = a.dt_has_hdim; sa.A_full = a.A_full;

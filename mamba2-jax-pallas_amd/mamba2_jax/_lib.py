@@ -19,7 +19,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm2ssd.so
 
 M2_F32 = 0
 M2_BF16 = 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -91,7 +91,7 @@ class SsuArgs(ctypes.Structure):
                 ("batch", _i64), ("nheads", _i64), ("headdim", _i64), ("ngroups", _i64),
                 ("dstate", _i64), ("dtype", _i32), ("dt_dtype", _i32),
                 ("dt_has_hdim", _i32), ("A_full", _i32), ("D_has_hdim", _i32),
-                ("dt_bias_has_hdim", _i32), ("dt_softplus", _i32)]
+                ("dt_bias_has_hdim", _i32), ("dt_softplus", _i32), ("new_state", _c_p)]
 
 
 class ConvOut(ctypes.Structure):

@@ -276,12 +276,27 @@ class Mamba2LMHeadModel:
         # (mamba2_block_step_fused) when the parameters allow it
         self.fuse_decode = True
 
-    def _prepared(self, params):
-        """Per-layer mixer dicts (cached per parameter dict) with A =
-        -exp(A_log) precomputed, so that a decode step launches no kernels for
-        it, and, for bf16 weights, K-contiguous copies of the projections
-        ([out, in]) for the decode step's skinny GEMM."""
-        if self._prep is None or self._prep[0] is not params:
+    @staticmethod
+    def _sources(params):
+        """The tensors _prepared derives its copies from, with the storage
+        address and version counter of each: an in-place update of any of
+        them (optimizer step, load_state_dict copy) changes the key."""
+        ts = [t for lp in params["layers"]
+              for t in (lp["mixer"]["A_log"], lp["mixer"]["in_proj_kernel"],
+                        lp["mixer"]["out_proj_kernel"])] + [params["lm_head_weight"]]
+        return tuple((t.data_ptr(), t._version) for t in ts)
+
+    def _prepared(self, params, head=False):
+        """Per-layer mixer dicts with A = -exp(A_log) precomputed, so that a
+        decode step launches no kernels for it, and, for bf16 weights,
+        K-contiguous copies of the projections ([out, in]) for the decode
+        step's skinny GEMM; with head=True the float32 LM head weight (the
+        head's float32 matmul).  Cached per parameter dict and rebuilt when
+        any source tensor is replaced or updated in place.  The copies cost
+        memory: with bf16 weights the projections are held twice (about 5 GB
+        at 2.7b) and the float32 head once more (vocab x d_model x 4 bytes)."""
+        key = self._sources(params)
+        if self._prep is None or self._prep[0] is not params or self._prep[1] != key:
             mixers = []
             for lp in params["layers"]:
                 mx = dict(lp["mixer"])
@@ -291,17 +306,25 @@ class Mamba2LMHeadModel:
                     if k.dtype == torch.bfloat16 and k.shape[0] % 8 == 0:
                         mx[name + "_t"] = k.t().contiguous()
                 mixers.append(mx)
-            self._prep = (params, mixers)
-        return self._prep[1]
+            self._prep = (params, key, mixers, {})
+        if head:
+            extra = self._prep[3]
+            if "head32" not in extra:
+                w = params["lm_head_weight"]
+                extra["head32"] = w if w.dtype == torch.float32 else w.float()
+            return extra["head32"]
+        return self._prep[2]
 
-    def _run_layers(self, params, x, block):
+    def _run_layers(self, params, x, block, fp32_residual=None):
         """The residual stack (reference :196-211): per layer x = x +
-        mixer(rmsnorm(x)).  With a float32 residual the add is fused into the
-        next norm (one kernel per layer boundary).  block(i, xn, mixer) runs
-        layer i's mixer.  -> (residual, last mixer output not yet added)."""
+        mixer(rmsnorm(x)).  With a float32 residual (cfg.residual_in_fp32, or
+        fp32_residual=True: the decode step's, reference :680) the add is fused
+        into the next norm (one kernel per layer boundary).  block(i, xn,
+        mixer) runs layer i's mixer.  -> (residual, last mixer output not yet
+        added)."""
         cfg = self.config
         layers, mixers = params["layers"], self._prepared(params)
-        if cfg.residual_in_fp32:
+        if cfg.residual_in_fp32 if fp32_residual is None else fp32_residual:
             res = x.float().contiguous()        # a fresh buffer: updated in place
             out = None
             for i, (lp, mx) in enumerate(zip(layers, mixers)):
@@ -316,15 +339,22 @@ class Mamba2LMHeadModel:
         return x, None
 
     def _head(self, params, res, out=None):
-        """final norm (with the last residual add) and the tied LM head."""
+        """final norm (with the last residual add) and the LM head -> float32
+        logits: the reference multiplies the float32 normalised activations by
+        the head weight, which promotes to a float32 matmul (:213-216,
+        :732-736).  A decode-sized batch with bf16 weights runs the skinny GEMM
+        on the bf16-rounded activations with float32 accumulation and output;
+        otherwise the matmul is float32 throughout."""
         w = params["lm_head_weight"]
-        if out is None:
-            xn = rms_norm(res.float(), params["norm_f_weight"], out_dtype=w.dtype)
+        src, resid = (res.float(), None) if out is None else (out, res)
+        if res.dim() == 2 and w.dtype == torch.bfloat16 and res.shape[0] <= linear.PREFERRED_ROWS:
+            xn = rms_norm(src, params["norm_f_weight"], out_dtype=w.dtype, residual=resid)
+            if linear.preferred(xn, w):
+                return linear.linear_skinny(xn, w, out_dtype=torch.float32)
+            xn = xn.float()
         else:
-            xn = rms_norm(out, params["norm_f_weight"], out_dtype=w.dtype, residual=res)
-        if xn.dim() == 2 and linear.preferred(xn, w):
-            return linear.linear_skinny(xn, w, out_dtype=w.dtype)   # decode: the tied head
-        return xn @ w.t()
+            xn = rms_norm(src, params["norm_f_weight"], residual=resid)
+        return xn @ self._prepared(params, head=True).t()
 
     # -- prefill -------------------------------------------------------------
     def _layers(self, params, x, state=None):
@@ -334,7 +364,7 @@ class Mamba2LMHeadModel:
             if state is None:
                 return mamba2_block_forward(xn, mx, d)[0]
             return mamba2_block_forward(xn, mx, d, with_cache=True, conv_state=state.conv[i],
-                                        ssm_state=state.ssm[i])[0]
+                                        ssm_state=state.ssm[i], inplace=True)[0]
         return self._run_layers(params, x, block)
 
     def __call__(self, params, input_ids):
@@ -352,15 +382,16 @@ class Mamba2LMHeadModel:
     def _fusable(self, params, batch):
         cfg = self.config
         w = params["lm_head_weight"]
-        return (self.fuse_decode and cfg.residual_in_fp32 and w.dtype == torch.bfloat16
+        return (self.fuse_decode and w.dtype == torch.bfloat16
                 and w.dim() == 2 and w.shape[1] % 8 == 0 and w.is_cuda
                 and all(block_step_fusable(mx, cfg.mixer_dims(), batch, cfg.d_model)
                         for mx in self._prepared(params)))
 
     def decode_step(self, params, token, state: DecodeState):
-        """token (batch,) -> next-token logits (batch, vocab); states in place
-        (reference _scan_decode_step, :667-736).  Batches of up to 2 rows with bf16
-        projections: each layer's norms run inside its projections
+        """token (batch,) -> next-token logits (batch, vocab) float32; states in
+        place (reference _scan_decode_step, :667-736, whose residual is float32
+        whatever residual_in_fp32 says, :680).  Batches of up to 2 rows with
+        bf16 projections: each layer's norms run inside its projections
         (mamba2_block_step_fused; 4 kernels per layer), the final norm inside
         the LM head."""
         d = self.config.mixer_dims()
@@ -372,11 +403,11 @@ class Mamba2LMHeadModel:
             for i, (lp, mx) in enumerate(zip(params["layers"], self._prepared(params))):
                 mamba2_block_step_fused(res, lp["norm_weight"], mx, d, state.conv[i], state.ssm[i])
             w = params["lm_head_weight"]
-            return linear.linear_norm(res, params["norm_f_weight"], w, out_dtype=w.dtype)
+            return linear.linear_norm(res, params["norm_f_weight"], w, out_dtype=torch.float32)
 
         def block(i, xn, mx):
-            return mamba2_block_step(xn, mx, d, state.conv[i], state.ssm[i])[0]
-        return self._head(params, *self._run_layers(params, x, block))
+            return mamba2_block_step(xn, mx, d, state.conv[i], state.ssm[i], inplace=True)[0]
+        return self._head(params, *self._run_layers(params, x, block, fp32_residual=True))
 
     def capture_decode(self, params, state: DecodeState, warmup=2):
         """Capture decode_step into a HIP graph over static token / logits

@@ -16,9 +16,11 @@ them runs in libm2ssd.so:
 * the conv writes x, B and C straight into the contiguous layouts the SSD
   kernels read (no split / reshape copies);
 * rms_norm_gated reads z in place as a slice of the in-projection output;
-* the decode step updates conv_state and ssm_state IN PLACE (what the
-  reference gets from JAX buffer donation) and returns them in the new
-  inference_params dict, so a decode loop allocates no per-step state.
+* the decode step returns new conv / ssm states in the new inference_params
+  dict and leaves the caller's untouched, as the reference does; with the
+  keyword-only ``inplace=True`` it updates them in place instead (what the
+  reference gets from JAX buffer donation), so a decode loop that owns its
+  states allocates none per step.
 """
 
 from __future__ import annotations
@@ -132,14 +134,16 @@ class Mamba2(torch.nn.Module):
         """The parameters by reference name (absent optional ones as None)."""
         return {k: getattr(self, k) for k in _PARAM_NAMES}
 
-    def forward(self, u, seq_idx=None, cu_seqlens=None, inference_params=None):
+    def forward(self, u, seq_idx=None, cu_seqlens=None, inference_params=None, *, inplace=False):
         """u (batch, seqlen, d_model) -> out (batch, seqlen, d_model), plus the
         new inference_params dict when inference_params is given
-        (reference modules/mamba2.py:163-424)."""
+        (reference modules/mamba2.py:163-424).  The states in the given
+        inference_params are left untouched unless ``inplace`` (then the
+        returned dict holds the same, updated, tensors)."""
         if inference_params is not None and inference_params.get("seqlen_offset", 0) > 0:
             conv_state, ssm_state = inference_params["conv_state"], inference_params["ssm_state"]
             out, conv_state, ssm_state = mamba2_block_step(u[:, 0, :], self.params(), self.dims(),
-                                                           conv_state, ssm_state)
+                                                           conv_state, ssm_state, inplace=inplace)
             return out[:, None, :], {"conv_state": conv_state, "ssm_state": ssm_state,
                                      "seqlen_offset": inference_params["seqlen_offset"] + 1}
         if inference_params is None:
@@ -148,7 +152,7 @@ class Mamba2(torch.nn.Module):
         out, conv_state, ssm_state = mamba2_block_forward(
             u, self.params(), self.dims(), seq_idx, cu_seqlens, with_cache=True,
             conv_state=inference_params.get("conv_state"),
-            ssm_state=inference_params.get("ssm_state"))
+            ssm_state=inference_params.get("ssm_state"), inplace=inplace)
         return out, {"conv_state": conv_state, "ssm_state": ssm_state,
                      "seqlen_offset": inference_params.get("seqlen_offset", 0) + u.shape[1]}
 
@@ -216,14 +220,15 @@ def _D(p, d):
 
 
 def mamba2_block_forward(u, p, d, seq_idx=None, cu_seqlens=None, with_cache=False,
-                         conv_state=None, ssm_state=None):
+                         conv_state=None, ssm_state=None, inplace=False):
     """Prefill of one mixer (reference modules/mamba2.py:296-424) from a
     parameter dict ``p`` (reference names) and MixerDims ``d``.
 
     -> (out (batch, seqlen, d_model), conv_state, ssm_state); the states are
-    None unless with_cache, and are written into the given tensors when their
-    shapes match (conv_state: the last d_conv conv inputs, left-padded with
-    zeros; ssm_state: the SSD's final states).
+    None unless with_cache (conv_state: the last d_conv conv inputs,
+    left-padded with zeros; ssm_state: the SSD's final states).  They are new
+    tensors, or, with ``inplace``, written into the given conv_state /
+    ssm_state when their shapes and dtypes match.
     """
     batch, seqlen, _ = u.shape
     G, N, H, Pd = d.ngroups, d.d_state, d.nheads, d.headdim
@@ -236,7 +241,7 @@ def mamba2_block_forward(u, p, d, seq_idx=None, cu_seqlens=None, with_cache=Fals
             new_conv = xT[:, :, -d.d_conv:]
         else:
             new_conv = torch.nn.functional.pad(xT, (d.d_conv - seqlen, 0))
-        if conv_state is not None and tuple(conv_state.shape) == tuple(new_conv.shape):
+        if inplace and conv_state is not None and tuple(conv_state.shape) == tuple(new_conv.shape):
             conv_state.copy_(new_conv)
             new_conv = conv_state
         else:
@@ -254,28 +259,29 @@ def mamba2_block_forward(u, p, d, seq_idx=None, cu_seqlens=None, with_cache=Fals
                             return_final_states=with_cache, return_varlen_states=False)
     y, final = res if with_cache else (res, None)
     out = _mixer_out(y.reshape(batch, seqlen, d.d_ssm), z, z0, x0, p, d)
-    if with_cache and ssm_state is not None and tuple(ssm_state.shape) == tuple(final.shape) \
-            and ssm_state.dtype == final.dtype:
+    if with_cache and inplace and ssm_state is not None \
+            and tuple(ssm_state.shape) == tuple(final.shape) and ssm_state.dtype == final.dtype:
         ssm_state.copy_(final)
         final = ssm_state
     return out, new_conv, final
 
 
-def mamba2_block_step(u_t, p, d, conv_state, ssm_state):
+def mamba2_block_step(u_t, p, d, conv_state, ssm_state, inplace=False):
     """One decode token of one mixer (reference modules/mamba2.py:427-549):
-    u_t (batch, d_model) -> (out (batch, d_model), conv_state, ssm_state), the
-    states updated in place (float32 states: no copies)."""
+    u_t (batch, d_model) -> (out (batch, d_model), new conv_state, new
+    ssm_state).  With ``inplace`` the given float32 states are updated in place
+    and returned (no per-step state allocation)."""
     G, N, H, Pd = d.ngroups, d.d_state, d.nheads, d.headdim
     batch = u_t.shape[0]
     zxbcdt = _in_proj(u_t.to(p["in_proj_kernel"].dtype), p)
     z0, x0, z, xBC, dt = _split_last(zxbcdt, [d.d_mlp, d.d_mlp, d.d_ssm, d.conv_dim, d.nheads])
     conv_state, (x, B, C) = causal_conv1d_update(
         xBC, conv_state, p["conv1d_weight"], p.get("conv1d_bias"), "silu",
-        split_sizes=(d.d_ssm, G * N, G * N))
+        inplace=inplace, split_sizes=(d.d_ssm, G * N, G * N))
     z_step = None if d.rmsnorm else z.reshape(batch, H, Pd)
     ssm_state, y = selective_state_update(
         ssm_state, x.view(batch, H, Pd), dt, _A(p), B.view(batch, G, N), C.view(batch, G, N),
-        D=_D(p, d), z=z_step, dt_bias=p["dt_bias"], dt_softplus=True)
+        D=_D(p, d), z=z_step, dt_bias=p["dt_bias"], dt_softplus=True, inplace=inplace)
     out = _mixer_out(y.reshape(batch, d.d_ssm), z, z0, x0, p, d)
     return out, conv_state, ssm_state
 
@@ -318,10 +324,10 @@ def mamba2_block_step_fused(res, norm_weight, p, d, conv_state, ssm_state, eps=1
         _, _, z, xBC, dt = _split_last(zxbcdt, [0, 0, d.d_ssm, d.conv_dim, d.nheads])
         conv_state, (x, B, C) = causal_conv1d_update(
             xBC, conv_state, p["conv1d_weight"], p.get("conv1d_bias"), "silu",
-            split_sizes=(d.d_ssm, G * N, G * N))
+            inplace=True, split_sizes=(d.d_ssm, G * N, G * N))
     ssm_state, y = selective_state_update(
         ssm_state, x.view(batch, H, Pd), dt, _A(p), B.view(batch, G, N), C.view(batch, G, N),
-        D=_D(p, d), dt_bias=p["dt_bias"], dt_softplus=True)
+        D=_D(p, d), dt_bias=p["dt_bias"], dt_softplus=True, inplace=True)
     _lin.linear_norm(y.view(batch, d.d_ssm), p["norm_weight"], p["out_proj_t"], z=z,
                      group_size=d.d_ssm // G, norm_before_gate=d.norm_before_gate,
                      bias=p.get("out_proj_bias"), out_dtype=p["out_proj_t"].dtype, residual=res,

@@ -14,9 +14,10 @@ before every sequence start for all outputs).  Differences, all documented:
 * ``split_sizes`` (keyword only, not in the reference) writes consecutive
   channel ranges of the result into separate tensors, e.g. x, B and C of an
   SSD layer in the contiguous layouts the SSD kernels read, with no copy;
-* causal_conv1d_update updates conv_state IN PLACE when its dtype is the new
-  state's (what JAX's buffer donation gives) and returns it as new_conv_state;
-  ``inplace=False`` keeps the caller's state untouched.
+* causal_conv1d_update returns a new conv state and leaves the caller's
+  untouched, as the reference does; a decode loop that owns its state passes
+  the keyword-only ``inplace=True`` to have it updated in place (when its dtype
+  is the new state's), what JAX's buffer donation gives.
 """
 
 from __future__ import annotations
@@ -151,7 +152,7 @@ def update_from_columns(conv_state, weight, bias=None, activation=None, *, x_dty
 
 
 def causal_conv1d_update(x_new, conv_state, weight, bias=None, activation=None, *,
-                         inplace=True, split_sizes=None):
+                         inplace=False, split_sizes=None):
     """-> (new_conv_state (batch, d, width), out (batch, d)) (out: a tuple of
     (batch, d_j) parts with split_sizes).
 

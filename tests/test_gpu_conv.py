@@ -196,7 +196,7 @@ def test_update_matches_prefill(dts, k):
     names = (NAME[xdt], NAME[sdt], NAME[wdt], NAME[bdt])
     for t in range(L):
         new_state, out = causal_conv1d_update(dev(x[:, :, t], xdt), state, dev(w, wdt),
-                                              dev(bias, bdt), "silu")
+                                              dev(bias, bdt), "silu", inplace=True)
         st_np, want, nsdt, odt = X.causal_conv1d_update(x[:, :, t], st_np, w, bias, "silu", *names)
         assert NAME[new_state.dtype] == nsdt and NAME[out.dtype] == odt
         if new_state.dtype == state.dtype:
@@ -229,8 +229,12 @@ def test_update_copy_and_split():
     # x_new as a strided view (a slice of a wider row)
     wide = torch.zeros((b, 2 * d), device="cuda")
     wide[:, d:] = dev(x[:, :, 0])
-    ns2, out2 = causal_conv1d_update(wide[:, d:], dev(st), dev(w), dev(bias), "silu")
+    s1 = dev(st)
+    ns2, out2 = causal_conv1d_update(wide[:, d:], s1, dev(w), dev(bias), "silu")
     _close(out2, want, False, "strided x_new")
+    # the default is functional, as the reference (ops/causal_conv1d.py:88-139)
+    assert ns2.data_ptr() != s1.data_ptr() and np.array_equal(host(s1), st)
+    assert np.array_equal(host(ns2), want_s)
 
 
 def test_capi_token_vectors_with_ragged_tail():

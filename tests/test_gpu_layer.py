@@ -82,8 +82,9 @@ def test_layer_prefill_seq_idx():
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_layer_decode_continues_prefill(dtype):
     """prefill T0 tokens with a cache, then decode T1 tokens one by one: the
-    outputs equal the prefill of all T0 + T1 tokens, and the cache tensors
-    are updated in place."""
+    outputs equal the prefill of all T0 + T1 tokens.  With inplace=True the
+    cache tensors are updated in place; by default (the reference's functional
+    contract) the caller's cache is left untouched."""
     announce("Mamba2 prefill + decode", dtype)
     pd = torch.bfloat16 if dtype == "bf16" else torch.float32
     m = Mamba2(d_model=128, d_state=64, headdim=64, ngroups=2, chunk_size=64, seed=7,
@@ -95,13 +96,20 @@ def test_layer_decode_continues_prefill(dtype):
     full = m(u)
     cache = allocate_inference_cache(b, 128, d_state=64, headdim=64, ngroups=2)
     cs_ptr, ss_ptr = cache["conv_state"].data_ptr(), cache["ssm_state"].data_ptr()
-    out0, cache = m(u[:, :T0], inference_params=cache)
+    out0, cache = m(u[:, :T0], inference_params=cache, inplace=True)
     assert cache["seqlen_offset"] == T0
     check(out0, host(full[:, :T0]), 1e-5 if dtype == "f32" else 1e-2, "prefill with cache")
+    # one functional step first: the cache it is given stays as it was
+    before = {k: cache[k].clone() for k in ("conv_state", "ssm_state")}
+    o_f, c_f = m(u[:, T0:T0 + 1], inference_params=cache)
+    assert all(torch.equal(cache[k], before[k]) for k in before)
+    assert c_f["ssm_state"].data_ptr() != ss_ptr and c_f["seqlen_offset"] == T0 + 1
     outs = []
     for t in range(T0, T0 + T1):
-        o, cache = m(u[:, t:t + 1], inference_params=cache)
+        o, cache = m(u[:, t:t + 1], inference_params=cache, inplace=True)
         outs.append(o)
+        if t == T0:
+            assert torch.equal(o, o_f) and torch.equal(cache["ssm_state"], c_f["ssm_state"])
     assert cache["seqlen_offset"] == T0 + T1
     assert cache["conv_state"].data_ptr() == cs_ptr and cache["ssm_state"].data_ptr() == ss_ptr
     check(torch.cat(outs, 1), host(full[:, T0:]), TOL[dtype], "decode == prefill")

@@ -84,14 +84,20 @@ def test_lm_prefill_then_decode(dtype):
     check(dec, truth, max(2 * e_pre, TOL["bf16"]), "bf16 decode vs f32")
 
 
-def test_decode_graph_replays_match_eager():
+@pytest.mark.parametrize("batch", [1, 2, 3])
+def test_decode_graph_replays_match_eager(batch):
     """Every replay of the captured step equals the eager step from the same
-    state; eager work and syncs run between the replays."""
-    announce("LM decode graph replays")
+    state, bit for bit (logits and both states); eager work and syncs run
+    between the replays.  Batches 1 and 2 with bf16 parameters run the fused
+    decode layer (norms inside the projections, the conv update in the
+    in-projection's epilogue), the path of the LM decode figures; batch 3 the
+    separate kernels."""
+    announce("LM decode graph replays", batch)
     params = init_params(CFG, dtype=torch.bfloat16, seed=5)
     m = Mamba2LMHeadModel(CFG)
-    ids = _ids(np.random.default_rng(6), 3, 40)
-    st_e, st_g = DecodeState(CFG, 3), DecodeState(CFG, 3)
+    assert m._fusable(params, batch) == (batch <= 2)
+    ids = _ids(np.random.default_rng(6), batch, 40)
+    st_e, st_g = DecodeState(CFG, batch), DecodeState(CFG, batch)
     m.prefill(params, ids[:, :30], st_e)
     m.prefill(params, ids[:, :30], st_g)
     g, tok, out = m.capture_decode(params, st_g)
@@ -143,3 +149,64 @@ def test_fused_decode_matches_unfused(batch):
         check(lf, host(lp), TOL["bf16"], f"logits, token {t}")
     check(st_f.ssm, host(st_p.ssm), TOL["bf16"], "ssm states")
     check(st_f.conv, host(st_p.conv), TOL["bf16"], "conv states")
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_logits_are_float32_with_bf16_params(batch):
+    """The reference's head multiplies float32 activations by the head weight,
+    which promotes to float32 logits (models/mamba2_lm.py:213-216, 732-736):
+    prefill and decode (fused and unfused batches) return float32."""
+    announce("LM logits dtype", batch)
+    params = init_params(CFG, dtype=torch.bfloat16, seed=11)
+    m = Mamba2LMHeadModel(CFG)
+    ids = _ids(np.random.default_rng(12), batch, 20)
+    st = DecodeState(CFG, batch)
+    assert m(params, ids).dtype == torch.float32
+    assert m.prefill(params, ids[:, :19], st).dtype == torch.float32
+    assert m.decode_step(params, ids[:, 19], st).dtype == torch.float32
+
+
+def test_decode_residual_is_float32_without_residual_in_fp32():
+    """residual_in_fp32=False: the reference's decode step still keeps its
+    residual in float32 (_scan_decode_step, models/mamba2_lm.py:680), so the
+    decode equals the float32-residual decode of the same parameters exactly,
+    and stays within the bf16 bar of the bf16-residual prefill."""
+    announce("LM decode residual f32")
+    import dataclasses
+    cfg16 = dataclasses.replace(CFG, residual_in_fp32=False)
+    params = init_params(CFG, dtype=torch.bfloat16, seed=13)
+    m16, m32 = Mamba2LMHeadModel(cfg16), Mamba2LMHeadModel(CFG)
+    m16.fuse_decode = m32.fuse_decode = False
+    ids = _ids(np.random.default_rng(14), 3, 24)
+    s16, s32 = DecodeState(cfg16, 3), DecodeState(CFG, 3)
+    m32.prefill(params, ids[:, :20], s32)
+    s16.conv.copy_(s32.conv)
+    s16.ssm.copy_(s32.ssm)
+    for t in range(20, 24):
+        a = m16.decode_step(params, ids[:, t], s16)
+        b = m32.decode_step(params, ids[:, t], s32)
+        assert torch.equal(a, b), f"token {t}"
+
+
+def test_prepared_copies_follow_in_place_weight_updates():
+    """The decode step's derived copies (A, [out, in] projections, the float32
+    head) are rebuilt when a source weight is updated in place."""
+    announce("LM prepared-cache invalidation")
+    params = init_params(CFG, dtype=torch.bfloat16, seed=15)
+    m = Mamba2LMHeadModel(CFG)
+    ids = _ids(np.random.default_rng(16), 1, 12)
+    st = DecodeState(CFG, 1)
+    m.prefill(params, ids[:, :11], st)
+    saved = (st.conv.clone(), st.ssm.clone())
+    before = m.decode_step(params, ids[:, 11], st)
+    with torch.no_grad():
+        params["layers"][0]["mixer"]["out_proj_kernel"].mul_(2.0)
+    fresh = Mamba2LMHeadModel(CFG)
+    st.conv.copy_(saved[0])
+    st.ssm.copy_(saved[1])
+    after = m.decode_step(params, ids[:, 11], st)
+    st.conv.copy_(saved[0])
+    st.ssm.copy_(saved[1])
+    want = fresh.decode_step(params, ids[:, 11], st)
+    assert not torch.equal(before, after)
+    assert torch.equal(after, want)

@@ -4,7 +4,8 @@
   parameter-shape variant the reference supports;
 * 256 consecutive in-place steps against the oracle's float64 trajectory and
   against the HIP prefill over the same tokens (decode == prefill);
-* in-place / copy semantics.
+* functional (default) / in-place semantics, and the reference's own usage
+  pattern (expected values computed from the state after the call).
 """
 
 import numpy as np
@@ -79,7 +80,7 @@ def test_256_steps_trajectory_and_prefill():
         new, y = selective_state_update(state, dev(d["x"][t], torch.bfloat16), dev(d["dt"][t]),
                                         dev(d["A"]), dev(d["B"][t], torch.bfloat16),
                                         dev(d["C"][t], torch.bfloat16), D=dev(d["D"]), z=z,
-                                        dt_bias=dev(d["dt_bias"]), dt_softplus=True)
+                                        dt_bias=dev(d["dt_bias"]), dt_softplus=True, inplace=True)
         assert new.data_ptr() == state.data_ptr()
         ys.append(y)
         ref, wy = O.selective_state_update(ref, d["x"][t], d["dt"][t], d["A"], d["B"][t],
@@ -102,19 +103,56 @@ def test_256_steps_trajectory_and_prefill():
 
 
 def test_inplace_and_copy_semantics():
+    """Default: the caller's state is untouched and a new tensor comes back;
+    inplace=True writes through a float32 contiguous state; a state the kernel
+    cannot write through (non-contiguous) is never written, inplace or not."""
     announce("ssu in-place / copy")
     rng = np.random.default_rng(5)
     d = _step_inputs(rng, 2, 8, 2, 64, 128)
     t = _dev(d)
     s_before = t["state"].clone()
-    new, _ = selective_state_update(**{**t, "state": t["state"]}, dt_softplus=True, inplace=False)
+    new, _ = selective_state_update(**t, dt_softplus=True)
     assert new.data_ptr() != t["state"].data_ptr()
-    torch.testing.assert_close(t["state"], s_before, rtol=0, atol=0)
-    new2, _ = selective_state_update(**t, dt_softplus=True)
+    assert torch.equal(t["state"], s_before), "the default leaves the state alone"
+    new2, _ = selective_state_update(**t, dt_softplus=True, inplace=True)
     assert new2.data_ptr() == t["state"].data_ptr()
-    torch.testing.assert_close(new2, new, rtol=0, atol=0)
-    # a non-contiguous state is never written through: a fresh tensor comes back
+    assert torch.equal(new2, new)
     st_nc = s_before.transpose(2, 3).contiguous().transpose(2, 3)
-    new3, _ = selective_state_update(**{**t, "state": st_nc}, dt_softplus=True)
-    assert new3.data_ptr() != st_nc.data_ptr()
-    torch.testing.assert_close(new3, new, rtol=0, atol=0)
+    keep = st_nc.clone()
+    new3, _ = selective_state_update(**{**t, "state": st_nc}, dt_softplus=True, inplace=True)
+    assert new3.data_ptr() != st_nc.data_ptr() and torch.equal(st_nc, keep)
+    assert torch.equal(new3, new)
+
+
+@pytest.mark.parametrize("with_extras", [False, True])
+def test_reference_usage_pattern(with_extras):
+    """The reference's own tests (tests/test_mamba2_ops.py:25-103) compute the
+    expected state from ``state`` AFTER the call, which only works when the
+    call leaves it untouched: same shapes (b 2, H 4, P 8, N 16, G 2 / 1), float32
+    inputs, the closed form evaluated in float32 torch on the GPU, the
+    reference's bounds (state 1e-5, out 1e-5 / 1e-4)."""
+    announce("ssu reference usage pattern", with_extras)
+    g = torch.Generator(device="cuda").manual_seed(42 + with_extras)
+    r = lambda *s: torch.randn(*s, generator=g, device="cuda")
+    b, H, P, N = 2, 4, 8, 16
+    G = 1 if with_extras else 2
+    state, x = r(b, H, P, N), r(b, H, P)
+    A = -r(H).abs()
+    Bm, Cm = r(b, G, N), r(b, G, N)
+    if with_extras:
+        dt, D, z, bias = r(b, H), r(H), r(b, H, P), r(H)
+        new, out = selective_state_update(state, x, dt, A, Bm, Cm, D=D, z=z, dt_bias=bias,
+                                          dt_softplus=True)
+        dtr = torch.nn.functional.softplus(dt + bias)
+    else:
+        dt = torch.rand(b, H, generator=g, device="cuda") * 0.09 + 0.01
+        new, out = selective_state_update(state, x, dt, A, Bm, Cm, dt_softplus=False)
+        dtr = dt
+    Be, Ce = Bm.repeat_interleave(H // G, dim=1), Cm.repeat_interleave(H // G, dim=1)
+    dA = torch.exp(dtr[:, :, None, None] * A[None, :, None, None])
+    ref_state = state * dA + dtr[:, :, None, None] * Be[:, :, None, :] * x[:, :, :, None]
+    ref_out = (ref_state * Ce[:, :, None, :]).sum(-1)
+    if with_extras:
+        ref_out = (ref_out + D[None, :, None] * x) * torch.nn.functional.silu(z)
+    assert (new - ref_state).abs().max().item() < 1e-5
+    assert (out - ref_out).abs().max().item() < (1e-4 if with_extras else 1e-5)
