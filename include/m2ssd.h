@@ -207,6 +207,20 @@ size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a);
 int m2_ssd_combined(const m2_ssd_combined_args* a, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * m2_ssd_combined without a workspace: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): the same kernels and
+ * results as m2_ssd_combined, with the workspace taken from a static device
+ * array of M2_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends);
+ * a->workspace / a->workspace_bytes are not read.  Calls no allocating
+ * routine.  Problems whose m2_ssd_combined_workspace_size exceeds the array
+ * return M2_ERR_WORKSPACE.  Calls that overlap in time on one GPU race on its
+ * array; the array keeps the last call's contents.
+ * ------------------------------------------------------------------------- */
+#define M2_NOALLOC_SCRATCH_BYTES (128u << 20)
+int m2_ssd_combined_noalloc(const m2_ssd_combined_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
  * selective_state_update (one decode token):
  * dt' = softplus?(dt + dt_bias); new = state * exp(dt' A) + dt' x B^T;
  * out = new @ C + D x; out *= silu(z).

@@ -115,8 +115,15 @@ extern "C" size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a) 
 
 extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
     if (!ap) return m2::set_error(M2_ERR_INVALID, "m2_ssd_combined: NULL args");
-    const m2_ssd_combined_args a = internal_args(*ap);
-    hipStream_t s = (hipStream_t)stream_;
+    return m2::ssd_combined_on(*ap, ap->workspace, ap->workspace_bytes, (hipStream_t)stream_);
+}
+
+// The whole forward over the workspace ws (ws_bytes long): both entry points
+// (m2_ssd_combined with the caller's workspace, m2_ssd_combined_noalloc with
+// the library's static scratch) run this.
+int m2::ssd_combined_on(const m2_ssd_combined_args& a0, void* workspace, size_t workspace_bytes,
+                        hipStream_t s) {
+    const m2_ssd_combined_args a = internal_args(a0);
     M2_REQUIRE(a.chunk_size > 0 && a.batch > 0 && a.seqlen > 0, M2_ERR_INVALID,
                "m2_ssd_combined: batch, seqlen and chunk_size must be positive");
     M2_REQUIRE(m2_dtype_size(a.dtype) != 0, M2_ERR_UNSUPPORTED, "m2_ssd_combined: dtype %d", a.dtype);
@@ -125,10 +132,10 @@ extern "C" int m2_ssd_combined(const m2_ssd_combined_args* ap, void* stream_) {
     M2_REQUIRE(!a.varlen_states || (a.cu_seqlens && a.batch == 1 && a.nseq > 0), M2_ERR_INVALID,
                "m2_ssd_combined: varlen states need cu_seqlens, nseq > 0 and batch == 1");
     const Layout l = layout_of(a);
-    M2_REQUIRE(a.workspace && a.workspace_bytes >= l.total, M2_ERR_WORKSPACE,
+    M2_REQUIRE(workspace && workspace_bytes >= l.total, M2_ERR_WORKSPACE,
                "m2_ssd_combined: workspace of %zu bytes needed, %zu given", l.total,
-               a.workspace_bytes);
-    char* ws = (char*)a.workspace;
+               workspace_bytes);
+    char* ws = (char*)workspace;
     float* dA = (float*)(ws + l.dA);
     float* dto = (float*)(ws + l.dt);
     float* states = (float*)(ws + l.states);

@@ -37,6 +37,10 @@ int launch_scan_fused_cb(const m2_chunk_scan_args& a, hipStream_t stream);
 int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const float* dt_out,
                       const void* states_passed, hipStream_t stream);
 
+// m2_ssd_combined over the workspace `ws` of `ws_bytes` (the argument
+// struct's own workspace fields are not read)
+int ssd_combined_on(const m2_ssd_combined_args& a, void* ws, size_t ws_bytes, hipStream_t stream);
+
 // chunk_state + state_passing of the combined forward in one chunk-sequential
 // pass (bf16 inputs), from the weights / decay of launch_chunk_cumsum_ex;
 // writes the states entering each chunk (bf16) and the final states

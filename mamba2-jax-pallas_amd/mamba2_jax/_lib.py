@@ -20,6 +20,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm2ssd.so
 M2_F32 = 0
 M2_BF16 = 1
 ABI_VERSION = 4
+# bytes of the static scratch m2_ssd_combined_noalloc runs in (M2_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 128 << 20
 
 _c_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -149,6 +151,7 @@ ENTRY_POINTS = {
     "m2_chunk_scan": ChunkScanArgs,
     "m2_chunk_state_varlen": ChunkStateVarlenArgs,
     "m2_ssd_combined": SsdCombinedArgs,
+    "m2_ssd_combined_noalloc": SsdCombinedArgs,
     "m2_selective_state_update": SsuArgs,
     "m2_causal_conv1d": CausalConv1dArgs,
     "m2_causal_conv1d_update": CausalConv1dUpdateArgs,

@@ -83,6 +83,24 @@ def test_struct_layout_matches_header(tmp_path):
             assert int(got[f"{py}.{fname}"]) == getattr(st, fname).offset, f"{py}.{fname}"
 
 
+def test_noalloc_scratch_size_matches_header():
+    src = open(HEADER).read()
+    m = re.search(r"#define M2_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", src)
+    assert m and int(m.group(1)) << int(m.group(2)) == L.NOALLOC_SCRATCH_BYTES
+
+
+def test_noalloc_rejects_oversized_problem_without_gpu():
+    """The size check runs on the host before any device call: the c3 shape
+    (~570 MB of workspace) is refused with M2_ERR_WORKSPACE."""
+    lib = L.load_library()
+    a = L.SsdCombinedArgs(batch=1, seqlen=8192, nheads=256, headdim=64, ngroups=8, dstate=256,
+                          chunk_size=128, dtype=L.M2_BF16, dt_dtype=L.M2_BF16, x=16, dt=16, A=16,
+                          B=16, C=16, out=16)
+    assert lib.m2_ssd_combined_workspace_size(ctypes.byref(a)) > L.NOALLOC_SCRATCH_BYTES
+    assert lib.m2_ssd_combined_noalloc(ctypes.byref(a), None) == -4
+    assert b"static scratch" in lib.m2_last_error()
+
+
 def test_null_args_are_rejected_without_gpu():
     lib = L.load_library()
     for name, st in L.ENTRY_POINTS.items():
