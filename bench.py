@@ -8,14 +8,20 @@ synthetic inputs already resident in HBM, returning the output and the final
 states.  For bf16 at the benchmark shapes the five stages run as three kernels:
 chunk_cumsum (+ chunk-state weights), chunk_state + state_passing (one
 chunk-sequential kernel) and bmm_chunk + chunk_scan (one kernel).  Prints ONE
-JSON line (rank 0): tokens/s and ms per layer (K back-to-back steps with events
-only around them), the roofline fraction of the dominant kernel and the
-per-stage table (a second timed pass of K steps with HIP events recorded on the
-launch stream at every kernel boundary), a decode-step measurement (c4: 256 in-place
-selective_state_update steps) and the CPU baseline (the oracle's NumPy
-restatement of the reference's naive path, timed on a bounded head sample on
-this host's cores).  At c2 it also times the shape with fp32 inputs and each
-stage operator of the reference's API called on its own (stage_operators).
+JSON line (rank 0): tokens/s and ms per layer (W warm-up steps, then K
+back-to-back steps with events only around them), the roofline fraction of the
+dominant kernel and the per-stage table (a pass of max(K, 300) steps just
+before, with HIP events recorded on the launch stream at every kernel
+boundary; it also brings the GPU to the steady clocks an idle GPU lacks).
+
+Measured in the same run, before the headline (which they also bring to steady
+GPU clocks): the other BASELINE configurations c0, c1 and c3 (`configs`: ms per
+layer, tokens/s, per-kernel table, dominant kernel's roofline, a sampled CPU
+baseline), the headline shape with fp32 inputs, each stage operator of the
+reference's API called on its own (`stage_operators`) and the decode step
+(c4: 256 in-place selective_state_update steps).  Then the CPU baseline: the
+oracle's NumPy restatement of the reference's naive path on the full c2
+workload, on this host's cores.
 """
 
 from __future__ import annotations
@@ -182,17 +188,18 @@ def cpu_baseline(cfg, heads, min_seconds=10.0, max_reps=20):
         times.append(time.perf_counter() - t0)
     t = float(np.median(times)) * cfg.nheads / heads
     threads = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    what = ("the full workload" if heads == cfg.nheads else
+            f"{heads} of {cfg.nheads} heads (whole groups) x {cfg.nheads / heads:g} (linear in heads)")
     return {
         "value": cfg.tokens / t, "unit": "tokens/s", "cores": threads, "kind": "port",
-        "ms_per_layer": t * 1e3,
-        "sample": (f"oracle NumPy float32 restatement of ssd_naive, {heads} of {cfg.nheads} heads "
-                   f"(whole groups), full L={cfg.seqlen}; median of {len(times)} runs "
-                   f"x {cfg.nheads / heads:g} (linear in heads); host affinity "
+        "cpu": cpu_model(), "ms_per_layer": t * 1e3,
+        "sample": (f"oracle NumPy float32 restatement of ssd_naive, {what}, full L={cfg.seqlen}; "
+                   f"median of {len(times)} runs; host affinity "
                    f"{len(os.sched_getaffinity(0))} cpus, BLAS threads {threads}"),
     }
 
 
-def bench_decode(steps=256, warmup=16):
+def bench_decode(steps=256, warmup=128):
     """c4: `steps` consecutive in-place decode steps (batch 64, H 128, G 8, P 64, N 128)."""
     import torch
     from mamba2_jax import configs
@@ -326,7 +333,7 @@ def bench_ops(lm_configs=("130m",)):
     return out
 
 
-def bench_fp32_same_shape(cfg, steps=30, warmup=5):
+def bench_fp32_same_shape(cfg, steps=30, warmup=25):
     """The configuration's shape with fp32 inputs (the reference's published
     numbers are fp32 runs at the nemotron-h-8b shape, README.md:35)."""
     import dataclasses
@@ -406,86 +413,80 @@ def bench_stage_operators(cfg, calls=10, replays=5):
     return out
 
 
-def main(argv=None):
-    ap = argparse.ArgumentParser(description=__doc__)
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", default="c2")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=32)
-    ap.add_argument("--ops", action="store_true",
-                    help="instead of the SSD layer: time the ops around it and the LM decode "
-                         "step (one JSON line)")
-    ap.add_argument("--lm", default="130m", help="LM shapes for --ops (comma list: 130m,2.7b)")
-    ap.add_argument("--copy-mb", type=int, default=0,
-                    help="run one device copy of this many MiB first (HBM counter calibration)")
-    args = ap.parse_args(argv)
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): "
-              "this build has no multi-GPU path; the SSD forward shards by head groups with no "
-              "communication, so per-GPU throughput is the one-GPU figure.", file=sys.stderr)
-        return 2
-
-    if args.ops:
-        print(json.dumps({"ops": bench_ops(tuple(x for x in args.lm.split(",") if x))}))
-        return 0
-
-    import numpy as np
+def _layer_inputs(cfg):
+    """Synthetic inputs of a configuration, resident on the GPU, as keyword
+    arguments of mamba_chunk_scan_combined_fwd."""
     import torch
     from mamba2_jax import configs
-    from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
-
-    cfg = configs.CONFIGS[args.config]
-    dev = torch.device("cuda")
     d = configs.make_ssd_inputs(cfg)
+    dev = torch.device("cuda")
     T = torch.bfloat16 if cfg.dtype == "bf16" else torch.float32
     t = lambda a, dt=None: None if a is None else torch.from_numpy(a).to(dev).to(dt or torch.float32)
-    kw = dict(x=t(d["x"], T), dt=t(d["dt"], T), A=t(d["A"]), B=t(d["B"], T), C=t(d["C"], T),
-              D=t(d["D"]), dt_bias=t(d["dt_bias"]), initial_states=t(d["initial_states"]),
-              seq_idx=None if d["seq_idx"] is None else torch.from_numpy(d["seq_idx"]).to(dev),
-              cu_seqlens=None if d["cu_seqlens"] is None else torch.from_numpy(d["cu_seqlens"]).to(dev),
-              chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
-              return_varlen_states=d["cu_seqlens"] is not None)
+    return dict(x=t(d["x"], T), dt=t(d["dt"], T), A=t(d["A"]), B=t(d["B"], T), C=t(d["C"], T),
+                D=t(d["D"]), dt_bias=t(d["dt_bias"]), initial_states=t(d["initial_states"]),
+                seq_idx=None if d["seq_idx"] is None else torch.from_numpy(d["seq_idx"]).to(dev),
+                cu_seqlens=None if d["cu_seqlens"] is None else torch.from_numpy(d["cu_seqlens"]).to(dev),
+                chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
+                return_varlen_states=d["cu_seqlens"] is not None)
 
-    if args.copy_mb:
-        # a plain copy of known size: reads and writes copy_mb MiB once each
-        src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-    for _ in range(args.warmup):
+
+def time_layer(kw, steps, warmup):
+    """(ms per layer, wall ms per step): `warmup` untimed calls, then `steps`
+    back-to-back calls with events only around them, synchronised on both sides."""
+    import torch
+    from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
+    for _ in range(warmup):
         mamba_chunk_scan_combined_fwd(**kw)
-    K = args.steps
-    # timed region 1 (value): K back-to-back steps, events only around them
     torch.cuda.synchronize()
     g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
     g0.record()
-    for i in range(K):
+    for _ in range(steps):
         mamba_chunk_scan_combined_fwd(**kw)
     g1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    ms = g0.elapsed_time(g1) / K
-    # timed region 2 (stages): the same K steps with HIP events recorded on the
-    # launch stream at each kernel boundary; a fused kernel's time lands in the
-    # first slot of its group (the other slots of the group are not recorded)
-    hev = HipEvents()
+    return g0.elapsed_time(g1) / steps, wall / steps * 1e3
+
+
+def stage_table(cfg, kw, steps):
+    """Per-kernel times of the combined path: `steps` calls with HIP events
+    recorded on the launch stream at every kernel boundary (a fused kernel's
+    time lands in the first slot of its group; the other slots of the group are
+    not recorded).  -> (stages dict, dominant stage, its roofline dict, total
+    ms with events, algorithmic bytes of the layer)."""
+    return stage_table_enqueue(cfg, kw, steps)()
+
+
+def stage_table_enqueue(cfg, kw, steps, events=None):
+    """stage_table in two halves: this enqueues the calls and returns a
+    function that waits for them and computes the table, so that other GPU
+    work can be enqueued in between without the GPU going idle.  `events`:
+    the result of stage_events(cfg, steps), made beforehand (creating them
+    takes host time during which the GPU would idle)."""
+    from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
+    hev, evs, keep, fs, fc = events or stage_events(cfg, steps)
+    for _ in range(3):
+        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[0])
+    for i in range(steps):
+        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[i])
+    return lambda: _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc)
+
+
+def stage_events(cfg, steps):
+    """The HIP events of a stage_table pass of `steps` calls (host side only)."""
     import dataclasses
+    hev = HipEvents()
     icfg = dataclasses.replace(cfg, chunk_size=internal_chunk(cfg))
     fs, fc = states_is_fused(icfg), scan_is_fused(icfg)
     keep = [True, True, True, not fs, not fc, True]
-    evs = [[hev.new() if k else None for k in keep] for _ in range(K)]
-    for _ in range(3):
-        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[0])
-    torch.cuda.synchronize()
-    for i in range(K):
-        mamba_chunk_scan_combined_fwd(**kw, _stage_events=evs[i])
+    evs = [[hev.new() if k else None for k in keep] for _ in range(steps)]
+    return hev, evs, keep, fs, fc
+
+
+def _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc):
+    import numpy as np
+    import torch
     torch.cuda.synchronize()
 
     def slot(j):
@@ -493,11 +494,10 @@ def main(argv=None):
         a = max(x for x in range(j + 1) if keep[x])
         if not keep[j + 1]:
             return 0.0
-        return float(np.mean([hev.elapsed_ms(evs[i][a], evs[i][j + 1]) for i in range(K)]))
+        return float(np.mean([hev.elapsed_ms(evs[i][a], evs[i][j + 1]) for i in range(steps)]))
     slot_ms = [slot(j) for j in range(5)]
-    stages_ms_total = float(np.mean([hev.elapsed_ms(evs[i][0], evs[i][5]) for i in range(K)]))
-    work = stage_work(cfg, with_init=d["initial_states"] is not None)
-    # event slots: cumsum, chunk_state, state_passing, bmm_chunk, chunk_scan
+    total = float(np.mean([hev.elapsed_ms(evs[i][0], evs[i][5]) for i in range(steps)]))
+    work = stage_work(cfg, with_init=kw["initial_states"] is not None)
     slots = dict(zip(STAGES, slot_ms))
     stage_ms = {}
     if fs:
@@ -520,19 +520,124 @@ def main(argv=None):
     dom = max(stage_ms, key=lambda s: stage_ms[s])
     by, fl = work[dom]
     ridge = peak_mfma * 1e12 / (PEAK_HBM_GBS * 1e9)
-    bound = "mfma" if fl / by > ridge else "hbm"
-    if bound == "hbm":
-        roof = {"bound": "hbm", "achieved": stages[dom]["hbm_gbs"], "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": stages[dom]["hbm_frac"]}
-    else:
+    if fl / by > ridge:
         roof = {"bound": "mfma", "achieved": stages[dom]["mfma_tflops"], "peak": peak_mfma,
                 "unit": "TFLOP/s", "frac": stages[dom]["mfma_frac"]}
-    traffic = measured_traffic(args.config)
+    else:
+        roof = {"bound": "hbm", "achieved": stages[dom]["hbm_gbs"], "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": stages[dom]["hbm_frac"]}
     roof.update({"kernel": dom, "algorithmic_bytes": by, "algorithmic_flop": fl,
-                 "avg_launch_ms": stage_ms[dom], "traffic": traffic.get(dom)})
+                 "avg_launch_ms": stage_ms[dom]})
+    del hev
+    return stages, dom, roof, total, sum(w[0] for w in work.values())
+
+
+def bench_other_config(name, steps=50, warmup=20, cpu=True):
+    """One more BASELINE configuration measured in the same run: ms per layer,
+    tokens/s, the per-kernel table with its dominant kernel's roofline, and a
+    sampled CPU baseline."""
+    from mamba2_jax import configs
+    cfg = configs.CONFIGS[name]
+    kw = _layer_inputs(cfg)
+    # the event pass first (>= 300 steps): it brings the GPU back to its
+    # steady clocks after the host-side input generation
+    nev = max(steps, 300)
+    finish = stage_table_enqueue(cfg, kw, nev, stage_events(cfg, nev))
+    ms, _ = time_layer(kw, steps, warmup)
+    stages, dom, roof, _, tot_by = finish()
+    out = {"workload": f"{cfg.name} SSD layer forward ({name})", "dtype": cfg.dtype,
+           "batch": cfg.batch, "seq_len": cfg.seqlen, "nheads": cfg.nheads,
+           "ngroups": cfg.ngroups, "headdim": cfg.headdim, "dstate": cfg.dstate,
+           "chunk_size": cfg.chunk_size, "steps": steps, "warmup": warmup,
+           "ms_per_layer": ms, "tokens_per_s": cfg.tokens / (ms * 1e-3),
+           "layer_hbm_frac": tot_by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+           "roofline": roof, "stages": stages}
+    del kw
+    return out
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--config", default="c2")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other configurations (c0, c1, c3) and the c2 extras")
+    ap.add_argument("--cpu-heads", type=int, default=0,
+                    help="heads of the CPU baseline sample (0: all heads for c2)")
+    ap.add_argument("--ops", action="store_true",
+                    help="instead of the SSD layer: time the ops around it and the LM decode "
+                         "step (one JSON line)")
+    ap.add_argument("--lm", default="130m", help="LM shapes for --ops (comma list: 130m,2.7b)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="run one device copy of this many MiB first (HBM counter calibration)")
+    args = ap.parse_args(argv)
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}): "
+              "this build has no multi-GPU path; the SSD forward shards by head groups with no "
+              "communication, so per-GPU throughput is the one-GPU figure.", file=sys.stderr)
+        return 2
+
+    if args.ops:
+        print(json.dumps({"ops": bench_ops(tuple(x for x in args.lm.split(",") if x))}))
+        return 0
+
+    import torch
+    from mamba2_jax import configs
+
+    cfg = configs.CONFIGS[args.config]
+    dev = torch.device("cuda")
+    kw = _layer_inputs(cfg)
+    K = args.steps
+    nev = max(K, 300)
+    events = stage_events(cfg, nev)
+    res_extra = {}
+    # The other measurements run first and the headline follows them with no
+    # idle gap: besides their own figures they keep the GPU at its steady
+    # clocks, which an idle GPU drops (measured at the headline shape: 0.126 ms
+    # per layer after 5 warm-up steps on an idle GPU, 0.107 ms when busy).
+    if args.config == "c2" and not args.no_configs:
+        res_extra["configs"] = {c: bench_other_config(c) for c in ("c0", "c1", "c3")}
+        res_extra["fp32_same_shape"] = bench_fp32_same_shape(cfg)
+        res_extra["stage_operators"] = bench_stage_operators(cfg)
+    if not args.no_decode:
+        res_extra["decode"] = bench_decode()
+    if args.copy_mb:
+        # a plain copy of known size: reads and writes copy_mb MiB once each
+        src = torch.ones(args.copy_mb << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    # the per-kernel table: max(K, 300) steps with HIP events at kernel
+    # boundaries (~35 ms of the workload, which brings the GPU to its steady
+    # clocks); its events are read after the timed region, so the GPU does not
+    # idle between the two
+    finish = stage_table_enqueue(cfg, kw, nev, events)
+    # timed region (value): W warm-up steps, then K back-to-back steps
+    ms, wall_ms = time_layer(kw, K, args.warmup)
+    stages, dom, roof, stages_ms_total, tot_by = finish()
+    traffic = measured_traffic(args.config)
+    roof["traffic"] = traffic.get(dom)
     if traffic:
         roof["traffic_source"] = traffic.get("source")
-    tot_by = sum(w[0] for w in work.values())
     res = {
         "metric": METRIC, "value": cfg.tokens / (ms * 1e-3), "unit": "tokens/s",
         "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": ms,
@@ -542,20 +647,24 @@ def main(argv=None):
                    "batch": cfg.batch, "seq_len": cfg.seqlen, "nheads": cfg.nheads,
                    "ngroups": cfg.ngroups, "headdim": cfg.headdim, "dstate": cfg.dstate,
                    "chunk_size": cfg.chunk_size, "parallelism": "single-gpu"},
-        "ms_per_layer": ms, "wall_ms_per_step": wall / K * 1e3,
+        "ms_per_layer": ms, "wall_ms_per_step": wall_ms,
         "ms_per_layer_with_stage_events": stages_ms_total,
         "layer_hbm_frac": tot_by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
         "roofline": roof, "stages": stages,
         "reference_published": {"hardware": "H100", "dtype": "fp32", "pallas_ms": 0.94,
                                 "triton_ms": 0.69, "source": "reference README.md:35"},
     }
-    if args.config == "c2":
-        res["fp32_same_shape"] = bench_fp32_same_shape(cfg)
-        res["stage_operators"] = bench_stage_operators(cfg)
-    if not args.no_decode:
-        res["decode"] = bench_decode()
+    res.update(res_extra)
+    del kw
+    torch.cuda.synchronize()
+    # CPU baselines last (host only): the full c2 workload, bounded samples of the others
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(cfg, args.cpu_heads)
+        full = args.config == "c2" and args.cpu_heads == 0
+        res["cpu_baseline"] = cpu_baseline(cfg, cfg.nheads if full else (args.cpu_heads or 32))
+        for c, sample_heads in (("c0", 24), ("c1", 16), ("c3", 32)):
+            if c in res.get("configs", {}):
+                res["configs"][c]["cpu_baseline"] = cpu_baseline(configs.CONFIGS[c], sample_heads,
+                                                                 min_seconds=3.0)
     else:
         res["cpu_baseline"] = None
     print(json.dumps(res))

@@ -6,14 +6,16 @@
 //           previous chunk's (the previous id of chunk 0 is 0)
 // which are the chunk_state scale and the state_passing decay.
 //
-// One workgroup per (batch, chunk, block of 16 heads), 256 threads: thread
-// & 15 is a head, thread >> 4 one of 16 position segments of the chunk.  Each
-// thread loads its segment's dt (coalesced across the 16 heads: dt is
-// [b, L, H], so one head's positions are H elements apart), processes it
-// and sums it sequentially in registers; segment totals meet in
-// LDS and each thread adds the totals of the segments before it.  Outputs are
-// transposed through LDS so that each row [b, h, c, :] is written by
-// consecutive lanes.
+// One workgroup per (batch, chunk, block of 16 heads), 16 wavefronts.  The
+// chunk's dt rows for the 16 heads (32 contiguous bytes per position for
+// bf16) are loaded coalesced into an LDS tile [position][head]; then
+// wavefront w processes head w of the block alone: lane l takes positions
+// l, l + 64, ... (PPL = ceil(Q / 64) of them), processes dt, and the
+// chunk cumsum is a wavefront prefix scan (one per 64 positions, carried from
+// one to the next).  The outputs leave lanes-along-positions, so each store
+// instruction writes 256 contiguous bytes of a row [b, h, c, :].  A
+// wavefront thus runs a few dozen instructions per position batch instead of
+// a serial loop, and 16 wavefronts per CU hide each other's latencies.
 //
 // Follows reference kernels/chunk_cumsum_fwd.py:213-235 (bias -> softplus ->
 // clip -> zero pad) and ops/ssd_naive.py:67-68 (dA = dt' * A, then cumsum);
@@ -23,11 +25,9 @@
 
 namespace {
 
-constexpr int HB = 16;                 // heads per workgroup (256 workgroups at H 128, 32 chunks)
-constexpr int NSEG = 16;               // position segments per chunk
-constexpr int THREADS = HB * NSEG;
+constexpr int HB = 16;                 // heads per workgroup: one wavefront each
+constexpr int THREADS = HB * 64;
 constexpr int QMAX = 256;
-constexpr int TS = QMAX + 4;          // LDS tile row stride (16-byte rows)
 
 struct CumsumArgs {
     const void* dt;
@@ -42,107 +42,87 @@ struct CumsumArgs {
     float lo, hi;
 };
 
-// QS: positions per segment rounded up to a power of two (>= ceil(Q / 16)).
-// Every load is issued unconditionally (addresses clamped into the chunk's
-// valid range, results selected afterwards): loads under per-position
-// branches would each be waited for on their own.
-template <typename TD, int QS, bool VEC>
+// inclusive prefix sum over the 64 lanes of a wavefront
+M2_DEV float wave_scan(float v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_up(v, off, 64);
+        if (lane >= off) v += o;
+    }
+    return v;
+}
+
+// PPL: positions per lane (Q <= 64 PPL)
+template <typename TD, int PPL>
 __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
-    __shared__ float tot[NSEG][HB];
-    __shared__ __align__(16) float tile[3][HB][TS];
+    __shared__ float tile[QMAX][HB + 1];       // dt of the chunk, [position][head]
     // the head blocks of one (batch, chunk) read the same dt rows: they share
     // an XCD (and its L2)
     const int work = xcd_remap(blockIdx.x, a.nblocks);
     const int hb = work % a.nhb, c = (work / a.nhb) % a.nc, bi = work / (a.nhb * a.nc);
-    const int hh = threadIdx.x % HB, seg = threadIdx.x / HB;
-    const int h = hb * HB + hh;
-    const bool hok = h < a.H;
-    const int Q = a.Q, L = a.L;
-    const int qs = (Q + NSEG - 1) / NSEG;
-    const int q0 = seg * qs;
-    const int qe = min(q0 + qs, Q);                 // this segment: [q0, qe)
+    const int Q = a.Q, L = a.L, H = a.H;
     const int qhi = min(Q, L - c * Q);              // valid positions of the chunk
-    const int qv = min(qe, qhi);                    // valid positions of the segment: [q0, qv)
     const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
-    const TD* dtp = reinterpret_cast<const TD*>(a.dt) + tok0 * a.H + min(h, a.H - 1);
 
-    TD raw[QS];
-    int sq[QS];
+    // ---- coalesced tile load: thread t -> head t % 16, rows t / 16 + 64 i;
+    // addresses clamped into the valid rows / heads (masked below)
+    {
+        const int hh = threadIdx.x % HB, r0 = threadIdx.x / HB;
+        const TD* dtp = reinterpret_cast<const TD*>(a.dt) + tok0 * H + min(hb * HB + hh, H - 1);
+        TD raw[PPL];
 #pragma unroll
-    for (int j = 0; j < QS; ++j) raw[j] = dtp[(int64_t)min(q0 + j, qhi - 1) * a.H];
+        for (int i = 0; i < PPL; ++i) raw[i] = dtp[(int64_t)min(r0 + 64 * i, qhi - 1) * H];
+#pragma unroll
+        for (int i = 0; i < PPL; ++i)
+            if (r0 + 64 * i < Q) tile[r0 + 64 * i][hh] = to_f32(raw[i]);
+    }
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int h = hb * HB + w;
+    int sq[PPL];
     int se = 0, sprev = 0;
     if (a.seq) {
 #pragma unroll
-        for (int j = 0; j < QS; ++j) sq[j] = a.seq[tok0 + min(q0 + j, qhi - 1)];
+        for (int j = 0; j < PPL; ++j) sq[j] = a.seq[tok0 + min(lane + 64 * j, qhi - 1)];
         se = a.seq[tok0 + qhi - 1];
         if (c > 0) sprev = a.seq[tok0 - 1];
     }
-    const float Ah = a.A[min(h, a.H - 1)];
-    const float bias = a.bias ? a.bias[min(h, a.H - 1)] : 0.f;
+    const float Ah = a.A[min(h, H - 1)];
+    const float bias = a.bias ? a.bias[min(h, H - 1)] : 0.f;
+    __syncthreads();
+    if (h >= H) return;                             // no barrier follows
 
-    float v[QS], dA[QS];
-    float run = 0.f;
+    float v[PPL], dA[PPL];
+    float carry = 0.f;
 #pragma unroll
-    for (int j = 0; j < QS; ++j) {
-        float d = to_f32(raw[j]);
+    for (int j = 0; j < PPL; ++j) {
+        const int q = lane + 64 * j;
+        float d = q < Q ? tile[q][w] : 0.f;
         if (a.bias) d += bias;
         if (a.softplus) d = softplus_f(d);
         d = fminf(fmaxf(d, a.lo), a.hi);
-        v[j] = (hok && q0 + j < qv) ? d : 0.f;
-        run += v[j] * Ah;
-        dA[j] = run;
+        v[j] = q < qhi ? d : 0.f;
+        dA[j] = wave_scan(v[j] * Ah) + carry;
+        carry = __shfl(dA[j], 63, 64);
     }
-    tot[seg][hh] = run;
-    __syncthreads();
-    // totals summed in segment order: off + (last segment's total) is the
-    // same sum as `total`, so dA[Q - 1] == total exactly
-    float off = 0.f, total = 0.f;
+    const float total = carry;                      // == dA[Q - 1] exactly
+    float* const rowp = a.dA + (((int64_t)bi * H + h) * a.nc + c) * Q;
+    const int64_t off = rowp - a.dA;
 #pragma unroll
-    for (int k = 0; k < NSEG; ++k) {
-        const float t = tot[k][hh];
-        if (k < seg) off += t;
-        total += t;
-    }
-    // outputs go through LDS [head][position] so that the rows [b, h, c, :]
-    // are written by consecutive lanes (16 bytes per lane when VEC)
-    const int nout = a.wts ? 3 : 2;
-#pragma unroll
-    for (int j = 0; j < QS; ++j) {
-        const int q = q0 + j;
-        if (j < qs && q < qe) {
-            const float d = off + dA[j];
-            tile[0][hh][q] = d;
-            tile[1][hh][q] = v[j];
-            if (a.wts) {
-                float wv = expf(fminf(total - d, 0.f)) * v[j];
-                if (a.seq && (q >= qhi || se < 0 || sq[j] != se)) wv = 0.f;
-                tile[2][hh][q] = wv;
-            }
+    for (int j = 0; j < PPL; ++j) {
+        const int q = lane + 64 * j;
+        if (q >= Q) continue;
+        a.dA[off + q] = dA[j];
+        a.dto[off + q] = v[j];
+        if (a.wts) {
+            float wv = expf(fminf(total - dA[j], 0.f)) * v[j];
+            if (a.seq && (q >= qhi || se < 0 || sq[j] != se)) wv = 0.f;
+            a.wts[off + q] = wv;
         }
     }
-    __syncthreads();
-    float* outs[3] = {a.dA, a.dto, a.wts};
-    const int nh = min(HB, a.H - (int)hb * HB);
-    const int64_t row0 = (((int64_t)bi * a.H + hb * HB) * a.nc + c) * Q;
-    const int64_t hstride = (int64_t)a.nc * Q;       // between heads' rows
-    if (VEC) {
-        const int q4n = Q / 4;
-        for (int idx = threadIdx.x; idx < nout * nh * q4n; idx += THREADS) {
-            const int o = idx / (nh * q4n), rem = idx - o * (nh * q4n);
-            const int r = rem / q4n, q = 4 * (rem - r * q4n);
-            *reinterpret_cast<float4*>(outs[o] + row0 + r * hstride + q) =
-                *reinterpret_cast<const float4*>(&tile[o][r][q]);
-        }
-    } else {
-        for (int idx = threadIdx.x; idx < nout * nh * Q; idx += THREADS) {
-            const int o = idx / (nh * Q), rem = idx - o * (nh * Q);
-            const int r = rem / Q, q = rem - r * Q;
-            outs[o][row0 + r * hstride + q] = tile[o][r][q];
-        }
-    }
-    if (a.scl && seg == 0 && hok) {
+    if (a.scl && lane == 0) {
         const bool keep = !a.seq || se == sprev;
-        a.scl[((int64_t)bi * a.H + h) * a.nc + c] = keep ? expf(total) : 0.f;
+        a.scl[((int64_t)bi * H + h) * a.nc + c] = keep ? expf(total) : 0.f;
     }
 }
 
@@ -171,23 +151,13 @@ int launch_chunk_cumsum_ex(const m2_chunk_cumsum_args& a, const int32_t* seq_idx
     const dim3 grid((unsigned)nblocks);
     if (a.dt_dtype != M2_F32 && a.dt_dtype != M2_BF16)
         return set_error(M2_ERR_UNSUPPORTED, "chunk_cumsum: dt dtype %d", a.dt_dtype);
-    const int qs = (k.Q + NSEG - 1) / NSEG;
     const bool f32 = a.dt_dtype == M2_F32;
-    // 16-byte row stores need 16-byte aligned outputs and chunk_size % 4 == 0
-    const bool vec = k.Q % 4 == 0 && ((uintptr_t)k.dA % 16 == 0) && ((uintptr_t)k.dto % 16 == 0) &&
-                     ((uintptr_t)k.wts % 16 == 0);
-#define M2_CUMSUM_LAUNCH(QS)                                                          \
-    if (vec) {                                                                        \
-        if (f32) k_chunk_cumsum<float, QS, true><<<grid, THREADS, 0, s>>>(k);         \
-        else k_chunk_cumsum<bf16, QS, true><<<grid, THREADS, 0, s>>>(k);              \
-    } else {                                                                          \
-        if (f32) k_chunk_cumsum<float, QS, false><<<grid, THREADS, 0, s>>>(k);        \
-        else k_chunk_cumsum<bf16, QS, false><<<grid, THREADS, 0, s>>>(k);             \
-    }
-    if (qs <= 2) { M2_CUMSUM_LAUNCH(2) }
-    else if (qs <= 4) { M2_CUMSUM_LAUNCH(4) }
-    else if (qs <= 8) { M2_CUMSUM_LAUNCH(8) }
-    else { M2_CUMSUM_LAUNCH(16) }
+#define M2_CUMSUM_LAUNCH(PPL)                                                \
+    if (f32) k_chunk_cumsum<float, PPL><<<grid, THREADS, 0, s>>>(k);         \
+    else k_chunk_cumsum<bf16, PPL><<<grid, THREADS, 0, s>>>(k);
+    if (k.Q <= 64) { M2_CUMSUM_LAUNCH(1) }
+    else if (k.Q <= 128) { M2_CUMSUM_LAUNCH(2) }
+    else { M2_CUMSUM_LAUNCH(4) }
 #undef M2_CUMSUM_LAUNCH
     return check_launch("chunk_cumsum");
 }
