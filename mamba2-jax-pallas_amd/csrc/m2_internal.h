@@ -30,6 +30,30 @@ int launch_varlen_states(const m2_chunk_state_varlen_args& a, hipStream_t stream
 bool chunk_state_fast_supported(const m2_chunk_state_args& a);
 int launch_chunk_state_fast(const m2_chunk_state_args& a, hipStream_t stream);
 
+// Arguments of the fused bmm_chunk + chunk_scan kernels (one workgroup per
+// (batch, chunk, group, slice of the group's heads)).
+struct ScanFusedArgs {
+    const bf16* x;
+    const bf16* B;
+    const bf16* C;
+    const bf16* states;    // state entering each chunk, [b, nc, H, P, N]
+    const float* dt;       // [b, H, nc, Q]
+    const float* dA;       // [b, H, nc, Q]
+    const float* D;
+    const bf16* z;
+    const int32_t* seq_idx;
+    const void* cb;        // given CB [b, nc, G, Q, Q] (fp32 or bf16), or NULL: built here
+    float* out;
+    int D_has_hdim, cb_bf16;
+    int L, H, G, nc, hpg, nwork;
+    int hps, nslice;          // heads per workgroup (a slice of the group's), slices
+};
+// the chunk-128 scan kernel (csrc/ssd_scan128.hip) for dstate 32 * ns (ns 2, 4,
+// 8), with the z gate / with CB given; NULL for other sizes; its block size
+typedef void (*ScanKernel)(ScanFusedArgs);
+ScanKernel scan_q128_kernel(int ns, bool hasz, bool cbin);
+constexpr int SCAN_Q128_THREADS = 768;
+
 // fused bmm_chunk + chunk_scan of the combined forward (bf16 inputs)
 bool scan_fused_supported(int64_t headdim, int64_t dstate, int64_t chunk_size);
 bool scan_fused_cb_supported(const m2_chunk_scan_args& a);

@@ -80,22 +80,7 @@ M2_DEV float rbf(float v) { return (float)(bf16)v; }
 M2_DEV int xswz(int r) { return ((r >> 1) & 3) << 1; }
 template <int CPR> M2_DEV int sswz(int r) { return CPR == 8 ? ((r >> 1) & 7) : (r & 15); }
 
-struct ScanFusedArgs {
-    const bf16* x;
-    const bf16* B;
-    const bf16* C;
-    const bf16* states;    // state entering each chunk, [b, nc, H, P, N]
-    const float* dt;       // [b, H, nc, Q]
-    const float* dA;       // [b, H, nc, Q]
-    const float* D;
-    const bf16* z;
-    const int32_t* seq_idx;
-    const void* cb;        // given CB [b, nc, G, Q, Q] (fp32 or bf16), or NULL: built here
-    float* out;
-    int D_has_hdim, cb_bf16;
-    int L, H, G, nc, hpg, nwork;
-    int hps, nslice;          // heads per workgroup (a slice of the group's), slices
-};
+using m2::ScanFusedArgs;
 
 template <int NS, int QT, bool HASZ>
 struct Shape {
@@ -637,14 +622,16 @@ int launch_scan_fused_common(ScanFusedArgs& f, const Sizes& a, bool hz, bool cbi
     f.L = (int)a.seqlen; f.H = (int)a.nheads; f.G = (int)a.ngroups; f.nc = (int)nc;
     f.hpg = hpg; f.nwork = (int)nwork; f.hps = hps; f.nslice = nslice;
     void (*kern)(ScanFusedArgs) = nullptr;
+    // chunk 128: the kernel with per-wavefront compile-time unit lists
+    // (csrc/ssd_scan128.hip); chunk 64: k_scan_fused
+    if (a.chunk_size == 128 && a.dstate % 32 == 0) kern = m2::scan_q128_kernel((int)(a.dstate / 32), hz, cbin);
 #define M2_SF_CASE(NSV, QTV)                                                        \
     if (a.dstate == 32 * NSV && a.chunk_size == 16 * QTV)                           \
         kern = cbin ? k_scan_fused<NSV, QTV, false, true>                          \
                     : hz ? k_scan_fused<NSV, QTV, true, false> : k_scan_fused<NSV, QTV, false, false>;
-    M2_SF_CASE(2, 4) M2_SF_CASE(2, 8)
-    M2_SF_CASE(4, 4) M2_SF_CASE(4, 8)
-    M2_SF_CASE(8, 4) M2_SF_CASE(8, 8)
+    M2_SF_CASE(2, 4) M2_SF_CASE(4, 4) M2_SF_CASE(8, 4)
 #undef M2_SF_CASE
+    static_assert(THREADS == m2::SCAN_Q128_THREADS, "both scan kernels take the same block");
     M2_REQUIRE(kern && a.headdim == P, M2_ERR_UNSUPPORTED, "scan_fused: unsupported sizes");
     kern<<<(unsigned)nwork, THREADS, 0, s>>>(f);
     return m2::check_launch("scan_fused");
