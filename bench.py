@@ -545,6 +545,10 @@ def bench_other_config(name, steps=50, warmup=20, cpu=True):
     finish = stage_table_enqueue(cfg, kw, nev, stage_events(cfg, nev))
     ms, _ = time_layer(kw, steps, warmup)
     stages, dom, roof, _, tot_by = finish()
+    traffic = measured_traffic(name)
+    roof["traffic"] = traffic.get(dom)
+    if traffic:
+        roof["traffic_source"] = traffic.get("source")
     out = {"workload": f"{cfg.name} SSD layer forward ({name})", "dtype": cfg.dtype,
            "batch": cfg.batch, "seq_len": cfg.seqlen, "nheads": cfg.nheads,
            "ngroups": cfg.ngroups, "headdim": cfg.headdim, "dstate": cfg.dstate,
@@ -578,6 +582,10 @@ def main(argv=None):
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other configurations (c0, c1, c3) and the c2 extras")
+    ap.add_argument("--event-steps", type=int, default=300,
+                    help="steps of the per-kernel event pass (at least --steps)")
+    ap.add_argument("--stage-ops", action="store_true",
+                    help="instead of the layer: time each stage operator at --config (one JSON line)")
     ap.add_argument("--cpu-heads", type=int, default=0,
                     help="heads of the CPU baseline sample (0: all heads for c2)")
     ap.add_argument("--ops", action="store_true",
@@ -602,10 +610,13 @@ def main(argv=None):
     from mamba2_jax import configs
 
     cfg = configs.CONFIGS[args.config]
+    if args.stage_ops:
+        print(json.dumps({"stage_operators": bench_stage_operators(cfg), "config": args.config}))
+        return 0
     dev = torch.device("cuda")
     kw = _layer_inputs(cfg)
     K = args.steps
-    nev = max(K, 300)
+    nev = max(K, args.event_steps)
     events = stage_events(cfg, nev)
     res_extra = {}
     # The other measurements run first and the headline follows them with no
@@ -626,7 +637,7 @@ def main(argv=None):
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    # the per-kernel table: max(K, 300) steps with HIP events at kernel
+    # the per-kernel table: max(K, 300) steps (--event-steps) with HIP events at kernel
     # boundaries (~35 ms of the workload, which brings the GPU to its steady
     # clocks); its events are read after the timed region, so the GPU does not
     # idle between the two
