@@ -1,7 +1,9 @@
 // bmm_chunk: CB[b,c,g] = a_c @ b_c^T for every chunk c and group g
 // (Q x Q output, contraction over K = dstate).
 //
-// Both operands are K-contiguous in HBM ([.., L, G, K] rows), which is exactly
+// bf16 operands at the usual sizes take k_bmm_chunk_lds (one workgroup per
+// chunk and group, operands staged in LDS once).  Otherwise: both operands are
+// K-contiguous in HBM ([.., L, G, K] rows), which is exactly
 // the per-lane layout MFMA wants, so every fragment is one 16-byte global load
 // (bf16) straight into VGPRs -- no LDS round trip.  A workgroup owns a 64 x 64
 // tile of one (b, c, g) block (so that even a few chunks fill the CUs); each of
@@ -97,8 +99,112 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
     }
 }
 
+// One workgroup per (b, c, g) for bf16 operands whose two Q x K row blocks fit
+// in LDS: both blocks are loaded once (coalesced 16-byte loads, 16-byte chunks
+// XOR-swizzled by row so that the fragment reads of 16 rows at one chunk hit
+// distinct banks), then wavefront w computes row tiles w, w + 8, ... against
+// every column tile from LDS.  Every operand byte enters the CU once; the
+// tiled kernel above reads each row block several times (once per column
+// block, and the column rows once per wavefront).
+constexpr int LDS_THREADS = 512;
+template <typename TO, int QT, int KC>
+__global__ void __launch_bounds__(LDS_THREADS)
+k_bmm_chunk_lds(const bf16* __restrict__ a, const bf16* __restrict__ b,
+                const int32_t* __restrict__ seq_idx, TO* __restrict__ out, int L, int G, int nc,
+                int causal) {
+    constexpr int Q = 16 * QT, K = 8 * KC;                 // KC 16-byte chunks per row
+    __shared__ __align__(16) bf16 sa[Q * K], sb[Q * K];
+    __shared__ int seqs[Q];
+    const int work = blockIdx.x;
+    const int g = work % G, c = (work / G) % nc, bi = work / (G * nc);
+    const int64_t tbase = (int64_t)bi * L + (int64_t)c * Q;
+    const int valid = min(Q, L - c * Q);
+    // ---- both row blocks into LDS; rows past the end are zero
+    {
+        constexpr int NCH = Q * KC;                        // 16-byte chunks per block
+        for (int i = threadIdx.x; i < NCH; i += LDS_THREADS) {
+            const int r = i / KC, ch = i % KC;
+            const int so = r * K + 8 * (ch ^ (r & (KC - 1) & 15));
+            u32x4 va = {0u, 0u, 0u, 0u}, vb = {0u, 0u, 0u, 0u};
+            if (r < valid) {
+                const int64_t go = ((tbase + r) * G + g) * K + 8 * ch;
+                va = *reinterpret_cast<const u32x4*>(a + go);
+                vb = *reinterpret_cast<const u32x4*>(b + go);
+            }
+            *reinterpret_cast<u32x4*>(sa + so) = va;
+            *reinterpret_cast<u32x4*>(sb + so) = vb;
+        }
+        for (int q = threadIdx.x; q < Q; q += LDS_THREADS)
+            seqs[q] = (seq_idx && q < valid) ? seq_idx[tbase + q] : -1;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int ln = lane & 15, kg = lane >> 4;
+    TO* op = out + ((((int64_t)bi * nc + c) * G + g) * Q) * Q;
+    for (int rt = w; rt < QT; rt += LDS_THREADS / 64) {
+        const int row = 16 * rt + ln;                      // this lane's output row (a row)
+        f32x4 acc[QT];
+#pragma unroll
+        for (int ct = 0; ct < QT; ++ct) acc[ct] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KC / 4; ++ks) {
+            const int ch = 4 * ks + kg;
+            const bf16x8 af = *reinterpret_cast<const bf16x8*>(sa + row * K + 8 * (ch ^ (row & (KC - 1) & 15)));
+#pragma unroll
+            for (int ct = 0; ct < QT; ++ct) {
+                const int col = 16 * ct + ln;
+                const bf16x8 bf = *reinterpret_cast<const bf16x8*>(sb + col * K + 8 * (ch ^ (col & (KC - 1) & 15)));
+                // transposed product (A = b rows, B = a rows): lane (ln, kg)
+                // ends with row 16 rt + ln, columns 16 ct + 4 kg + i
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, af, acc[ct], 0, 0, 0);
+            }
+        }
+        const int srow = seqs[row];
+#pragma unroll
+        for (int ct = 0; ct < QT; ++ct) {
+            const int col0 = 16 * ct + 4 * kg;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int col = col0 + i;
+                v[i] = acc[ct][i];
+                if (causal && col > row) v[i] = 0.f;
+                if (seq_idx && srow != seqs[col]) v[i] = 0.f;
+            }
+            TO* dst = op + (int64_t)row * Q + col0;
+            if constexpr (sizeof(TO) == 4) {
+                *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                const bf16x4 o = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+                *reinterpret_cast<bf16x4*>(dst) = o;
+            }
+        }
+    }
+}
+
+template <typename TO>
+bool launch_lds(const m2_bmm_chunk_args& a, hipStream_t s) {
+    const int Q = (int)a.chunk_size, K = (int)a.k;
+    const int nc = (int)((a.seqlen + Q - 1) / Q);
+    const int64_t nblocks = a.batch * nc * a.ngroups;
+    if (nblocks >= (1ll << 31)) return false;
+    void (*kern)(const bf16*, const bf16*, const int32_t*, TO*, int, int, int, int) = nullptr;
+#define M2_BMML_CASE(QV, KV) if (Q == QV && K == KV) kern = k_bmm_chunk_lds<TO, QV / 16, KV / 8>;
+    M2_BMML_CASE(64, 64) M2_BMML_CASE(64, 128) M2_BMML_CASE(64, 256)
+    M2_BMML_CASE(128, 64) M2_BMML_CASE(128, 128) M2_BMML_CASE(128, 256)
+#undef M2_BMML_CASE
+    if (!kern) return false;
+    kern<<<(unsigned)nblocks, LDS_THREADS, 0, s>>>((const bf16*)a.a, (const bf16*)a.b, a.seq_idx,
+                                                    (TO*)a.out, (int)a.seqlen, (int)a.ngroups, nc,
+                                                    a.causal);
+    return true;
+}
+
 template <typename T, typename TO>
 int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
+    if constexpr (sizeof(T) == 2) {
+        if (launch_lds<TO>(a, s)) return m2::check_launch("bmm_chunk");
+    }
     const int Q = (int)a.chunk_size;
     const int nc = (int)((a.seqlen + Q - 1) / Q);
     const int rowblocks = (Q + 63) / 64;
