@@ -15,19 +15,20 @@
 // with q the positions of chunk c, [qlo, qhi) the part of s in it, and
 // states[c] the state entering chunk c.
 //
-// One workgroup per (chunk or sequence, head, 64-column dstate block): 8192
-// chunk states at the nemotron-h-8b shape, 6144 varlen states at the packed
-// 47b shape, several per CU, so a one-shot kernel hides its latency by
-// occupancy.  The x rows [Q x 64] and the block's B rows [Q x 64] arrive by
+// One workgroup per (chunk or sequence, head, NB-column dstate block), NB =
+// 128 when dstate allows (x then enters the CU once per 128 columns instead
+// of once per 64), else 64: 4096 chunk states at the nemotron-h-8b shape,
+// 3072 varlen states at the packed 47b shape, several per CU, so a one-shot
+// kernel hides its latency by occupancy.  The x rows [Q x 64] and the block's B rows [Q x 64] arrive by
 // direct global -> LDS loads (16-byte chunks of each 128-byte row
 // XOR-swizzled, so the transposed reads hit distinct banks); the weights are
 // computed from dA / dt while they are in flight.  Wavefront w owns head-dim
-// rows 16 w .. 16 w + 15 and all 64 columns (four 16 x 16 tiles): it computes
+// rows 16 w .. 16 w + 15 and all NB columns (NB / 16 tiles of 16 x 16): it computes
 // h^T[n, p] += B^T[n, q] (w x)[q, p] with MFMA operands read through the
 // gfx950 LDS transpose read, w x split into hi + lo bf16 parts (near-fp32
 // accuracy, as the reference's fp32 einsum).  The result goes through LDS so
-// that each output row of 64 fp32 (and its carry row) moves as 16 lanes x 16
-// bytes.
+// that each output row of NB fp32 (and its carry row) moves as NB / 4 lanes x
+// 16 bytes.
 //
 // Follows reference kernels/chunk_state_fwd.py:104-187 (product), :239-269
 // (weights, seq_idx rule) and :448-597 (varlen states).
@@ -37,18 +38,18 @@ namespace {
 
 constexpr int THREADS = 256;
 constexpr int P = 64;        // head dim
-constexpr int NB = 64;       // dstate columns per workgroup
-constexpr int CPR = 8;       // 16-byte chunks per 128-byte tile row
-constexpr int OS = NB + 4;   // output staging row stride (floats)
+constexpr int CPR = 8;       // 16-byte chunks per 128-byte x row
 
-// 16-byte chunk swizzle of tile row R (128-byte rows): 8 consecutive rows read
-// at one chunk pair land on disjoint banks.
-M2_DEV int swz(int R) { return ((R >> 1) & 3) << 1; }
+// 16-byte chunk swizzle of tile row R: for 128-byte rows (x, and B blocks of
+// 64 columns) 8 consecutive rows read at one chunk pair land on disjoint
+// banks; 256-byte rows (B blocks of 128 columns) start on the same bank, so
+// 8 consecutive rows are spread by their low bits.
+template <int RB> M2_DEV int swz(int R) { return RB == 128 ? ((R >> 1) & 3) << 1 : (R & 7) << 1; }
 
-// LDS bytes of the x and B tiles, which the output staging [64][OS] fp32
+// LDS bytes of the x and B tiles, which the output staging [64][NB + 4] fp32
 // later reuses
-__host__ __device__ inline int tiles_bytes(int Q) {
-    return Q * (P + NB) * 2 > P * OS * 4 ? Q * (P + NB) * 2 : P * OS * 4;
+__host__ __device__ inline int tiles_bytes(int Q, int NB) {
+    return Q * (P + NB) * 2 > P * (NB + 4) * 4 ? Q * (P + NB) * 2 : P * (NB + 4) * 4;
 }
 
 struct VarlenArgs {
@@ -63,14 +64,17 @@ struct VarlenArgs {
     int L, H, G, N, Q, nc, nblk, nwork, states_bf16;
 };
 
-template <bool CHUNK>
+template <bool CHUNK, int NB>
 __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
+    constexpr int OS = NB + 4;                                  // output staging row stride (floats)
+    constexpr int NT = NB / 16;                                 // 16-column tiles per wavefront
+    constexpr int BCPR = NB / 8;                                // 16-byte chunks per B row
     extern __shared__ __align__(16) char smem[];
     const int Q = a.Q, H = a.H, N = a.N;
     const int XB = Q * P * 2;                                   // x tile bytes
     char* xs = smem;                                            // [Q][64] bf16, then B
     float* ot = reinterpret_cast<float*>(smem);                 // [64][OS], after the tiles
-    float* wq = reinterpret_cast<float*>(smem + tiles_bytes(Q)); // [Q]
+    float* wq = reinterpret_cast<float*>(smem + tiles_bytes(Q, NB)); // [Q]
 
     const int work = xcd_remap(blockIdx.x, a.nwork);
     const int nb = work % a.nblk;
@@ -106,7 +110,7 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     }
 
     // ---- direct loads of the chunk's x rows and the block's B rows: load u
-    // (64 lanes x 16 bytes = 8 rows) goes to tile bytes [1024 u, 1024 u + 1024);
+    // (64 lanes x 16 bytes = 1 KB) goes to tile bytes [1024 u, 1024 u + 1024);
     // rows past the end of the batch row are clamped (their weight is 0)
     const int64_t t0 = (int64_t)bi * a.L + (int64_t)c * Q, tend = (int64_t)bi * a.L + a.L - 1;
     const bf16* xsrc = a.x + (int64_t)h * P;
@@ -115,22 +119,30 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     for (int u = w; u < Q * CPR / 64; u += THREADS / 64) {
         const int gi = 64 * u + lane, r = gi / CPR;
         const int64_t t = min(t0 + r, tend);
-        const int col = ((gi % CPR) ^ swz(r)) * 8;
+        const int col = ((gi % CPR) ^ swz<128>(r)) * 8;
         dma16(xsrc + t * H * P + col, xl + 1024 * u);
+    }
+    for (int u = w; u < Q * BCPR / 64; u += THREADS / 64) {
+        const int gi = 64 * u + lane, r = gi / BCPR;
+        const int64_t t = min(t0 + r, tend);
+        const int col = ((gi % BCPR) ^ swz<2 * NB>(r)) * 8;
         dma16(bsrc + t * a.G * N + col, xl + XB + 1024 * u);
     }
 
-    // ---- the carry rows of this lane's outputs (rows 16 w + 4 it + (lane >> 4),
-    // columns 4 (lane & 15) + i), loaded now so that their latency overlaps
-    // the tiles'
+    // ---- the carry rows of this lane's outputs (rows 16 w + RPI it + lane /
+    // (NB / 4), columns 4 (lane % (NB / 4)) + i), loaded now so that their
+    // latency overlaps the tiles'
+    constexpr int LPR = NB / 4;                       // lanes per output row
+    constexpr int RPI = 64 / LPR;                     // rows per store instruction
+    constexpr int NIT = 16 / RPI;
     const int64_t soff = (((int64_t)c * H + h) * P) * N + NB * nb;
-    const int orr = 16 * w + (lane >> 4), occ = 4 * (lane & 15);
-    bf16x4 cv16[4];
-    float4 cv32[4];
+    const int orr = 16 * w + lane / LPR, occ = 4 * (lane % LPR);
+    bf16x4 cv16[NIT];
+    float4 cv32[NIT];
     if (!CHUNK && carry) {
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int64_t e = soff + (int64_t)(orr + 4 * it) * N + occ;
+        for (int it = 0; it < NIT; ++it) {
+            const int64_t e = soff + (int64_t)(orr + RPI * it) * N + occ;
             if (a.states_bf16)
                 cv16[it] = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16*>(a.states) + e);
             else
@@ -159,17 +171,17 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     const int c1 = ln & 3;                            // 8-byte column group of the read
     const int cb = 8 * (c1 & 1);
     const int wpos = (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // k index ln & 7
-    const int xo0 = rA * (2 * P) + (((2 * w + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
-    const int xo1 = (rA + 16) * (2 * P) + (((2 * w + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
-    int bo0[4], bo1[4];
+    const int xo0 = rA * (2 * P) + (((2 * w + (c1 >> 1)) ^ swz<128>(rA)) * 16) + cb;
+    const int xo1 = (rA + 16) * (2 * P) + (((2 * w + (c1 >> 1)) ^ swz<128>(rA + 16)) * 16) + cb;
+    int bo0[NT], bo1[NT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
-        bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
+    for (int j = 0; j < NT; ++j) {
+        bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz<2 * NB>(rA)) * 16) + cb;
+        bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz<2 * NB>(rA + 16)) * 16) + cb;
     }
-    f32x4 acc[4];
+    f32x4 acc[NT];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = zero4();
+    for (int j = 0; j < NT; ++j) acc[j] = zero4();
     // the row swizzle repeats every 8 rows, so step ks is step 0 moved by 32 rows
     for (int ks = 0; ks < Q / 32; ++ks) {
         const float wl = wq[wpos + 32 * ks];
@@ -186,7 +198,7 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
             xlo[j] = (bf16)(v - (float)hi);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NT; ++j) {
             const bf16x4 b0 = ds_read_tr(xs + bo0[j] + ks * 32 * (2 * NB));
             const bf16x4 b1 = ds_read_tr(xs + bo1[j] + ks * 32 * (2 * NB));
             const bf16x8 bf = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
@@ -200,12 +212,12 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     lds_barrier();
     float* orow = ot + (16 * w) * OS;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NT; ++j)
         *reinterpret_cast<f32x4*>(orow + ln * OS + 16 * j + 4 * kg) = acc[j];
     const float cs = !CHUNK && carry ? expf(dA_ref) : 0.f;
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int r = orr + 4 * it;
+    for (int it = 0; it < NIT; ++it) {
+        const int r = orr + RPI * it;
         float4 v = *reinterpret_cast<const float4*>(ot + r * OS + occ);
         if (!CHUNK && carry) {
             float cv[4];
@@ -221,14 +233,19 @@ __global__ void __launch_bounds__(THREADS) k_varlen_states(VarlenArgs a) {
     }
 }
 
+// the dstate block width of a launch: 128 columns when dstate allows
+int block_cols(int64_t N) { return N % 128 == 0 ? 128 : 64; }
+
 template <bool CHUNK>
 int launch_k(const VarlenArgs& k, hipStream_t s, const char* who) {
-    const size_t shm = (size_t)tiles_bytes(k.Q) + (size_t)k.Q * 4;
+    const int NB = block_cols(k.N);
+    const size_t shm = (size_t)tiles_bytes(k.Q, NB) + (size_t)k.Q * 4;
+    void (*kern)(VarlenArgs) = NB == 128 ? k_varlen_states<CHUNK, 128> : k_varlen_states<CHUNK, 64>;
     if (shm > 65536 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k_varlen_states<CHUNK>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
         return m2::set_error(M2_ERR_LAUNCH, "%s: cannot reserve %zu B of LDS", who, shm);
-    k_varlen_states<CHUNK><<<(unsigned)k.nwork, THREADS, shm, s>>>(k);
+    kern<<<(unsigned)k.nwork, THREADS, shm, s>>>(k);
     return m2::check_launch(who);
 }
 
@@ -237,7 +254,7 @@ int launch_k(const VarlenArgs& k, hipStream_t s, const char* who) {
 namespace m2 {
 
 bool varlen_states_fast_supported(const m2_chunk_state_varlen_args& a) {
-    return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
+    return a.dtype == M2_BF16 && a.headdim == P && a.dstate % 64 == 0 &&
            a.chunk_size % 32 == 0 && a.chunk_size <= 256;
 }
 
@@ -249,7 +266,7 @@ int launch_varlen_states(const m2_chunk_state_varlen_args& a, hipStream_t s) {
     k.cu = a.cu_seqlens; k.states = a.chunk_states; k.out = a.out;
     k.states_bf16 = a.states_dtype == M2_BF16;
     k.L = (int)a.seqlen; k.H = (int)a.nheads; k.G = (int)a.ngroups; k.N = (int)a.dstate;
-    k.Q = (int)a.chunk_size; k.nc = (int)a.nchunks; k.nblk = (int)(a.dstate / NB);
+    k.Q = (int)a.chunk_size; k.nc = (int)a.nchunks; k.nblk = (int)(a.dstate / block_cols(a.dstate));
     const int64_t nwork = a.nseq * a.nheads * k.nblk;
     M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "varlen_states: too many workgroups");
     k.nwork = (int)nwork;
@@ -257,7 +274,7 @@ int launch_varlen_states(const m2_chunk_state_varlen_args& a, hipStream_t s) {
 }
 
 bool chunk_state_fast_supported(const m2_chunk_state_args& a) {
-    return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
+    return a.dtype == M2_BF16 && a.headdim == P && a.dstate % 64 == 0 &&
            a.chunk_size % 32 == 0 && a.chunk_size <= 256;
 }
 
@@ -269,7 +286,7 @@ int launch_chunk_state_fast(const m2_chunk_state_args& a, hipStream_t s) {
     k.seq = a.seq_idx; k.out = a.states;
     k.L = (int)a.seqlen; k.H = (int)a.nheads; k.G = (int)a.ngroups; k.N = (int)a.dstate;
     k.Q = (int)a.chunk_size; k.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
-    k.nblk = (int)(a.dstate / NB);
+    k.nblk = (int)(a.dstate / block_cols(a.dstate));
     const int64_t nwork = a.batch * k.nc * a.nheads * k.nblk;
     M2_REQUIRE(nwork < (1ll << 31) && a.batch * a.seqlen < (1ll << 31), M2_ERR_UNSUPPORTED,
                "chunk_state: too many workgroups");
