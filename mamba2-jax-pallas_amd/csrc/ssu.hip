@@ -8,8 +8,12 @@
 // workgroup per (batch, head), or per slice of its rows for small batches
 // (enough workgroups to fill the chip); each thread owns 4 consecutive n
 // (16-byte accesses) of RPT rows p, issuing all RPT state loads before any
-// arithmetic so that RPT x 16 B stay in flight per thread.  The readout over n is a
-// butterfly reduction across the N/4 lanes that share a row.
+// arithmetic so that RPT x 16 B stay in flight per thread.  The per-row
+// operands (dt', x, D x, silu(z)) of the workgroup's rows are loaded and
+// prepared into LDS while the state loads are in flight: vmcnt is one in-order
+// counter, so a small load issued per row after the state loads would cost a
+// memory round trip per row.  The readout over n is a butterfly reduction
+// across the N/4 lanes that share a row.
 //
 // Follows reference ops/selective_state_update.py:68-123.
 #include "m2_internal.h"
@@ -65,16 +69,33 @@ __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
         const int p = p0 + r * ROWS_PER_PASS + tr;
         if (p < P) s[r] = *reinterpret_cast<const float4*>(st + (int64_t)p * N + n0);
     }
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        const int p = p0 + r * ROWS_PER_PASS + tr;
-        if (p >= P) continue;
-        const int64_t hp = (int64_t)bh * P + p;       // (batch, head, p) index
+    // per-row operands of this workgroup's rows, while the state loads are in
+    // flight: one memory round trip for the workgroup instead of one per row
+    constexpr int NROWS = RPT * ROWS_PER_PASS;
+    __shared__ float sd[NROWS], sx[NROWS], sy0[NROWS], sz[NROWS];
+    for (int lr = threadIdx.x; lr < NROWS; lr += THREADS) {
+        const int p = min(p0 + lr, P - 1);
+        const int64_t hp = (int64_t)bh * P + p;
         float d = a.dt_has_hdim ? (a.dt_bf16 ? ld<bf16>(a.dt, hp) : ld<float>(a.dt, hp))
                                 : (a.dt_bf16 ? ld<bf16>(a.dt, bh) : ld<float>(a.dt, bh));
         if (a.dt_bias) d += a.bias_has_hdim ? a.dt_bias[h * P + p] : a.dt_bias[h];
         if (a.softplus) d = softplus_f(d);
         const float xv = ld<T>(a.x, hp);
+        sd[lr] = d;
+        sx[lr] = xv;
+        sy0[lr] = a.D ? (a.D_has_hdim ? a.D[h * P + p] : a.D[h]) * xv : 0.f;
+        // silu(z) in z's dtype, as the reference (ops/selective_state_update.py:121)
+        sz[lr] = a.z ? to_f32(from_f32<T>(silu_f(ld<T>(a.z, hp)))) : 1.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        const int p = p0 + r * ROWS_PER_PASS + tr;
+        if (p >= P) continue;
+        const int64_t hp = (int64_t)bh * P + p;       // (batch, head, p) index
+        const int lr = r * ROWS_PER_PASS + tr;
+        const float d = sd[lr];
+        const float xv = sx[lr];
         const float dx = d * xv;
         float v[4] = {s[r].x, s[r].y, s[r].z, s[r].w};
         float part = 0.f;
@@ -96,13 +117,7 @@ __global__ void __launch_bounds__(THREADS) k_ssu(SsuArgs a) {
         *reinterpret_cast<float4*>(nst + (int64_t)p * N + n0) = make_float4(v[0], v[1], v[2], v[3]);
 #pragma unroll
         for (int off = TPR / 2; off > 0; off >>= 1) part += __shfl_xor(part, off, TPR);
-        if (threadIdx.x % TPR == 0) {
-            float y = part;
-            if (a.D) y += (a.D_has_hdim ? a.D[h * P + p] : a.D[h]) * xv;
-            // silu(z) in z's dtype, as the reference (ops/selective_state_update.py:121)
-            if (a.z) y *= to_f32(from_f32<T>(silu_f(ld<T>(a.z, hp))));
-            a.out[hp] = y;
-        }
+        if (threadIdx.x % TPR == 0) a.out[hp] = (part + sy0[lr]) * sz[lr];
     }
 }
 
