@@ -6,6 +6,9 @@
 //
 // with the weights w[q] = exp(min(dA[last] - dA[q], 0)) dt'[q] and the decay
 // scl[c] = exp(dA[Q-1]) (seq_idx rules applied) precomputed by chunk_cumsum.
+// Two kernels: k_ssd_states (a head's 64-column dstate block per workgroup,
+// below) and k_ssd_pair (two heads of a group per workgroup, further down);
+// launch_states_fused picks one per shape.
 // The unfused stages write the fp32 chunk states S_c to HBM and read them
 // back; here the running state h stays in the MFMA accumulators of one
 // workgroup that walks the chunks of a (batch, head, 64-column dstate block) in
@@ -43,6 +46,9 @@
 //
 // Follows reference kernels/chunk_state_fwd.py:104-187 (product),
 // kernels/state_passing_fwd.py:108-151 (recurrence) and ops/ssd_naive.py:77-182.
+#include <stdlib.h>
+#include <string.h>
+
 #include "m2_internal.h"
 
 namespace {
@@ -311,6 +317,227 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
     }
 }
 
+// 16-byte chunk swizzle of a tile row R: 128-byte rows read at one chunk pair
+// by 8 consecutive rows, 256-byte rows likewise (each repeats every 8 rows)
+template <int RB> M2_DEV int rswz(int R) { return RB == 128 ? ((R >> 1) & 3) << 1 : (R & 7) << 1; }
+
+// ---------------------------------------------------------------------------
+// k_ssd_pair: the same pass with one workgroup per (batch, pair of heads of a
+// group, NB-column dstate block), for shapes with enough such workgroups to
+// fill the CUs.  A CU pulls at most ~16 bytes per clock from L2 / HBM, and
+// the pass is bound by that rate (with the compute wavefronts running, the
+// load wavefronts issue at ~10-14 bytes per clock): two heads share each B
+// row the CU brings in, and 128-column blocks bring x in once per 128
+// columns, so a pair moves 16 (NB 128) or 24 (NB 64) KB into the CU per head,
+// 64 columns and 128 positions, against 32 KB for the kernel above.
+// Compute wavefront w owns head (w >> 2) of the pair, head-dim rows
+// 16 (w & 3) .. +15 and all NB columns, and takes every position of a stage
+// (no position halves, so no exchange): each x element is weighted by one
+// wavefront, and the bf16 state entering a chunk is stored straight from the
+// accumulators.
+//
+// A slot holds the stage's x rows of both heads [KB x 2 P] (the heads are
+// adjacent in memory: 256 contiguous bytes per row), the B rows [KB x NB],
+// the heads' weights [2][KB] and their chunk decays.
+template <int NB, int KB>
+struct PairCfg {
+    static constexpr int HP = 2;
+    static constexpr int XROW = HP * P * 2, XCPR = XROW / 16;     // x row bytes, 16-byte chunks
+    static constexpr int BROW = NB * 2, BCPR = BROW / 16;
+    static constexpr int XB = KB * XROW, BB = KB * BROW;
+    static constexpr int AUXB = HP * KB * 4 + 256;
+    static constexpr int SLOT = XB + BB + AUXB;
+    static constexpr int DEPTH = 150 * 1024 / SLOT < 8 ? 150 * 1024 / SLOT : 8;
+    static constexpr int XL = XB / 1024 / NLOAD, BL = BB / 1024 / NLOAD;
+    static constexpr int KS = KB / 32;                            // K steps per stage
+    static constexpr int NT = NB / 16;                            // column tiles per wavefront
+    // loads of one load wavefront that may still be in flight when stage s is
+    // needed: DEPTH - 2 later stages (+ weights / decay for load wavefronts 0, 1)
+    static constexpr int WAIT01 = (DEPTH - 2) * (XL + BL + 1), WAIT23 = (DEPTH - 2) * (XL + BL);
+    static_assert(XB % (1024 * NLOAD) == 0 && BB % (1024 * NLOAD) == 0, "even load split");
+    static_assert(DEPTH >= 3 && WAIT01 <= 63, "ring depth / vmcnt range");
+    static_assert(HP * KB / 4 <= 64, "weights: one 16-byte load per lane");
+};
+
+template <int NB, int KB>
+__global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
+    typedef PairCfg<NB, KB> C;
+    constexpr int HP = C::HP;
+    constexpr int DEPTH = C::DEPTH, XB = C::XB, BB = C::BB, SLOT = C::SLOT, NT = C::NT;
+    __shared__ __align__(16) char ring[DEPTH * SLOT];
+
+    // work = head pair x nblk + column block: the column blocks of a pair and
+    // the pairs of a group, which read the same x and B rows, share an XCD
+    const int work = xcd_remap(blockIdx.x, a.nwork);
+    const int nb = work % a.nblk;
+    const int hq = work / a.nblk;                             // (b H + h0) / 2
+    const int H = a.H, L = a.L, Q = a.Q, nc = a.nc, N = a.N;
+    const int h0 = (hq * HP) % H, bi = (hq * HP) / H;
+    const int g = h0 / (H / a.G);
+    const int SPC = Q / KB;
+    const int NST = nc * SPC;                                 // stages
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int ln = lane & 15, kg = lane >> 4;
+
+    if (w >= NWAVES) {
+        // ---- the load wavefronts: stage i -> slot i % DEPTH.  Lane l of
+        // load u brings 16-byte chunk 64 u + l of the x / B tile (row, swizzled
+        // column); load wavefront li takes its XL x and BL B loads, wavefront 0
+        // also the heads' weights of the stage, wavefront 1 their chunk decays.
+        const bf16* xsrc = a.x + ((int64_t)bi * L * H + h0) * P;
+        const int64_t xstr = (int64_t)H * P;
+        const bf16* bsrc = a.B + ((int64_t)bi * L * a.G + g) * N + nb * NB;
+        const int64_t bstr = (int64_t)a.G * N;
+        const int64_t bhc = ((int64_t)bi * H + h0) * nc;
+        const uint32_t ring_lds = lds_addr(ring);
+        const int li = w - NWAVES;
+        auto issue = [&](int st, int k) {
+            const uint32_t sb = ring_lds + k * SLOT;
+#pragma unroll
+            for (int uu = 0; uu < C::XL; ++uu) {
+                const int u = li * C::XL + uu;
+                const int gi = 64 * u + lane, r = gi / C::XCPR;
+                const int64_t t = min(st * KB + r, L - 1);    // past the end: weight 0
+                dma16(xsrc + t * xstr + ((gi % C::XCPR) ^ rswz<C::XROW>(r)) * 8, sb + 1024 * u);
+            }
+#pragma unroll
+            for (int uu = 0; uu < C::BL; ++uu) {
+                const int u = li * C::BL + uu;
+                const int gi = 64 * u + lane, r = gi / C::BCPR;
+                const int64_t t = min(st * KB + r, L - 1);
+                dma16(bsrc + t * bstr + ((gi % C::BCPR) ^ rswz<C::BROW>(r)) * 8, sb + XB + 1024 * u);
+            }
+            const int c = st / SPC, off = (st - c * SPC) * KB;
+            if (li == 0 && lane < HP * KB / 4) {
+                const int hh = lane / (KB / 4), q = 4 * (lane % (KB / 4));
+                dma16(a.wts + (bhc + (int64_t)hh * nc + c) * Q + off + q, sb + XB + BB);
+            }
+            if (li == 1 && lane < HP) dma4(a.scl + bhc + (int64_t)lane * nc + c, sb + XB + BB + HP * KB * 4);
+        };
+#pragma unroll
+        for (int i = 0; i < DEPTH - 1; ++i) issue(min(i, NST - 1), i);
+        for (int i = 0; i < NST; ++i) {
+            // stage i complete (later stages may be in flight)
+            if (li < 2) wait_vmem<C::WAIT01>();
+            else wait_vmem<C::WAIT23>();
+            lds_barrier();               // slot i % DEPTH complete, slot (i-1) % DEPTH free
+            issue(min(i + DEPTH - 1, NST - 1), (i + DEPTH - 1) % DEPTH);
+        }
+        wait_vmem<0>();                  // the tail stages re-loaded into unused slots
+        return;
+    }
+
+    const int pw = w & 3, hh = w >> 2;
+    const int h = h0 + hh;
+    const int64_t hoff = ((int64_t)bi * H + h) * P * N;
+    const int64_t bhc = ((int64_t)bi * H + h) * nc;
+
+    // ---- running state h^T tiles: acc[j][i] = h[p][n], p = 16 pw + ln,
+    // n = NB nb + 16 j + 4 kg + i
+    f32x4 acc[NT];
+    const int prow = 16 * pw + ln;
+    const int ncol = NB * nb + 4 * kg;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        if (a.init) {
+            const float4 v = *reinterpret_cast<const float4*>(a.init + hoff + (int64_t)prow * N + ncol + 16 * j);
+            acc[j][0] = v.x; acc[j][1] = v.y; acc[j][2] = v.z; acc[j][3] = v.w;
+        } else {
+            acc[j] = zero4();
+        }
+    }
+    // this lane's part of the bf16 state [p][n] (8 bytes per tile) into passed[c]
+    auto store_state = [&](int c) {
+        bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + prow) * N + ncol;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+            typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+            const u2 v = {pk_bf16(acc[j][0], acc[j][1]), pk_bf16(acc[j][2], acc[j][3])};
+            *reinterpret_cast<u2*>(pp + 16 * j) = v;
+        }
+    };
+
+    // MFMA operand offsets.  K step ks covers stage rows 32 ks .. 32 ks + 31:
+    // MFMA k index j < 4 is row 32 ks + 4 kg + j, j >= 4 is 16 more; the row
+    // swizzles repeat every 8 rows, so step ks is step 0 moved by 32 rows.
+    // hT[n, p] += B^T[n, q] (w x)[q, p]: the lane reads B column n and x column
+    // p through the gfx950 LDS transpose read (4 rows per lane group).
+    const int rA = 4 * kg + (ln >> 2);
+    const int c1 = ln & 3;                           // 8-byte column group of the read
+    const int cb = 8 * (c1 & 1);
+    const int wpos = (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // row of k index ln & 7
+    const int xch = 8 * hh + 2 * pw + (c1 >> 1);     // 16-byte chunk of the x row
+    const int xo0 = rA * C::XROW + ((xch ^ rswz<C::XROW>(rA)) * 16) + cb;
+    const int xo1 = (rA + 16) * C::XROW + ((xch ^ rswz<C::XROW>(rA + 16)) * 16) + cb;
+    int bo0[NT], bo1[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        bo0[j] = XB + rA * C::BROW + (((2 * j + (c1 >> 1)) ^ rswz<C::BROW>(rA)) * 16) + cb;
+        bo1[j] = XB + (rA + 16) * C::BROW + (((2 * j + (c1 >> 1)) ^ rswz<C::BROW>(rA + 16)) * 16) + cb;
+    }
+    for (int s = 0; s < NST; ++s) {
+        const int c = s / SPC, kb = s - c * SPC;
+        const int i = s;
+        lds_barrier();                               // slot i % DEPTH complete
+        const char* slot = ring + (i % DEPTH) * SLOT;
+        const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
+        // every LDS operand of the stage is read first, so that the reads'
+        // latencies overlap
+        float wl[C::KS];
+        bf16x4 xa[C::KS], xb[C::KS], ba[C::KS][NT], bb[C::KS][NT];
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+            wl[ks] = aux[hh * KB + wpos + 32 * ks];
+            xa[ks] = ds_read_tr(slot + xo0 + ks * 32 * C::XROW);
+            xb[ks] = ds_read_tr(slot + xo1 + ks * 32 * C::XROW);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                ba[ks][j] = ds_read_tr(slot + bo0[j] + ks * 32 * C::BROW);
+                bb[ks][j] = ds_read_tr(slot + bo1[j] + ks * 32 * C::BROW);
+            }
+        }
+        if (kb == 0) {
+            // acc = h_c, the state entering chunk c; then h <- scl[c] h
+            const float sc = aux[HP * KB + hh];
+            store_state(c);
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[j][r] *= sc;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // acc += B^T (w x): w x split into packed bf16 hi / lo pairs (two MFMAs),
+        // so the weighted operand keeps near-fp32 accuracy
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+            const float w0 = wl[ks];
+            const float wv[8] = {row_bcast<0>(w0), row_bcast<1>(w0), row_bcast<2>(w0), row_bcast<3>(w0),
+                                 row_bcast<4>(w0), row_bcast<5>(w0), row_bcast<6>(w0), row_bcast<7>(w0)};
+            typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+            const u2 pa = __builtin_bit_cast(u2, xa[ks]), pb = __builtin_bit_cast(u2, xb[ks]);
+            uint32_t hi[4], lo[4];
+            split2(bf16_lo(pa[0]) * wv[0], bf16_hi(pa[0]) * wv[1], hi[0], lo[0]);
+            split2(bf16_lo(pa[1]) * wv[2], bf16_hi(pa[1]) * wv[3], hi[1], lo[1]);
+            split2(bf16_lo(pb[0]) * wv[4], bf16_hi(pb[0]) * wv[5], hi[2], lo[2]);
+            split2(bf16_lo(pb[1]) * wv[6], bf16_hi(pb[1]) * wv[7], hi[3], lo[3]);
+            const bf16x8 xh = as_bf16x8(hi[0], hi[1], hi[2], hi[3]), xl = as_bf16x8(lo[0], lo[1], lo[2], lo[3]);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const bf16x8 bf = __builtin_shufflevector(ba[ks][j], bb[ks][j], 0, 1, 2, 3, 4, 5, 6, 7);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
+            }
+        }
+    }
+
+    if (a.fin) {
+        float* fp = a.fin + hoff + (int64_t)prow * N + ncol;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+            *reinterpret_cast<float4*>(fp + 16 * j) = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+    }
+}
+
 }  // namespace
 
 namespace m2 {
@@ -319,6 +546,32 @@ bool states_fused_supported(const m2_ssd_combined_args& a) {
     return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
            a.chunk_size % 64 == 0 && a.chunk_size <= 256 && a.ngroups > 0 &&
            a.nheads % a.ngroups == 0;
+}
+
+// Work split of the pass (see k_ssd_pair): the time of a workgroup's chunk
+// (128 positions) measured with every CU busy at the BASELINE shapes (1.36 us
+// for a head in 64-column halves, 2.6 for a pair of heads x 64 columns, 4.0
+// for a pair x 128 columns), times the rounds of 256 workgroups (one per CU)
+// and the chunks.  M2_STATES_KERNEL (halves / pair64 / pair128) forces a split where
+// the shape allows it (tests).
+enum StatesSplit { SPLIT_HALVES, SPLIT_PAIR64, SPLIT_PAIR128 };
+
+StatesSplit states_split(const m2_ssd_combined_args& a) {
+    const bool pair = (a.nheads / a.ngroups) % 2 == 0 && a.chunk_size % 128 == 0;
+    const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
+    const int64_t bh = a.batch * a.nheads;
+    auto rounds = [](int64_t wg) { return (double)((wg + 255) / 256); };
+    const double t_halves = rounds(bh * (a.dstate / 64)) * nc * 1.36;
+    const double t_p64 = pair ? rounds(bh / 2 * (a.dstate / 64)) * nc * 2.6 : 1e30;
+    const double t_p128 = pair && a.dstate % 128 == 0 ? rounds(bh / 2 * (a.dstate / 128)) * nc * 4.0 : 1e30;
+    if (const char* e = getenv("M2_STATES_KERNEL")) {
+        if (!strcmp(e, "halves")) return SPLIT_HALVES;
+        if (!strcmp(e, "pair64") && t_p64 < 1e30) return SPLIT_PAIR64;
+        if (!strcmp(e, "pair128") && t_p128 < 1e30) return SPLIT_PAIR128;
+    }
+    if (t_p128 < t_halves && t_p128 <= t_p64) return SPLIT_PAIR128;
+    if (t_p64 < t_halves) return SPLIT_PAIR64;
+    return SPLIT_HALVES;
 }
 
 int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const float* scl,
@@ -330,11 +583,15 @@ int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const f
     sa.init = a.initial_states; sa.passed = (bf16*)passed; sa.fin = a.final_states;
     sa.L = (int)a.seqlen; sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.N = (int)a.dstate;
     sa.Q = (int)a.chunk_size; sa.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
-    sa.nblk = (int)(a.dstate / NB);
-    const int64_t nwork = a.batch * a.nheads * sa.nblk;
+    const StatesSplit sp = states_split(a);
+    const int nbw = sp == SPLIT_PAIR128 ? 128 : 64;
+    sa.nblk = (int)(a.dstate / nbw);
+    const int64_t nwork = a.batch * a.nheads / (sp == SPLIT_HALVES ? 1 : 2) * sa.nblk;
     M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "ssd_states: too many workgroups");
     sa.nwork = (int)nwork;
-    if (sa.Q % 128 == 0) k_ssd_states<128><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    if (sp == SPLIT_PAIR128) k_ssd_pair<128, 64><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    else if (sp == SPLIT_PAIR64) k_ssd_pair<64, 128><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    else if (sa.Q % 128 == 0) k_ssd_states<128><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
     else k_ssd_states<64><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
     return check_launch("ssd_states");
 }

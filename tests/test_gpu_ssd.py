@@ -205,3 +205,43 @@ def test_return_arity_and_dispatch():
     yn = _ssd_combined_fwd(use_pallas=False, chunk_size=64, **t)
     yh = _ssd_combined_fwd(use_pallas=True, chunk_size=64, **t)
     check(yh, host(yn), TOL["f32"], "hip vs naive")
+
+
+# The fused state pass splits its work one of three ways, chosen from the
+# shape (M2_STATES_KERNEL forces one where the shape allows it): a head in
+# 64-column halves, a pair of heads x 64 columns, a pair of heads x 128
+# columns.  Each must match the oracle with an initial state, ragged lengths,
+# batch > 1, sequence resets, dstate 64 / 128 / 256.
+_SPLIT_CASES = {
+    "init_b2": configs.SSDConfig("split", 2, 1024, 8, 2, 64, 128, 128, "bf16", init_state=True, seed=31),
+    "ragged": configs.SSDConfig("split", 1, 5 * 128 - 37, 16, 4, 64, 128, 128, "bf16", seed=32),
+    "n64_init": configs.SSDConfig("split", 1, 256, 8, 1, 64, 64, 128, "bf16", init_state=True, seed=33),
+    "seq_resets": configs.SSDConfig("split", 1, 1536, 8, 2, 64, 128, 128, "bf16", nseq=5, min_seqlen=100, seed=34),
+    "n256_init": configs.SSDConfig("split", 1, 768, 8, 2, 64, 256, 128, "bf16", init_state=True, seed=35),
+}
+
+
+@pytest.mark.parametrize("split", ["halves", "pair64", "pair128"])
+@pytest.mark.parametrize("case", sorted(_SPLIT_CASES))
+def test_state_pass_splits(case, split, monkeypatch):
+    announce("state-pass split", case, split)
+    monkeypatch.setenv("M2_STATES_KERNEL", split)
+    cfg = _SPLIT_CASES[case]
+    d = configs.make_ssd_inputs(cfg)
+    kw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True)
+    t = _dev_inputs(d, cfg.dtype)
+    t.pop("cu_seqlens")
+    got = mamba_chunk_scan_combined_fwd(**t, **kw)
+    d = dict(d, cu_seqlens=None)
+    want = O.ssd_combined(io_dtype=cfg.dtype, **d, **kw)
+    check(got[0], want[0], TOL[cfg.dtype], "out")
+    check(got[1], want[1], TOL[cfg.dtype], "final_states")
+
+
+@pytest.mark.parametrize("split", ["pair64", "pair128"])
+def test_state_pass_pair_splits_varlen(split, monkeypatch):
+    """Packed sequences through the pair splits: outputs, final and varlen states."""
+    announce("state-pass pair split, varlen", split)
+    monkeypatch.setenv("M2_STATES_KERNEL", split)
+    cfg = dataclasses.replace(configs.CONFIGS["c3"], seqlen=2048, nheads=32, min_seqlen=64)
+    _run_and_check(cfg, varlen=True)
