@@ -95,7 +95,8 @@ int record(void** ev, int i, hipStream_t s) {
 // same function of the inputs for every chunk size (the chunked algorithm is
 // exact; only the rounding points at chunk boundaries move).  bf16 chunks of
 // 256 run as chunks of 128 when that puts both halves of the layer on the
-// fused kernels (the fused scan keeps at most 128 positions of a chunk in LDS).
+// fused kernels (the fused scan keeps at most 128 positions of a chunk in
+// LDS); fp32 chunks of 256 always run as chunks of 128.
 m2_ssd_combined_args internal_args(const m2_ssd_combined_args& a0) {
     m2_ssd_combined_args a = a0;
     if (a0.dtype == M2_BF16 && a0.chunk_size == 256) {
@@ -103,6 +104,10 @@ m2_ssd_combined_args internal_args(const m2_ssd_combined_args& a0) {
         if (!m2::states_fused_supported(a) || !m2::scan_fused_supported(a.headdim, a.dstate, 128))
             a.chunk_size = 256;
     }
+    // fp32 has no rounding points at chunk boundaries: chunks of 128 give the
+    // same result up to fp32 summation order, with twice the workgroups and
+    // half the intra-chunk work
+    if (a0.dtype == M2_F32 && a0.chunk_size == 256) a.chunk_size = 128;
     return a;
 }
 

@@ -257,6 +257,266 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_chunk_scan_f32: the same computation for fp32 x / C / states, with every
+// fp32 operand split into bf16 hi + lo parts once, when it is staged, rather
+// than at each use: x goes to LDS transposed as two bf16 planes [P][Q] (8
+// consecutive positions of one head-dim column are one 16-byte read: the B
+// operand of the intra-chunk product), the carried state as two planes
+// [P][N]; a product of two split operands is three 16x16x32 bf16 MFMAs
+// (hi.hi + hi.lo + lo.hi, ~2^-16 relative).  The decay weights use the
+// hardware exp2.  One workgroup per (b, c, h), 8 wavefronts, snake tile order
+// (two heads per workgroup, sharing the C / CB fragments, measured slower:
+// half the workgroups, one per CU).
+// ---------------------------------------------------------------------------
+constexpr float LOG2E = 1.4426950408889634f;
+
+// padded row lengths (bf16 elements) of the planes: rows 16 bytes apart in
+// the bank map, so 16 lanes reading one 16-byte column of 16 rows hit
+// distinct banks
+__host__ __device__ inline int f32_xrow(int Q) { return Q + 8; }
+__host__ __device__ inline int f32_srow(int N) { return N + 8; }
+__host__ __device__ inline size_t f32_scan_lds(int Q, int P, int N) {
+    return (size_t)2 * P * f32_xrow(Q) * 2 + (size_t)2 * P * f32_srow(N) * 2 + (size_t)Q * 3 * 4;
+}
+
+M2_DEV f32x4 mma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, const bf16x8& bl, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+}
+// 8 floats as bf16 hi / lo parts
+M2_DEV void split8(const float* v, bf16x8& hi, bf16x8& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) split2(v[2 * i], v[2 * i + 1], h[i], l[i]);
+    hi = as_bf16x8(h[0], h[1], h[2], h[3]);
+    lo = as_bf16x8(l[0], l[1], l[2], l[3]);
+}
+
+template <int PT, int NS, int QT, typename TCB>
+__global__ void __launch_bounds__(THREADS, 4) k_chunk_scan_f32(ScanArgs a) {
+    // NS: dstate / 32, QT: chunk / 32 (compile-time, so every load of a stage
+    // is issued before the first of them is used)
+    extern __shared__ __align__(16) char smem[];
+    constexpr int P = PT * 16;
+    constexpr int Q = 32 * QT, N = 32 * NS;
+    const int L = a.L, H = a.H, nc = a.nc;
+    constexpr int XR = Q + 8, SR = N + 8;
+    bf16* xh = reinterpret_cast<bf16*>(smem);            // [P][XR]: x^T hi
+    bf16* xl = xh + P * XR;                              // [P][XR]: x^T lo
+    bf16* sh = xl + P * XR;                              // [P][SR]: state hi
+    bf16* sl = sh + P * SR;                              // [P][SR]: state lo
+    float* dAs = reinterpret_cast<float*>(sl + P * SR);  // [Q]
+    float* dts = dAs + Q;                                // [Q]
+    int* seqs = reinterpret_cast<int*>(dts + Q);         // [Q] (seq_idx only)
+
+    const int work = xcd_remap(blockIdx.x, a.nblocks);
+    const int h = work % H;
+    const int rest = work / H;
+    const int c = rest % nc;
+    const int bi = rest / nc;
+    const int g = h / (H / a.G);
+    const int valid = min(Q, L - c * Q);
+    const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
+
+    // --- stage dA, dt, seq_idx; x and the carried state as hi / lo planes ---
+    const int64_t cq = (((int64_t)bi * H + h) * nc + c) * Q;
+    int seq_prev = 0;
+    if (a.seq_idx && c > 0) seq_prev = a.seq_idx[tok0 - 1];
+    for (int q = threadIdx.x; q < Q; q += THREADS) {
+        dAs[q] = a.dA[cq + q];
+        dts[q] = a.dt[cq + q];
+        if (a.seq_idx) seqs[q] = q < valid ? a.seq_idx[tok0 + q] : -1;
+    }
+    {
+        // x[r][4 v .. 4 v + 3] -> column entries (4 v + i, r) of both planes
+        const float* xsrc = reinterpret_cast<const float*>(a.x) + (tok0 * H + h) * P;
+        constexpr int VPR = P / 4, XI = Q * VPR / THREADS;
+        static_assert(Q * VPR % THREADS == 0 && P * (N / 4) % THREADS == 0, "even staging split");
+        float4 xf[XI];
+#pragma unroll
+        for (int it = 0; it < XI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, r = idx / VPR, v = idx % VPR;
+            xf[it] = *reinterpret_cast<const float4*>(xsrc + (int64_t)min(r, valid - 1) * H * P + 4 * v);
+        }
+        constexpr int VS = N / 4, SI = P * VS / THREADS;
+        const int64_t soff = (((int64_t)bi * nc + c) * H + h) * (int64_t)P * N;
+        float sv[SI][4];
+#pragma unroll
+        for (int it = 0; it < SI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, r = idx / VS, v = idx % VS;
+            if (a.states_bf16) {
+                const bf16x4 b4 = *reinterpret_cast<const bf16x4*>(reinterpret_cast<const bf16*>(a.states) + soff + (int64_t)r * N + 4 * v);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sv[it][i] = (float)b4[i];
+            } else {
+                const float4 f = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.states) + soff + (int64_t)r * N + 4 * v);
+                sv[it][0] = f.x; sv[it][1] = f.y; sv[it][2] = f.z; sv[it][3] = f.w;
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < XI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, r = idx / VPR, v = idx % VPR;
+            const float4 f = r < valid ? xf[it] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bf16 hv = (bf16)fv[i];
+                xh[(4 * v + i) * XR + r] = hv;
+                xl[(4 * v + i) * XR + r] = (bf16)(fv[i] - (float)hv);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < SI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, r = idx / VS, v = idx % VS;
+            uint32_t h01, l01, h23, l23;
+            split2(sv[it][0], sv[it][1], h01, l01);
+            split2(sv[it][2], sv[it][3], h23, l23);
+            typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+            *reinterpret_cast<u2*>(sh + r * SR + 4 * v) = u2{h01, h23};
+            *reinterpret_cast<u2*>(sl + r * SR + 4 * v) = u2{l01, l23};
+        }
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int ln = lane & 15, kg = lane >> 4;
+    const float* Cbase = reinterpret_cast<const float*>(a.C) + (tok0 * a.G + g) * N;
+    const TCB* cbbase = reinterpret_cast<const TCB*>(a.cb) + (((int64_t)bi * nc + c) * a.G + g) * (int64_t)Q * Q;
+    const bf16x8 zero8 = as_bf16x8(0u, 0u, 0u, 0u);
+    const int ntiles = Q / 16;
+    for (int r = 0;; ++r) {
+        const int t = r * NW + ((r & 1) ? (NW - 1 - w) : w);
+        if (t >= ntiles) break;
+        const int m0 = t * 16;
+        const int m = m0 + ln;
+        f32x4 acc[PT];
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt) acc[pt] = zero4();
+
+        // 1. carried state: C[m, :] @ state^T (C split as its rows arrive)
+        {
+            const bool mok = m < valid;
+            const float* crow = Cbase + (int64_t)min(m, valid - 1) * a.G * N + kg * 8;
+            constexpr int NS4 = NS < 4 ? NS : 4;             // C loads in flight together
+#pragma unroll
+            for (int ks0 = 0; ks0 < NS; ks0 += NS4) {
+            float4 cf[NS4][2];
+#pragma unroll
+            for (int u = 0; u < NS4; ++u) {
+                cf[u][0] = *reinterpret_cast<const float4*>(crow + 32 * (ks0 + u));
+                cf[u][1] = *reinterpret_cast<const float4*>(crow + 32 * (ks0 + u) + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < NS4; ++u) {
+                const int ks = ks0 + u;
+                __builtin_amdgcn_sched_barrier(0);           // one k-step's operands live at a time
+                const float cv[8] = {cf[u][0].x, cf[u][0].y, cf[u][0].z, cf[u][0].w,
+                                     cf[u][1].x, cf[u][1].y, cf[u][1].z, cf[u][1].w};
+                bf16x8 ch, cl;
+                split8(cv, ch, cl);
+                if (!mok) { ch = zero8; cl = zero8; }
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) {
+                    const int pr = pt * 16 + ln;
+                    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(sh + pr * SR + 32 * ks + kg * 8);
+                    const bf16x8 bl = *reinterpret_cast<const bf16x8*>(sl + pr * SR + 32 * ks + kg * 8);
+                    acc[pt] = mma3(ch, cl, bh, bl, acc[pt]);
+                }
+            }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int mr = m0 + kg * 4 + i;
+                float f = __builtin_amdgcn_exp2f(dAs[mr] * LOG2E);
+                if (a.seq_idx && seqs[mr] != seq_prev) f = 0.f;
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) acc[pt][i] *= f;
+            }
+        }
+
+        // 2. intra-chunk: (cb o decay o dt)[m, k <= m] @ x[k, :], the weights
+        // split into hi / lo, x from the transposed planes
+        {
+            const float dAm = dAs[m];
+            const TCB* cbrow = cbbase + (int64_t)m * Q;
+            const int nks = (m0 + 16 + 31) / 32;             // k-steps up to the diagonal
+            constexpr int KB4 = QT < 4 ? QT : 4;             // CB loads in flight together
+            for (int ks0 = 0; ks0 < nks; ks0 += KB4) {
+            float cbv[KB4][8];
+#pragma unroll
+            for (int u = 0; u < KB4; ++u)
+                if (ks0 + u < nks) load_cb<8>(cbrow + 32 * (ks0 + u) + kg * 8, cbv[u]);
+#pragma unroll
+            for (int u = 0; u < KB4; ++u) {
+                const int ks = ks0 + u;
+                if (ks >= nks) break;
+                __builtin_amdgcn_sched_barrier(0);           // one k-step's operands live at a time
+                const int kb = 32 * ks + kg * 8;
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int k = kb + j;
+                    v[j] = k <= m ? cbv[u][j] * __builtin_amdgcn_exp2f((dAm - dAs[k]) * LOG2E) * dts[k] : 0.f;
+                }
+                bf16x8 wh, wl;
+                split8(v, wh, wl);
+#pragma unroll
+                for (int pt = 0; pt < PT; ++pt) {
+                    const int pr = pt * 16 + ln;
+                    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(xh + pr * XR + kb);
+                    const bf16x8 bl = *reinterpret_cast<const bf16x8*>(xl + pr * XR + kb);
+                    acc[pt] = mma3(wh, wl, bh, bl, acc[pt]);
+                }
+            }
+            }
+        }
+
+        // 3. epilogue: + D x, out_x, z gate, store
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt) {
+            const int p = pt * 16 + ln;
+            const float dv = a.D ? (a.D_has_hdim ? a.D[h * P + p] : a.D[h]) : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int mr = m0 + kg * 4 + i;
+                if (mr >= valid) continue;
+                float v = acc[pt][i];
+                if (a.D) v += dv * ((float)xh[p * XR + mr] + (float)xl[p * XR + mr]);
+                const int64_t o = ((tok0 + mr) * H + h) * (int64_t)P + p;
+                if (a.out_x) a.out_x[o] = v;
+                if (a.z) v *= silu_f(reinterpret_cast<const float*>(a.z)[o]);
+                a.out[o] = v;
+            }
+        }
+    }
+}
+
+// compile-time chunk 64 / 128 / 256, dstate 64 / 128 / 256 (others: the
+// generic kernel)
+template <typename TCB>
+int launch_f32(const ScanArgs& sa, hipStream_t s) {
+    const size_t shm = f32_scan_lds(sa.Q, sa.P, sa.N);
+    void (*kern)(ScanArgs) = nullptr;
+#define M2_F32_SCAN(PTV, NSV, QTV) \
+    if (sa.P == 16 * PTV && sa.N == 32 * NSV && sa.Q == 32 * QTV) kern = k_chunk_scan_f32<PTV, NSV, QTV, TCB>;
+    M2_F32_SCAN(2, 2, 2) M2_F32_SCAN(2, 4, 2) M2_F32_SCAN(2, 8, 2)
+    M2_F32_SCAN(2, 2, 4) M2_F32_SCAN(2, 4, 4) M2_F32_SCAN(2, 8, 4)
+    M2_F32_SCAN(2, 2, 8) M2_F32_SCAN(2, 4, 8) M2_F32_SCAN(2, 8, 8)
+    M2_F32_SCAN(4, 2, 2) M2_F32_SCAN(4, 4, 2) M2_F32_SCAN(4, 8, 2)
+    M2_F32_SCAN(4, 2, 4) M2_F32_SCAN(4, 4, 4) M2_F32_SCAN(4, 8, 4)
+    M2_F32_SCAN(4, 2, 8) M2_F32_SCAN(4, 4, 8) M2_F32_SCAN(4, 8, 8)
+#undef M2_F32_SCAN
+    if (!kern) return M2_ERR_UNSUPPORTED;
+    if (shm > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return m2::set_error(M2_ERR_LAUNCH, "chunk_scan: cannot reserve %zu B of LDS", shm);
+    kern<<<(unsigned)sa.nblocks, THREADS, shm, s>>>(sa);
+    return m2::check_launch("chunk_scan");
+}
+
 template <typename T, typename TCB>
 int launch_typed(const ScanArgs& sa, hipStream_t s) {
     const size_t shm = (size_t)sa.Q * (sa.P + ScanPad<T>::x) * sizeof(T) +
@@ -314,6 +574,12 @@ int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t s) {
         if (a.cb_dtype == M2_BF16) return launch_typed<bf16, bf16>(sa, s);
     } else if (a.dtype == M2_F32) {
         M2_REQUIRE(a.dstate % 32 == 0, M2_ERR_UNSUPPORTED, "chunk_scan: f32 needs dstate %% 32 == 0");
+        // split planes when they fit (head dim 32 / 64): x, C and states fp32
+        if (sa.P <= 64 && sa.states_same && f32_scan_lds(sa.Q, sa.P, sa.N) <= 160 * 1024) {
+            const int rc = a.cb_dtype == M2_F32 ? launch_f32<float>(sa, s)
+                         : a.cb_dtype == M2_BF16 ? launch_f32<bf16>(sa, s) : M2_ERR_UNSUPPORTED;
+            if (rc != M2_ERR_UNSUPPORTED) return rc;
+        }
         if (a.cb_dtype == M2_F32) return launch_typed<float, float>(sa, s);
         if (a.cb_dtype == M2_BF16) return launch_typed<float, bf16>(sa, s);
     }
