@@ -258,11 +258,12 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// k_chunk_scan_f32: the same computation for fp32 x / C / states, with every
-// fp32 operand split into bf16 hi + lo parts once, when it is staged, rather
-// than at each use: x goes to LDS transposed as two bf16 planes [P][Q] (8
-// consecutive positions of one head-dim column are one 16-byte read: the B
-// operand of the intra-chunk product), the carried state as two planes
+// k_chunk_scan_f32: the same computation for fp32 x / C / states (head dim
+// 64), with every fp32 operand split into bf16 hi + lo parts once, when it is
+// staged, rather than at each use: x goes to LDS as two row-major bf16
+// planes [Q][64] with XOR-swizzled 16-byte chunks, whose columns (8 positions
+// of one head-dim column: the B operand of the intra-chunk product) come
+// through the gfx950 LDS transpose read, and the carried state as two planes
 // [P][N]; a product of two split operands is three 16x16x32 bf16 MFMAs
 // (hi.hi + hi.lo + lo.hi, ~2^-16 relative).  The decay weights use the
 // hardware exp2.  One workgroup per (b, c, h), 8 wavefronts, snake tile order
@@ -274,11 +275,13 @@ constexpr float LOG2E = 1.4426950408889634f;
 // padded row lengths (bf16 elements) of the planes: rows 16 bytes apart in
 // the bank map, so 16 lanes reading one 16-byte column of 16 rows hit
 // distinct banks
-__host__ __device__ inline int f32_xrow(int Q) { return Q + 8; }
 __host__ __device__ inline int f32_srow(int N) { return N + 8; }
 __host__ __device__ inline size_t f32_scan_lds(int Q, int P, int N) {
-    return (size_t)2 * P * f32_xrow(Q) * 2 + (size_t)2 * P * f32_srow(N) * 2 + (size_t)Q * 3 * 4;
+    return (size_t)2 * Q * P * 2 + (size_t)2 * P * f32_srow(N) * 2 + (size_t)Q * 3 * 4;
 }
+// 16-byte chunk swizzle of an x plane row R (128-byte rows, head dim 64): the
+// 8 rows of a transpose read at one chunk pair land on distinct banks
+M2_DEV int xpswz(int R) { return ((R >> 1) & 3) << 1; }
 
 M2_DEV f32x4 mma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, const bf16x8& bl, f32x4 c) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
@@ -301,11 +304,12 @@ __global__ void __launch_bounds__(THREADS, 4) k_chunk_scan_f32(ScanArgs a) {
     extern __shared__ __align__(16) char smem[];
     constexpr int P = PT * 16;
     constexpr int Q = 32 * QT, N = 32 * NS;
+    static_assert(P == 64, "x planes: 128-byte rows");
     const int L = a.L, H = a.H, nc = a.nc;
-    constexpr int XR = Q + 8, SR = N + 8;
-    bf16* xh = reinterpret_cast<bf16*>(smem);            // [P][XR]: x^T hi
-    bf16* xl = xh + P * XR;                              // [P][XR]: x^T lo
-    bf16* sh = xl + P * XR;                              // [P][SR]: state hi
+    constexpr int XROW = P * 2, SR = N + 8;
+    char* xh = smem;                                     // [Q] rows of XROW: x hi
+    char* xl = xh + Q * XROW;                            // x lo
+    bf16* sh = reinterpret_cast<bf16*>(xl + Q * XROW);   // [P][SR]: state hi
     bf16* sl = sh + P * SR;                              // [P][SR]: state lo
     float* dAs = reinterpret_cast<float*>(sl + P * SR);  // [Q]
     float* dts = dAs + Q;                                // [Q]
@@ -330,7 +334,7 @@ __global__ void __launch_bounds__(THREADS, 4) k_chunk_scan_f32(ScanArgs a) {
         if (a.seq_idx) seqs[q] = q < valid ? a.seq_idx[tok0 + q] : -1;
     }
     {
-        // x[r][4 v .. 4 v + 3] -> column entries (4 v + i, r) of both planes
+        // x[r][4 v .. 4 v + 3] -> an 8-byte half of a swizzled chunk of row r
         const float* xsrc = reinterpret_cast<const float*>(a.x) + (tok0 * H + h) * P;
         constexpr int VPR = P / 4, XI = Q * VPR / THREADS;
         static_assert(Q * VPR % THREADS == 0 && P * (N / 4) % THREADS == 0, "even staging split");
@@ -359,13 +363,13 @@ __global__ void __launch_bounds__(THREADS, 4) k_chunk_scan_f32(ScanArgs a) {
         for (int it = 0; it < XI; ++it) {
             const int idx = threadIdx.x + it * THREADS, r = idx / VPR, v = idx % VPR;
             const float4 f = r < valid ? xf[it] : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float fv[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bf16 hv = (bf16)fv[i];
-                xh[(4 * v + i) * XR + r] = hv;
-                xl[(4 * v + i) * XR + r] = (bf16)(fv[i] - (float)hv);
-            }
+            uint32_t h01, l01, h23, l23;
+            split2(f.x, f.y, h01, l01);
+            split2(f.z, f.w, h23, l23);
+            typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+            const int off = r * XROW + (((v >> 1) ^ xpswz(r)) * 16) + 8 * (v & 1);
+            *reinterpret_cast<u2*>(xh + off) = u2{h01, h23};
+            *reinterpret_cast<u2*>(xl + off) = u2{l01, l23};
         }
 #pragma unroll
         for (int it = 0; it < SI; ++it) {
@@ -437,36 +441,47 @@ __global__ void __launch_bounds__(THREADS, 4) k_chunk_scan_f32(ScanArgs a) {
         }
 
         // 2. intra-chunk: (cb o decay o dt)[m, k <= m] @ x[k, :], the weights
-        // split into hi / lo, x from the transposed planes
+        // split into hi / lo.  In K step ks, MFMA k index j < 4 is position
+        // 32 ks + 4 kg + j and j >= 4 is 16 more: the rows the transpose read
+        // of the x planes gives this lane group
         {
             const float dAm = dAs[m];
             const TCB* cbrow = cbbase + (int64_t)m * Q;
             const int nks = (m0 + 16 + 31) / 32;             // k-steps up to the diagonal
+            const int rA = 4 * kg + (ln >> 2), c1 = ln & 3;
+            int xo[PT];
+#pragma unroll
+            for (int pt = 0; pt < PT; ++pt)
+                xo[pt] = rA * XROW + (((2 * pt + (c1 >> 1)) ^ xpswz(rA)) * 16) + 8 * (c1 & 1);
             constexpr int KB4 = QT < 4 ? QT : 4;             // CB loads in flight together
             for (int ks0 = 0; ks0 < nks; ks0 += KB4) {
             float cbv[KB4][8];
 #pragma unroll
             for (int u = 0; u < KB4; ++u)
-                if (ks0 + u < nks) load_cb<8>(cbrow + 32 * (ks0 + u) + kg * 8, cbv[u]);
+                if (ks0 + u < nks) {
+                    load_cb<4>(cbrow + 32 * (ks0 + u) + 4 * kg, cbv[u]);
+                    load_cb<4>(cbrow + 32 * (ks0 + u) + 16 + 4 * kg, cbv[u] + 4);
+                }
 #pragma unroll
             for (int u = 0; u < KB4; ++u) {
                 const int ks = ks0 + u;
                 if (ks >= nks) break;
                 __builtin_amdgcn_sched_barrier(0);           // one k-step's operands live at a time
-                const int kb = 32 * ks + kg * 8;
                 float v[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const int k = kb + j;
+                    const int k = 32 * ks + 4 * kg + (j & 3) + (j >> 2) * 16;
                     v[j] = k <= m ? cbv[u][j] * __builtin_amdgcn_exp2f((dAm - dAs[k]) * LOG2E) * dts[k] : 0.f;
                 }
                 bf16x8 wh, wl;
                 split8(v, wh, wl);
+                const int xs = ks * 32 * XROW;
 #pragma unroll
                 for (int pt = 0; pt < PT; ++pt) {
-                    const int pr = pt * 16 + ln;
-                    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(xh + pr * XR + kb);
-                    const bf16x8 bl = *reinterpret_cast<const bf16x8*>(xl + pr * XR + kb);
+                    const char* ph = xh + xs + xo[pt];
+                    const char* pl = xl + xs + xo[pt];
+                    const bf16x8 bh = __builtin_shufflevector(ds_read_tr(ph), ds_read_tr(ph + 16 * XROW), 0, 1, 2, 3, 4, 5, 6, 7);
+                    const bf16x8 bl = __builtin_shufflevector(ds_read_tr(pl), ds_read_tr(pl + 16 * XROW), 0, 1, 2, 3, 4, 5, 6, 7);
                     acc[pt] = mma3(wh, wl, bh, bl, acc[pt]);
                 }
             }
@@ -483,7 +498,11 @@ __global__ void __launch_bounds__(THREADS, 4) k_chunk_scan_f32(ScanArgs a) {
                 const int mr = m0 + kg * 4 + i;
                 if (mr >= valid) continue;
                 float v = acc[pt][i];
-                if (a.D) v += dv * ((float)xh[p * XR + mr] + (float)xl[p * XR + mr]);
+                if (a.D) {
+                    const int xoff = mr * XROW + (((p >> 3) ^ xpswz(mr)) * 16) + 2 * (p & 7);
+                    v += dv * ((float)*reinterpret_cast<const bf16*>(xh + xoff) +
+                               (float)*reinterpret_cast<const bf16*>(xl + xoff));
+                }
                 const int64_t o = ((tok0 + mr) * H + h) * (int64_t)P + p;
                 if (a.out_x) a.out_x[o] = v;
                 if (a.z) v *= silu_f(reinterpret_cast<const float*>(a.z)[o]);
@@ -493,17 +512,14 @@ __global__ void __launch_bounds__(THREADS, 4) k_chunk_scan_f32(ScanArgs a) {
     }
 }
 
-// compile-time chunk 64 / 128 / 256, dstate 64 / 128 / 256 (others: the
-// generic kernel)
+// head dim 64, compile-time chunk 64 / 128 / 256 and dstate 64 / 128 / 256
+// (others: the generic kernel)
 template <typename TCB>
 int launch_f32(const ScanArgs& sa, hipStream_t s) {
     const size_t shm = f32_scan_lds(sa.Q, sa.P, sa.N);
     void (*kern)(ScanArgs) = nullptr;
 #define M2_F32_SCAN(PTV, NSV, QTV) \
     if (sa.P == 16 * PTV && sa.N == 32 * NSV && sa.Q == 32 * QTV) kern = k_chunk_scan_f32<PTV, NSV, QTV, TCB>;
-    M2_F32_SCAN(2, 2, 2) M2_F32_SCAN(2, 4, 2) M2_F32_SCAN(2, 8, 2)
-    M2_F32_SCAN(2, 2, 4) M2_F32_SCAN(2, 4, 4) M2_F32_SCAN(2, 8, 4)
-    M2_F32_SCAN(2, 2, 8) M2_F32_SCAN(2, 4, 8) M2_F32_SCAN(2, 8, 8)
     M2_F32_SCAN(4, 2, 2) M2_F32_SCAN(4, 4, 2) M2_F32_SCAN(4, 8, 2)
     M2_F32_SCAN(4, 2, 4) M2_F32_SCAN(4, 4, 4) M2_F32_SCAN(4, 8, 4)
     M2_F32_SCAN(4, 2, 8) M2_F32_SCAN(4, 4, 8) M2_F32_SCAN(4, 8, 8)
@@ -575,7 +591,7 @@ int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t s) {
     } else if (a.dtype == M2_F32) {
         M2_REQUIRE(a.dstate % 32 == 0, M2_ERR_UNSUPPORTED, "chunk_scan: f32 needs dstate %% 32 == 0");
         // split planes when they fit (head dim 32 / 64): x, C and states fp32
-        if (sa.P <= 64 && sa.states_same && f32_scan_lds(sa.Q, sa.P, sa.N) <= 160 * 1024) {
+        if (sa.P == 64 && sa.states_same && f32_scan_lds(sa.Q, sa.P, sa.N) <= 160 * 1024) {
             const int rc = a.cb_dtype == M2_F32 ? launch_f32<float>(sa, s)
                          : a.cb_dtype == M2_BF16 ? launch_f32<bf16>(sa, s) : M2_ERR_UNSUPPORTED;
             if (rc != M2_ERR_UNSUPPORTED) return rc;

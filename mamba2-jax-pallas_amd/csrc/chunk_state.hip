@@ -207,6 +207,194 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// k_chunk_state_f32: chunk mode for fp32 x / B.  One workgroup per (b, c,
+// HP heads of a group, 128-column dstate block): the weighted rows w[q] x[q, :]
+// of the HP heads and the block's B rows are staged once as bf16 hi / lo
+// planes, row-major with the 16-byte chunks of each row XOR-swizzled, and
+// the MFMA operands (8 consecutive positions of one column) come through the
+// gfx950 LDS transpose read; a product of two split operands is three
+// 16x16x32 bf16 MFMAs (~2^-16 relative).  With two heads the block's B rows
+// serve both.  The product is computed transposed, h^T[n, p] = B^T[n, q]
+// (w x)[q, p], so each lane holds 4 consecutive dstate columns of one
+// head-dim row (16-byte stores).  Wavefront w: with two heads, head w >> 2,
+// p-row tiles 2 ((w >> 1) & 1) .. +1; with one head, p-row tile w >> 1; n
+// tiles 4 (w & 1) .. +3.
+// ---------------------------------------------------------------------------
+constexpr float LOG2E_CS = 1.4426950408889634f;
+constexpr int F32_NB = 128;                            // dstate columns per workgroup
+__host__ __device__ inline size_t cs_f32_lds(int Q, int HP) {
+    return (size_t)2 * Q * (HP * 64 + F32_NB) * 2 + (size_t)HP * Q * 4;
+}
+// 16-byte chunk swizzle of plane row R (128- or 256-byte rows): the 8 rows a
+// transpose read touches at one chunk pair land on distinct banks
+template <int RB> M2_DEV int cswz(int R) { return RB == 128 ? ((R >> 1) & 3) << 1 : (R & 7) << 1; }
+
+M2_DEV f32x4 mma3cs(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, const bf16x8& bl, f32x4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, c, 0, 0, 0);
+}
+// 8 k of one column: rows r and r + 16 of the transpose read
+M2_DEV bf16x8 tr8(const char* p0, const char* p1) {
+    return __builtin_shufflevector(ds_read_tr(p0), ds_read_tr(p1), 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int HP, int QT>
+__global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
+    constexpr int P = 64, Q = 32 * QT;
+    constexpr int XROW = HP * P * 2, BROW = F32_NB * 2;     // plane row bytes
+    extern __shared__ __align__(16) char smem[];
+    char* xh = smem;                                     // [Q] rows of XROW: (w x) hi
+    char* xl = xh + Q * XROW;                            // (w x) lo
+    char* bh = xl + Q * XROW;                            // [Q] rows of BROW: B hi
+    char* bl = bh + Q * BROW;                            // B lo
+    float* wq = reinterpret_cast<float*>(bl + Q * BROW); // [HP][Q]
+
+    const int H = a.H, L = a.L, N = a.N, nc = a.nc;
+    const int nblk = N / F32_NB;
+    const int work = xcd_remap(blockIdx.x, a.nblocks);
+    const int nb = work % nblk;
+    const int hq = (work / nblk) % (H / HP);
+    const int rest = work / (nblk * (H / HP));
+    const int c = rest % nc, bi = rest / nc;
+    const int h0 = hq * HP;
+    const int g = h0 / (H / a.G);
+    const int qhi = min(Q, L - c * Q);                   // valid positions
+    const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
+
+    // ---- weights w[q] = exp(min(dA[last] - dA[q], 0)) dt[q], 0 past the end
+    // and where seq_idx differs from the chunk's last position (or that id < 0)
+    const int se = a.seq_idx ? a.seq_idx[tok0 + qhi - 1] : 0;
+    for (int i = threadIdx.x; i < HP * Q; i += THREADS) {
+        const int hh = i / Q, q = i % Q;
+        const int64_t row = (((int64_t)bi * H + h0 + hh) * nc + c) * Q;
+        float v = 0.f;
+        if (q < qhi) {
+            v = __builtin_amdgcn_exp2f(fminf(a.dA[row + qhi - 1] - a.dA[row + q], 0.f) * LOG2E_CS) * a.dt[row + q];
+            if (a.seq_idx && (se < 0 || a.seq_idx[tok0 + q] != se)) v = 0.f;
+        }
+        wq[i] = v;
+    }
+    __syncthreads();
+
+    // ---- staging: every row load in flight first, then weighted / split and
+    // written as 8-byte halves of swizzled 16-byte chunks
+    {
+        typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+        const float* xsrc = reinterpret_cast<const float*>(a.x) + (tok0 * H + h0) * P;
+        const float* bsrc = reinterpret_cast<const float*>(a.B) + (tok0 * a.G + g) * N + nb * F32_NB;
+        constexpr int XV = HP * P / 4, XI = Q * XV / THREADS;   // float4 per x row, per thread
+        constexpr int BV = F32_NB / 4, BI = Q * BV / THREADS;
+        static_assert(Q * XV % THREADS == 0 && Q * BV % THREADS == 0, "even staging split");
+        float4 xf[XI], bf[BI];
+#pragma unroll
+        for (int it = 0; it < XI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, q = idx / XV, v = idx % XV;
+            xf[it] = *reinterpret_cast<const float4*>(xsrc + (int64_t)min(q, qhi - 1) * H * P + 4 * v);
+        }
+#pragma unroll
+        for (int it = 0; it < BI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, q = idx / BV, v = idx % BV;
+            bf[it] = *reinterpret_cast<const float4*>(bsrc + (int64_t)min(q, qhi - 1) * a.G * N + 4 * v);
+        }
+#pragma unroll
+        for (int it = 0; it < XI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, q = idx / XV, v = idx % XV;
+            const float wv = wq[(4 * v / P) * Q + q];    // zero past the end
+            uint32_t h01, l01, h23, l23;
+            split2(xf[it].x * wv, xf[it].y * wv, h01, l01);
+            split2(xf[it].z * wv, xf[it].w * wv, h23, l23);
+            const int off = q * XROW + (((v >> 1) ^ cswz<XROW>(q)) * 16) + 8 * (v & 1);
+            *reinterpret_cast<u2*>(xh + off) = u2{h01, h23};
+            *reinterpret_cast<u2*>(xl + off) = u2{l01, l23};
+        }
+#pragma unroll
+        for (int it = 0; it < BI; ++it) {
+            const int idx = threadIdx.x + it * THREADS, q = idx / BV, v = idx % BV;
+            uint32_t h01, l01, h23, l23;
+            split2(bf[it].x, bf[it].y, h01, l01);
+            split2(bf[it].z, bf[it].w, h23, l23);
+            const int off = q * BROW + (((v >> 1) ^ cswz<BROW>(q)) * 16) + 8 * (v & 1);
+            *reinterpret_cast<u2*>(bh + off) = u2{h01, h23};
+            *reinterpret_cast<u2*>(bl + off) = u2{l01, l23};
+        }
+    }
+    __syncthreads();
+
+    // ---- h^T[n, p] over the chunk's positions.  K step ks covers rows
+    // 32 ks .. +31: MFMA k index j < 4 is row 32 ks + 4 kg + j, j >= 4 is 16
+    // more; the swizzles repeat every 8 rows
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int ln = lane & 15, kg = lane >> 4;
+    constexpr int PTW = HP == 2 ? 2 : 1;                 // p-row tiles per wavefront
+    const int pt0 = HP == 2 ? 4 * (w >> 2) + 2 * ((w >> 1) & 1) : (w >> 1);   // over the HP heads
+    const int nt0 = 4 * (w & 1);                         // first n tile
+    const int rA = 4 * kg + (ln >> 2), c1 = ln & 3, cb = 8 * (c1 & 1);
+    int xo[PTW], bo[4];
+#pragma unroll
+    for (int i = 0; i < PTW; ++i)
+        xo[i] = rA * XROW + (((2 * (pt0 + i) + (c1 >> 1)) ^ cswz<XROW>(rA)) * 16) + cb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        bo[j] = rA * BROW + (((2 * (nt0 + j) + (c1 >> 1)) ^ cswz<BROW>(rA)) * 16) + cb;
+    f32x4 acc[4][PTW];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < PTW; ++i) acc[j][i] = zero4();
+#pragma unroll
+    for (int ks = 0; ks < QT; ++ks) {
+        const int xs = ks * 32 * XROW, bs = ks * 32 * BROW;
+        bf16x8 ph[PTW], pl[PTW];
+#pragma unroll
+        for (int i = 0; i < PTW; ++i) {
+            ph[i] = tr8(xh + xs + xo[i], xh + xs + xo[i] + 16 * XROW);
+            pl[i] = tr8(xl + xs + xo[i], xl + xs + xo[i] + 16 * XROW);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const bf16x8 nh = tr8(bh + bs + bo[j], bh + bs + bo[j] + 16 * BROW);
+            const bf16x8 nlo = tr8(bl + bs + bo[j], bl + bs + bo[j] + 16 * BROW);
+#pragma unroll
+            for (int i = 0; i < PTW; ++i) acc[j][i] = mma3cs(nh, nlo, ph[i], pl[i], acc[j][i]);
+        }
+    }
+    // lane: p-tile pt0 + i, p = 16 (pt0 + i) + ln over the heads, n = 16 (nt0 + j) + 4 kg .. + 3
+#pragma unroll
+    for (int i = 0; i < PTW; ++i) {
+        const int pr = 16 * (pt0 + i) + ln;
+        const int hh = pr / P, pp = pr % P;
+        float* op = a.out + ((((int64_t)bi * nc + c) * H + h0 + hh) * P + pp) * N + nb * F32_NB;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<float4*>(op + 16 * (nt0 + j) + 4 * kg) =
+                make_float4(acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]);
+    }
+}
+
+// fp32 chunk mode: head dim 64, dstate a multiple of 128, chunk 64 / 128,
+// the plane LDS in budget; two heads per workgroup when the group's head
+// count is even
+int launch_chunk_state_f32(const StateArgs& sa, int64_t bhc, hipStream_t s) {
+    if (sa.P != 64 || sa.N % F32_NB || (sa.Q != 64 && sa.Q != 128)) return M2_ERR_UNSUPPORTED;
+    const int HP = (sa.H / sa.G) % 2 == 0 ? 2 : 1;
+    const size_t shm = cs_f32_lds(sa.Q, HP);
+    if (shm > 160 * 1024) return M2_ERR_UNSUPPORTED;
+    void (*kern)(StateArgs) = HP == 2 ? (sa.Q == 64 ? k_chunk_state_f32<2, 2> : k_chunk_state_f32<2, 4>)
+                                      : (sa.Q == 64 ? k_chunk_state_f32<1, 2> : k_chunk_state_f32<1, 4>);
+    if (shm > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return m2::set_error(M2_ERR_LAUNCH, "chunk_state: cannot reserve %zu B of LDS", shm);
+    StateArgs k = sa;
+    const int64_t nblocks = bhc / HP * (sa.N / F32_NB);
+    if (nblocks >= (1ll << 31)) return M2_ERR_UNSUPPORTED;
+    k.nblocks = (int)nblocks;
+    kern<<<(unsigned)nblocks, THREADS, shm, s>>>(k);
+    return m2::check_launch("chunk_state");
+}
+
 template <typename T, bool VARLEN>
 int launch_typed(const StateArgs& sa, int64_t nblocks, hipStream_t s) {
     const int KB = Pad<T>::KB < sa.Q ? Pad<T>::KB : sa.Q;
@@ -258,7 +446,11 @@ int launch_chunk_state(const m2_chunk_state_args& a, hipStream_t s) {
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_state: too many blocks");
     sa.nblocks = (int)nblocks;
     if (a.dtype == M2_BF16) return launch_typed<bf16, false>(sa, nblocks, s);
-    if (a.dtype == M2_F32) return launch_typed<float, false>(sa, nblocks, s);
+    if (a.dtype == M2_F32) {
+        const int rc = launch_chunk_state_f32(sa, nblocks, s);
+        if (rc != M2_ERR_UNSUPPORTED) return rc;
+        return launch_typed<float, false>(sa, nblocks, s);
+    }
     return set_error(M2_ERR_UNSUPPORTED, "chunk_state: dtype %d", a.dtype);
 }
 
