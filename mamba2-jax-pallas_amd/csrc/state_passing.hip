@@ -7,7 +7,8 @@
 // in registers; chunk c+DEPTH is loaded while chunk c is combined so that
 // DEPTH 16-byte loads per thread stay in flight.  Loads and stores are 16 B
 // per lane (8 B for bf16 output) and contiguous across the workgroup.  The
-// per-chunk decay and the seq_idx reset are wave-uniform scalars.
+// per-chunk decays (seq_idx resets applied) are computed for every chunk
+// into LDS before the walk, so no global load or exp sits on its serial path.
 //
 // Follows reference kernels/state_passing_fwd.py:108-151 (recurrence),
 // :208-225 (seq_idx reset: end-of-chunk id differs from the previous chunk's,
@@ -17,7 +18,7 @@
 namespace {
 
 constexpr int THREADS = 256;
-constexpr int DEPTH = 4;
+constexpr int DEPTH = 8;
 
 template <int VW> struct Vec;
 template <> struct Vec<4> {
@@ -49,15 +50,30 @@ k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
                 const int32_t* __restrict__ seq_idx, TO* __restrict__ out,
                 float* __restrict__ fin, int nc, int H, int64_t D, int L, int Q,
                 int blocks_per_row) {
+    extern __shared__ float scl[];                        // [nc] chunk decays
     const int row = blockIdx.x / blocks_per_row;          // (batch, head)
     const int blk = blockIdx.x % blocks_per_row;
     const int bi = row / H, h = row % H;
+    {
+        const float* dAr = dAc + (int64_t)bi * sb + (int64_t)h * sh;
+        for (int c = threadIdx.x; c < nc; c += THREADS) {
+            float v = expf(dAr[(int64_t)c * sc]);
+            if (seq_idx) {
+                // reset where the chunk-end id differs from the previous
+                // chunk's (0 before chunk 0)
+                const int cur = seq_idx[(int64_t)bi * L + min((c + 1) * Q, L) - 1];
+                const int prev = c > 0 ? seq_idx[(int64_t)bi * L + c * Q - 1] : 0;
+                if (cur != prev) v = 0.f;
+            }
+            scl[c] = v;
+        }
+    }
+    __syncthreads();
     const int64_t d0 = ((int64_t)blk * THREADS + threadIdx.x) * VW;
     if (d0 >= D) return;
     const int64_t cstride = (int64_t)H * D;                // between chunks
     const float* src = states + ((int64_t)bi * nc * H + h) * D + d0;
     TO* dst = out + ((int64_t)bi * nc * H + h) * D + d0;
-    const float* dA = dAc + (int64_t)bi * sb + (int64_t)h * sh;
 
     Vec<VW> run;
     if (init) {
@@ -70,20 +86,13 @@ k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
 #pragma unroll
     for (int i = 0; i < DEPTH; ++i)
         if (i < nc) buf[i].load(src + i * cstride);
-    int prev_seq = 0;
     for (int c0 = 0; c0 < nc; c0 += DEPTH) {
 #pragma unroll
         for (int i = 0; i < DEPTH; ++i) {
             const int c = c0 + i;
             if (c < nc) {
                 run.store(dst + c * cstride);
-                float scale = expf(dA[(int64_t)c * sc]);
-                if (seq_idx) {
-                    const int end = min((c + 1) * Q, L) - 1;
-                    const int cur = seq_idx[(int64_t)bi * L + end];
-                    if (cur != prev_seq) scale = 0.f;
-                    prev_seq = cur;
-                }
+                const float scale = scl[c];
                 const Vec<VW> st = buf[i];
                 if (c + DEPTH < nc) buf[i].load(src + (int64_t)(c + DEPTH) * cstride);
 #pragma unroll
@@ -101,13 +110,15 @@ int launch_typed(const m2_state_passing_args& a, hipStream_t s) {
     const int bpr = (int)((a.dim + per_block - 1) / per_block);
     const int64_t nblocks = a.batch * a.nheads * bpr;
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "state_passing: too many blocks");
+    M2_REQUIRE(a.nchunks <= 16384, M2_ERR_UNSUPPORTED, "state_passing: more than 16384 chunks");
+    const size_t shm = (size_t)a.nchunks * sizeof(float);
     if (vw == 4)
-        k_state_passing<TO, 4><<<(unsigned)nblocks, THREADS, 0, s>>>(
+        k_state_passing<TO, 4><<<(unsigned)nblocks, THREADS, shm, s>>>(
             a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
             a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
             (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
     else
-        k_state_passing<TO, 1><<<(unsigned)nblocks, THREADS, 0, s>>>(
+        k_state_passing<TO, 1><<<(unsigned)nblocks, THREADS, shm, s>>>(
             a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
             a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
             (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
