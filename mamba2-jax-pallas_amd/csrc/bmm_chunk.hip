@@ -6,8 +6,9 @@
 // K-contiguous in HBM ([.., L, G, K] rows), which is exactly
 // the per-lane layout MFMA wants, so every fragment is one 16-byte global load
 // (bf16) straight into VGPRs -- no LDS round trip.  A workgroup owns a 64 x 64
-// tile of one (b, c, g) block (so that even a few chunks fill the CUs); each of
-// its 4 wavefronts owns one 16-row tile and the 4 column tiles, with the K
+// tile of one (b, c, g) block (64 x 32 or 64 x 16 when there are too few such
+// tiles to fill the CUs); each of its 4 wavefronts owns one 16-row tile and
+// the block's column tiles, with the K
 // loop unrolled so that several steps of loads are in flight.  Causal and
 // seq_idx masks are applied in the epilogue.
 //
@@ -23,12 +24,12 @@ template <typename T, typename TO, int CT>
 __global__ void __launch_bounds__(THREADS)
 k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
             const int32_t* __restrict__ seq_idx, TO* __restrict__ out, int L, int G,
-            int K, int Q, int nc, int causal, int rowblocks, int nblocks) {
+            int K, int Q, int nc, int causal, int rowblocks, int colblocks, int nblocks) {
     typedef MF<T> M;
     const int work = xcd_remap(blockIdx.x, nblocks);
-    const int cb = work % rowblocks;                     // 64-column block
-    const int rb = (work / rowblocks) % rowblocks;       // 64-row block
-    int rest = work / (rowblocks * rowblocks);
+    const int cb = work % colblocks;                     // (16 CT)-column block
+    const int rb = (work / colblocks) % rowblocks;       // 64-row block
+    int rest = work / (rowblocks * colblocks);
     const int g = rest % G;
     rest /= G;
     const int c = rest % nc;
@@ -46,7 +47,7 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
     bool bok[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-        const int col = cb * 64 + ct * 16 + ln;
+        const int col = cb * 16 * CT + ct * 16 + ln;
         bok[ct] = (c * Q + col) < L && col < Q;
         bp[ct] = b + ((tbase + min(col, Q - 1)) * G + g) * K + kg * M::KPL;
     }
@@ -76,7 +77,7 @@ k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
     if (seq_idx) srow = (c * Q + row) < L ? seq_idx[tbase + row] : -1;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-        const int col0 = cb * 64 + ct * 16 + 4 * kg;
+        const int col0 = cb * 16 * CT + ct * 16 + 4 * kg;
         if (col0 >= Q) continue;
         float v[4];
 #pragma unroll
@@ -208,14 +209,19 @@ int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
     const int Q = (int)a.chunk_size;
     const int nc = (int)((a.seqlen + Q - 1) / Q);
     const int rowblocks = (Q + 63) / 64;
-    const int64_t nblocks = a.batch * nc * a.ngroups * rowblocks * rowblocks;
+    // 64 x 64 tiles; narrower column blocks (more workgroups) when there are
+    // too few tiles to fill the CUs
+    int ct = Q < 64 ? Q / 16 : 4;
+    const int64_t items = a.batch * nc * a.ngroups * rowblocks;
+    while (ct > 1 && items * ((Q + 16 * ct - 1) / (16 * ct)) < 512 && Q % (16 * (ct / 2)) == 0) ct /= 2;
+    const int colblocks = (Q + 16 * ct - 1) / (16 * ct);
+    const int64_t nblocks = items * colblocks;
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "bmm_chunk: too many blocks");
-    const int ct = Q < 64 ? Q / 16 : 4;
 #define M2_BMM_CASE(CTV)                                                                  \
     case CTV:                                                                             \
         k_bmm_chunk<T, TO, CTV><<<(unsigned)nblocks, THREADS, 0, s>>>(                     \
             (const T*)a.a, (const T*)a.b, a.seq_idx, (TO*)a.out, (int)a.seqlen,           \
-            (int)a.ngroups, (int)a.k, Q, nc, a.causal, rowblocks, (int)nblocks);          \
+            (int)a.ngroups, (int)a.k, Q, nc, a.causal, rowblocks, colblocks, (int)nblocks); \
         break;
     switch (ct) {
         M2_BMM_CASE(1) M2_BMM_CASE(2) M2_BMM_CASE(3) M2_BMM_CASE(4)
