@@ -98,7 +98,10 @@ def test_layer_decode_continues_prefill(dtype):
     cs_ptr, ss_ptr = cache["conv_state"].data_ptr(), cache["ssm_state"].data_ptr()
     out0, cache = m(u[:, :T0], inference_params=cache, inplace=True)
     assert cache["seqlen_offset"] == T0
-    check(out0, host(full[:, :T0]), 1e-5 if dtype == "f32" else 1e-2, "prefill with cache")
+    # the two prefills run the projections as GEMMs of different shapes, and
+    # fp32 SSD products go through bf16 triples (~2^-16 relative each): the
+    # BASELINE bar, as for the decode checks below
+    check(out0, host(full[:, :T0]), TOL[dtype], "prefill with cache")
     # one functional step first: the cache it is given stays as it was
     before = {k: cache[k].clone() for k in ("conv_state", "ssm_state")}
     o_f, c_f = m(u[:, T0:T0 + 1], inference_params=cache)
@@ -115,6 +118,7 @@ def test_layer_decode_continues_prefill(dtype):
     check(torch.cat(outs, 1), host(full[:, T0:]), TOL[dtype], "decode == prefill")
     if dtype == "f32":
         want, fin, conv_state = X.mamba2_layer(_params(m), host(u), _cfg(m))
+        check(out0, want[:, :T0], TOL["f32"], "prefill with cache vs oracle")
         check(torch.cat(outs, 1), want[:, T0:], TOL["f32"], "decode vs oracle")
         check(cache["ssm_state"], fin, TOL["f32"], "final ssm state vs oracle")
         np.testing.assert_allclose(host(cache["conv_state"]), conv_state, rtol=1e-6, atol=1e-6)
