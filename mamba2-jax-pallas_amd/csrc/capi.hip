@@ -170,14 +170,20 @@ int m2::ssd_combined_on(const m2_ssd_combined_args& a0, void* workspace, size_t 
         c1.dt = a.dt; c1.A = a.A; c1.dt_bias = a.dt_bias; c1.dA_cumsum = dA; c1.dt_out = dto;
         c1.batch = a.batch; c1.seqlen = a.seqlen; c1.nheads = a.nheads; c1.chunk_size = a.chunk_size;
         c1.dt_dtype = a.dt_dtype; c1.dt_softplus = a.dt_softplus; c1.dt_min = a.dt_min; c1.dt_max = a.dt_max;
-        if ((rc = m2::launch_chunk_cumsum(c1, s))) return rc;
-        if ((rc = record(a.stage_events, 1, s))) return rc;
-
         m2_chunk_state_args c2{};
         c2.x = a.x; c2.B = a.B; c2.dt = dto; c2.dA_cumsum = dA; c2.seq_idx = a.seq_idx; c2.states = states;
         c2.batch = a.batch; c2.seqlen = a.seqlen; c2.nheads = a.nheads; c2.headdim = a.headdim;
         c2.ngroups = a.ngroups; c2.dstate = a.dstate; c2.chunk_size = a.chunk_size; c2.dtype = a.dtype;
-        if ((rc = m2::launch_chunk_state(c2, s))) return rc;
+        // fp32: chunk_cumsum inside the chunk_state kernel where it covers the
+        // shape (the cumsum event interval then stays empty)
+        if (m2::chunk_state_cumsum_supported(c1, c2)) {
+            if ((rc = record(a.stage_events, 1, s))) return rc;
+            if ((rc = m2::launch_chunk_state_cumsum(c1, c2, s))) return rc;
+        } else {
+            if ((rc = m2::launch_chunk_cumsum(c1, s))) return rc;
+            if ((rc = record(a.stage_events, 1, s))) return rc;
+            if ((rc = m2::launch_chunk_state(c2, s))) return rc;
+        }
         if ((rc = record(a.stage_events, 2, s))) return rc;
 
         m2_state_passing_args c3{};

@@ -42,17 +42,6 @@ struct CumsumArgs {
     float lo, hi;
 };
 
-// inclusive prefix sum over the 64 lanes of a wavefront
-M2_DEV float wave_scan(float v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const float o = __shfl_up(v, off, 64);
-        if (lane >= off) v += o;
-    }
-    return v;
-}
-
 // PPL: positions per lane (Q <= 64 PPL)
 template <typename TD, int PPL>
 __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
@@ -65,6 +54,20 @@ __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
     const int qhi = min(Q, L - c * Q);              // valid positions of the chunk
     const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
 
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int h = hb * HB + w;
+    // every global load of the workgroup is issued before the first wait:
+    // the head's A / bias and the chunk's seq ids, then the dt tile
+    const float Ah = a.A[min(h, H - 1)];
+    const float bias = a.bias ? a.bias[min(h, H - 1)] : 0.f;
+    int sq[PPL];
+    int se = 0, sprev = 0;
+    if (a.seq) {
+#pragma unroll
+        for (int j = 0; j < PPL; ++j) sq[j] = a.seq[tok0 + min(lane + 64 * j, qhi - 1)];
+        se = a.seq[tok0 + qhi - 1];
+        if (c > 0) sprev = a.seq[tok0 - 1];
+    }
     // ---- coalesced tile load: thread t -> head t % 16, rows t / 16 + 64 i;
     // addresses clamped into the valid rows / heads (masked below)
     {
@@ -77,18 +80,6 @@ __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
         for (int i = 0; i < PPL; ++i)
             if (r0 + 64 * i < Q) tile[r0 + 64 * i][hh] = to_f32(raw[i]);
     }
-    const int lane = threadIdx.x & 63, w = wave_id();
-    const int h = hb * HB + w;
-    int sq[PPL];
-    int se = 0, sprev = 0;
-    if (a.seq) {
-#pragma unroll
-        for (int j = 0; j < PPL; ++j) sq[j] = a.seq[tok0 + min(lane + 64 * j, qhi - 1)];
-        se = a.seq[tok0 + qhi - 1];
-        if (c > 0) sprev = a.seq[tok0 - 1];
-    }
-    const float Ah = a.A[min(h, H - 1)];
-    const float bias = a.bias ? a.bias[min(h, H - 1)] : 0.f;
     __syncthreads();
     if (h >= H) return;                             // no barrier follows
 
@@ -103,7 +94,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
         d = fminf(fmaxf(d, a.lo), a.hi);
         v[j] = q < qhi ? d : 0.f;
         dA[j] = wave_scan(v[j] * Ah) + carry;
-        carry = __shfl(dA[j], 63, 64);
+        carry = lane63(dA[j]);
     }
     const float total = carry;                      // == dA[Q - 1] exactly
     float* const rowp = a.dA + (((int64_t)bi * H + h) * a.nc + c) * Q;

@@ -69,6 +69,14 @@ struct StateArgs {
     int states_bf16;             // varlen only: dtype of chunk_states
     float* out;
     int L, H, G, P, N, Q, nc, nblocks;
+    // chunk_cumsum folded in (k_chunk_state_f32<..., true>): the raw dt and its
+    // processing; dA / dt above are then outputs (written by the first dstate
+    // block of each chunk and head)
+    const void* dt_raw;
+    int dt_bf16, softplus;
+    const float* A;
+    const float* dt_bias;
+    float dt_lo, dt_hi;
 };
 
 template <typename T, int PT, int CTW, bool VARLEN>
@@ -220,6 +228,12 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state(StateArgs a) {
 // head-dim row (16-byte stores).  Wavefront w: with two heads, head w >> 2,
 // p-row tiles 2 ((w >> 1) & 1) .. +1; with one head, p-row tile w >> 1; n
 // tiles 4 (w & 1) .. +3.
+// The x and B rows are loaded into registers before the weights are formed,
+// so the two overlap.  With CS the workgroup also does chunk_cumsum for its
+// heads (the combined forward's fp32 path): wavefront hh processes head
+// h0 + hh's dt column (bias, softplus, clamp, zero past the end) and scans
+// dt' A over the chunk exactly as k_chunk_cumsum does, and the first dstate
+// block writes dA_cumsum and dt' for the kernels that follow.
 // ---------------------------------------------------------------------------
 constexpr float LOG2E_CS = 1.4426950408889634f;
 constexpr int F32_NB = 128;                            // dstate columns per workgroup
@@ -240,7 +254,7 @@ M2_DEV bf16x8 tr8(const char* p0, const char* p1) {
     return __builtin_shufflevector(ds_read_tr(p0), ds_read_tr(p1), 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <int HP, int QT>
+template <int HP, int QT, bool CS>
 __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
     constexpr int P = 64, Q = 32 * QT;
     constexpr int XROW = HP * P * 2, BROW = F32_NB * 2;     // plane row bytes
@@ -263,31 +277,15 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
     const int qhi = min(Q, L - c * Q);                   // valid positions
     const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
 
-    // ---- weights w[q] = exp(min(dA[last] - dA[q], 0)) dt[q], 0 past the end
-    // and where seq_idx differs from the chunk's last position (or that id < 0)
-    const int se = a.seq_idx ? a.seq_idx[tok0 + qhi - 1] : 0;
-    for (int i = threadIdx.x; i < HP * Q; i += THREADS) {
-        const int hh = i / Q, q = i % Q;
-        const int64_t row = (((int64_t)bi * H + h0 + hh) * nc + c) * Q;
-        float v = 0.f;
-        if (q < qhi) {
-            v = __builtin_amdgcn_exp2f(fminf(a.dA[row + qhi - 1] - a.dA[row + q], 0.f) * LOG2E_CS) * a.dt[row + q];
-            if (a.seq_idx && (se < 0 || a.seq_idx[tok0 + q] != se)) v = 0.f;
-        }
-        wq[i] = v;
-    }
-    __syncthreads();
-
-    // ---- staging: every row load in flight first, then weighted / split and
-    // written as 8-byte halves of swizzled 16-byte chunks
+    // ---- x and B rows into registers (all loads in flight first)
+    typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+    constexpr int XV = HP * P / 4, XI = Q * XV / THREADS;   // float4 per x row, per thread
+    constexpr int BV = F32_NB / 4, BI = Q * BV / THREADS;
+    static_assert(Q * XV % THREADS == 0 && Q * BV % THREADS == 0, "even staging split");
+    float4 xf[XI], bf[BI];
     {
-        typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
         const float* xsrc = reinterpret_cast<const float*>(a.x) + (tok0 * H + h0) * P;
         const float* bsrc = reinterpret_cast<const float*>(a.B) + (tok0 * a.G + g) * N + nb * F32_NB;
-        constexpr int XV = HP * P / 4, XI = Q * XV / THREADS;   // float4 per x row, per thread
-        constexpr int BV = F32_NB / 4, BI = Q * BV / THREADS;
-        static_assert(Q * XV % THREADS == 0 && Q * BV % THREADS == 0, "even staging split");
-        float4 xf[XI], bf[BI];
 #pragma unroll
         for (int it = 0; it < XI; ++it) {
             const int idx = threadIdx.x + it * THREADS, q = idx / XV, v = idx % XV;
@@ -298,6 +296,70 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
             const int idx = threadIdx.x + it * THREADS, q = idx / BV, v = idx % BV;
             bf[it] = *reinterpret_cast<const float4*>(bsrc + (int64_t)min(q, qhi - 1) * a.G * N + 4 * v);
         }
+    }
+
+    // ---- weights w[q] = exp(min(dA[last] - dA[q], 0)) dt[q], 0 past the end
+    // and where seq_idx differs from the chunk's last position (or that id < 0)
+    const int se = a.seq_idx ? a.seq_idx[tok0 + qhi - 1] : 0;
+    if constexpr (CS) {
+        constexpr int PPL = Q / 64;
+        const int lane = threadIdx.x & 63, hh = wave_id();
+        if (hh < HP) {
+            const int h = h0 + hh;
+            const float Ah = a.A[h];
+            const float bias = a.dt_bias ? a.dt_bias[h] : 0.f;
+            int sq[PPL];
+            float d[PPL];
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) {
+                const int64_t t = tok0 + min(lane + 64 * j, qhi - 1);
+                d[j] = a.dt_bf16 ? to_f32(reinterpret_cast<const bf16*>(a.dt_raw)[t * H + h])
+                                 : reinterpret_cast<const float*>(a.dt_raw)[t * H + h];
+                sq[j] = a.seq_idx ? a.seq_idx[t] : 0;
+            }
+            float v[PPL], dA[PPL], carry = 0.f;
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) {
+                const int q = lane + 64 * j;
+                float dd = d[j];
+                if (a.dt_bias) dd += bias;
+                if (a.softplus) dd = softplus_f(dd);
+                dd = fminf(fmaxf(dd, a.dt_lo), a.dt_hi);
+                v[j] = q < qhi ? dd : 0.f;
+                dA[j] = wave_scan(v[j] * Ah) + carry;
+                carry = lane63(dA[j]);
+            }
+            const float total = carry;                  // dA at the chunk's last position
+            const int64_t row = (((int64_t)bi * H + h) * nc + c) * Q;
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) {
+                const int q = lane + 64 * j;
+                if (nb == 0) {
+                    const_cast<float*>(a.dA)[row + q] = dA[j];
+                    const_cast<float*>(a.dt)[row + q] = v[j];
+                }
+                float wv = q < qhi ? __builtin_amdgcn_exp2f(fminf(total - dA[j], 0.f) * LOG2E_CS) * v[j] : 0.f;
+                if (a.seq_idx && (se < 0 || sq[j] != se)) wv = 0.f;
+                wq[hh * Q + q] = wv;
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < HP * Q; i += THREADS) {
+            const int hh = i / Q, q = i % Q;
+            const int64_t row = (((int64_t)bi * H + h0 + hh) * nc + c) * Q;
+            float v = 0.f;
+            if (q < qhi) {
+                v = __builtin_amdgcn_exp2f(fminf(a.dA[row + qhi - 1] - a.dA[row + q], 0.f) * LOG2E_CS) * a.dt[row + q];
+                if (a.seq_idx && (se < 0 || a.seq_idx[tok0 + q] != se)) v = 0.f;
+            }
+            wq[i] = v;
+        }
+    }
+    __syncthreads();
+
+    // ---- staging: weighted / split and written as 8-byte halves of
+    // swizzled 16-byte chunks
+    {
 #pragma unroll
         for (int it = 0; it < XI; ++it) {
             const int idx = threadIdx.x + it * THREADS, q = idx / XV, v = idx % XV;
@@ -375,14 +437,18 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
 
 // fp32 chunk mode: head dim 64, dstate a multiple of 128, chunk 64 / 128,
 // the plane LDS in budget; two heads per workgroup when the group's head
-// count is even
-int launch_chunk_state_f32(const StateArgs& sa, int64_t bhc, hipStream_t s) {
+// count is even.  cs: chunk_cumsum folded in (the StateArgs cumsum fields set)
+int launch_chunk_state_f32(const StateArgs& sa, int64_t bhc, hipStream_t s, bool cs = false) {
     if (sa.P != 64 || sa.N % F32_NB || (sa.Q != 64 && sa.Q != 128)) return M2_ERR_UNSUPPORTED;
     const int HP = (sa.H / sa.G) % 2 == 0 ? 2 : 1;
     const size_t shm = cs_f32_lds(sa.Q, HP);
     if (shm > 160 * 1024) return M2_ERR_UNSUPPORTED;
-    void (*kern)(StateArgs) = HP == 2 ? (sa.Q == 64 ? k_chunk_state_f32<2, 2> : k_chunk_state_f32<2, 4>)
-                                      : (sa.Q == 64 ? k_chunk_state_f32<1, 2> : k_chunk_state_f32<1, 4>);
+    void (*kern)(StateArgs) = nullptr;
+#define M2_CSF_CASE(HPV, QV, CSV) \
+    if (HP == HPV && sa.Q == QV && cs == CSV) kern = k_chunk_state_f32<HPV, QV / 32, CSV>;
+    M2_CSF_CASE(2, 64, false) M2_CSF_CASE(2, 128, false) M2_CSF_CASE(1, 64, false) M2_CSF_CASE(1, 128, false)
+    M2_CSF_CASE(2, 64, true) M2_CSF_CASE(2, 128, true) M2_CSF_CASE(1, 64, true) M2_CSF_CASE(1, 128, true)
+#undef M2_CSF_CASE
     if (shm > 65536 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
@@ -452,6 +518,40 @@ int launch_chunk_state(const m2_chunk_state_args& a, hipStream_t s) {
         return launch_typed<float, false>(sa, nblocks, s);
     }
     return set_error(M2_ERR_UNSUPPORTED, "chunk_state: dtype %d", a.dtype);
+}
+
+// chunk_cumsum + chunk_state of the combined forward's fp32 path in one
+// kernel: c1's outputs (dA_cumsum, dt_out) are written as chunk_cumsum
+// writes them.  For the shapes chunk_state_cumsum_supported accepts; the
+// caller runs the two stages separately for the others.
+bool chunk_state_cumsum_supported(const m2_chunk_cumsum_args& c1, const m2_chunk_state_args& a) {
+    return a.dtype == M2_F32 && (c1.dt_dtype == M2_F32 || c1.dt_dtype == M2_BF16) &&
+           a.chunk_size == c1.chunk_size && a.dt == c1.dt_out && a.dA_cumsum == c1.dA_cumsum &&
+           a.headdim == 64 && a.dstate % F32_NB == 0 && (a.chunk_size == 64 || a.chunk_size == 128) &&
+           a.ngroups > 0 && a.nheads % a.ngroups == 0 &&
+           cs_f32_lds((int)a.chunk_size, (a.nheads / a.ngroups) % 2 == 0 ? 2 : 1) <= 160 * 1024;
+}
+
+int launch_chunk_state_cumsum(const m2_chunk_cumsum_args& c1, const m2_chunk_state_args& a,
+                              hipStream_t s) {
+    M2_REQUIRE(chunk_state_cumsum_supported(c1, a), M2_ERR_UNSUPPORTED,
+               "chunk_state: shape / dtype not covered with chunk_cumsum folded in");
+    M2_REQUIRE(c1.dt && c1.A && a.x && a.B && a.dt && a.dA_cumsum && a.states, M2_ERR_INVALID,
+               "chunk_state: x, B, dt, A and the outputs are required");
+    M2_REQUIRE(a.batch > 0 && a.seqlen > 0 && a.nheads > 0 && a.ngroups > 0 &&
+                   a.nheads % a.ngroups == 0,
+               M2_ERR_INVALID, "chunk_state: bad sizes (nheads must be a multiple of ngroups)");
+    StateArgs sa{};
+    sa.x = a.x; sa.B = a.B; sa.dt = a.dt; sa.dA = a.dA_cumsum; sa.seq_idx = a.seq_idx;
+    sa.out = a.states;
+    sa.L = (int)a.seqlen; sa.H = (int)a.nheads; sa.G = (int)a.ngroups; sa.P = (int)a.headdim;
+    sa.N = (int)a.dstate; sa.Q = (int)a.chunk_size;
+    sa.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
+    sa.dt_raw = c1.dt; sa.dt_bf16 = c1.dt_dtype == M2_BF16; sa.softplus = c1.dt_softplus;
+    sa.A = c1.A; sa.dt_bias = c1.dt_bias; sa.dt_lo = c1.dt_min; sa.dt_hi = c1.dt_max;
+    const int64_t nblocks = a.batch * sa.nc * a.nheads;
+    if (nblocks >= (1ll << 31)) return M2_ERR_UNSUPPORTED;
+    return launch_chunk_state_f32(sa, nblocks, s, true);
 }
 
 int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t s) {

@@ -38,6 +38,27 @@ M2_DEV float softplus_f(float v) {
 }
 M2_DEV float silu_f(float v) { return v / (1.f + expf(-v)); }
 
+// inclusive prefix sum over the 64 lanes of a wavefront, on DPP lane moves
+// (no LDS round trips): a Hillis-Steele scan inside each row of 16 lanes
+// (row_shr 1, 2, 4, 8; lanes shifted in from outside the row read 0), then
+// the last lane of row 0 / 2 is added into row 1 / 3 (row_bcast:15) and
+// lane 31 into rows 2 and 3 (row_bcast:31)
+template <int CTRL, int ROWS = 0xf>
+M2_DEV float dpp_add(float v) {
+    const int t = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf, true);
+    return v + __int_as_float(t);
+}
+M2_DEV float wave_scan(float v) {
+    v = dpp_add<0x111>(v);            // row_shr:1
+    v = dpp_add<0x112>(v);            // row_shr:2
+    v = dpp_add<0x114>(v);            // row_shr:4
+    v = dpp_add<0x118>(v);            // row_shr:8
+    v = dpp_add<0x142, 0xa>(v);       // row_bcast:15 into rows 1, 3
+    v = dpp_add<0x143, 0xc>(v);       // row_bcast:31 into rows 2, 3
+    return v;
+}
+M2_DEV float lane63(float v) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)); }
+
 // ---------------------------------------------------------------------------
 // MFMA 16x16 traits.  One instruction computes D(16x16) += A(16xK) B(Kx16).
 //   A operand: lane l holds row (l & 15), k = (l >> 4) * KPL + j, j < KPL

@@ -12,6 +12,9 @@ int launch_chunk_cumsum(const m2_chunk_cumsum_args& a, hipStream_t stream);
 int launch_chunk_cumsum_ex(const m2_chunk_cumsum_args& a, const int32_t* seq_idx, float* wts,
                            float* scl, hipStream_t stream);
 int launch_chunk_state(const m2_chunk_state_args& a, hipStream_t stream);
+bool chunk_state_cumsum_supported(const m2_chunk_cumsum_args& c1, const m2_chunk_state_args& a);
+int launch_chunk_state_cumsum(const m2_chunk_cumsum_args& c1, const m2_chunk_state_args& a,
+                              hipStream_t stream);
 int launch_state_passing(const m2_state_passing_args& a, hipStream_t stream);
 int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t stream);
 int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t stream);

@@ -4,11 +4,20 @@
 //
 // HBM-bound streaming kernel.  Each thread owns VW consecutive elements of one
 // (batch, head) row and walks the chunks in order, keeping its running state
-// in registers; chunk c+DEPTH is loaded while chunk c is combined so that
-// DEPTH 16-byte loads per thread stay in flight.  Loads and stores are 16 B
-// per lane (8 B for bf16 output) and contiguous across the workgroup.  The
-// per-chunk decays (seq_idx resets applied) are computed for every chunk
-// into LDS before the walk, so no global load or exp sits on its serial path.
+// in registers; loads and stores are 16 bytes per lane (8 for bf16 output)
+// and contiguous across the workgroup.  Two walks:
+//  * rows of at most DEPTH chunks (latency-bound shapes): every chunk's load is
+//    issued up front, the walk waits once, and its combines and stores then
+//    run with no wait between them (on this target a wait for a load also
+//    waits for every store issued before it, so a load consumed after a store
+//    serialises the walk on store acknowledgements);
+//  * longer rows: chunk c + ROLL is loaded while chunk c is combined; the many
+//    workgroups of such shapes keep HBM busy across those waits.
+// The first loads are issued before anything else; while they are in flight
+// the per-chunk decays (seq_idx resets applied) are computed into LDS, so
+// neither a global load nor an exp sits on the walk's serial path.  The
+// block size (64-256 threads) is chosen per shape so that short rows and few
+// heads still spread over every CU.
 //
 // Follows reference kernels/state_passing_fwd.py:108-151 (recurrence),
 // :208-225 (seq_idx reset: end-of-chunk id differs from the previous chunk's,
@@ -17,8 +26,9 @@
 
 namespace {
 
-constexpr int THREADS = 256;
-constexpr int DEPTH = 8;
+constexpr int THREADS = 256;                 // largest block
+constexpr int DEPTH = 16;                    // chunks of the one-batch walk
+constexpr int ROLL = 8;                      // loads in flight in the rolling walk
 
 template <int VW> struct Vec;
 template <> struct Vec<4> {
@@ -43,7 +53,7 @@ template <> struct Vec<1> {
     M2_DEV void store(bf16* p) const { *p = (bf16)v[0]; }
 };
 
-template <typename TO, int VW>
+template <typename TO, int VW, bool ONE_BATCH>
 __global__ void __launch_bounds__(THREADS)
 k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
                 int64_t sb, int64_t sh, int64_t sc, const float* __restrict__ init,
@@ -54,9 +64,34 @@ k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
     const int row = blockIdx.x / blocks_per_row;          // (batch, head)
     const int blk = blockIdx.x % blocks_per_row;
     const int bi = row / H, h = row % H;
+    const int64_t d0 = ((int64_t)blk * blockDim.x + threadIdx.x) * VW;
+    const bool active = d0 < D;
+    const int64_t cstride = (int64_t)H * D;                // between chunks
+    const int64_t base = ((int64_t)bi * nc * H + h) * D + (active ? d0 : 0);
+    const float* src = states + base;
+    TO* dst = out + base;
+
+    // one-batch walk: loads take the chunk index clamped to the last chunk, so
+    // none is conditional and the compiler's wait analysis sees one batch
+    Vec<VW> buf[ONE_BATCH ? DEPTH : ROLL], run;
+    if (active) {
+        if constexpr (ONE_BATCH) {
+#pragma unroll
+            for (int i = 0; i < DEPTH; ++i) buf[i].load(src + (int64_t)min(i, nc - 1) * cstride);
+        } else {
+#pragma unroll
+            for (int i = 0; i < ROLL; ++i)
+                if (i < nc) buf[i].load(src + i * cstride);
+        }
+        if (init) run.load(init + ((int64_t)bi * H + h) * D + d0);
+    }
+    if (!init || !active) {
+#pragma unroll
+        for (int j = 0; j < VW; ++j) run.v[j] = 0.f;
+    }
     {
         const float* dAr = dAc + (int64_t)bi * sb + (int64_t)h * sh;
-        for (int c = threadIdx.x; c < nc; c += THREADS) {
+        for (int c = threadIdx.x; c < nc; c += blockDim.x) {
             float v = expf(dAr[(int64_t)c * sc]);
             if (seq_idx) {
                 // reset where the chunk-end id differs from the previous
@@ -69,34 +104,33 @@ k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
         }
     }
     __syncthreads();
-    const int64_t d0 = ((int64_t)blk * THREADS + threadIdx.x) * VW;
-    if (d0 >= D) return;
-    const int64_t cstride = (int64_t)H * D;                // between chunks
-    const float* src = states + ((int64_t)bi * nc * H + h) * D + d0;
-    TO* dst = out + ((int64_t)bi * nc * H + h) * D + d0;
-
-    Vec<VW> run;
-    if (init) {
-        run.load(init + ((int64_t)bi * H + h) * D + d0);
-    } else {
+    if (!active) return;
+    if constexpr (ONE_BATCH) {
+        // nc <= DEPTH: one explicit wait (vmcnt 0) for all loads, so the
+        // guarded stores below need none
+        __builtin_amdgcn_s_waitcnt(0x0F70);
 #pragma unroll
-        for (int j = 0; j < VW; ++j) run.v[j] = 0.f;
-    }
-    Vec<VW> buf[DEPTH];
-#pragma unroll
-    for (int i = 0; i < DEPTH; ++i)
-        if (i < nc) buf[i].load(src + i * cstride);
-    for (int c0 = 0; c0 < nc; c0 += DEPTH) {
-#pragma unroll
-        for (int i = 0; i < DEPTH; ++i) {
-            const int c = c0 + i;
+        for (int c = 0; c < DEPTH; ++c) {
             if (c < nc) {
-                run.store(dst + c * cstride);
+                run.store(dst + (int64_t)c * cstride);
                 const float scale = scl[c];
-                const Vec<VW> st = buf[i];
-                if (c + DEPTH < nc) buf[i].load(src + (int64_t)(c + DEPTH) * cstride);
 #pragma unroll
-                for (int j = 0; j < VW; ++j) run.v[j] = fmaf(scale, run.v[j], st.v[j]);
+                for (int j = 0; j < VW; ++j) run.v[j] = fmaf(scale, run.v[j], buf[c].v[j]);
+            }
+        }
+    } else {
+        for (int c0 = 0; c0 < nc; c0 += ROLL) {
+#pragma unroll
+            for (int i = 0; i < ROLL; ++i) {
+                const int c = c0 + i;
+                if (c < nc) {
+                    run.store(dst + (int64_t)c * cstride);
+                    const float scale = scl[c];
+                    const Vec<VW> st = buf[i];
+                    if (c + ROLL < nc) buf[i].load(src + (int64_t)(c + ROLL) * cstride);
+#pragma unroll
+                    for (int j = 0; j < VW; ++j) run.v[j] = fmaf(scale, run.v[j], st.v[j]);
+                }
             }
         }
     }
@@ -106,22 +140,24 @@ k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
 template <typename TO>
 int launch_typed(const m2_state_passing_args& a, hipStream_t s) {
     const int vw = (a.dim % 4 == 0) ? 4 : 1;
-    const int64_t per_block = (int64_t)THREADS * vw;
+    // the largest block (of 64 / 128 / 256 threads) that still gives ~4
+    // workgroups per CU
+    int bs = THREADS;
+    while (bs > 64 && a.batch * a.nheads * ((a.dim + (int64_t)bs * vw - 1) / ((int64_t)bs * vw)) < 1024)
+        bs /= 2;
+    const int64_t per_block = (int64_t)bs * vw;
     const int bpr = (int)((a.dim + per_block - 1) / per_block);
     const int64_t nblocks = a.batch * a.nheads * bpr;
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "state_passing: too many blocks");
     M2_REQUIRE(a.nchunks <= 16384, M2_ERR_UNSUPPORTED, "state_passing: more than 16384 chunks");
     const size_t shm = (size_t)a.nchunks * sizeof(float);
-    if (vw == 4)
-        k_state_passing<TO, 4><<<(unsigned)nblocks, THREADS, shm, s>>>(
-            a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
-            a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
-            (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
-    else
-        k_state_passing<TO, 1><<<(unsigned)nblocks, THREADS, shm, s>>>(
-            a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
-            a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
-            (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
+    const bool one = a.nchunks <= DEPTH;
+    auto kern = vw == 4 ? (one ? k_state_passing<TO, 4, true> : k_state_passing<TO, 4, false>)
+                        : (one ? k_state_passing<TO, 1, true> : k_state_passing<TO, 1, false>);
+    kern<<<(unsigned)nblocks, bs, shm, s>>>(
+        a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
+        a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
+        (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
     return m2::check_launch("state_passing");
 }
 

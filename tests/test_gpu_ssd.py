@@ -245,3 +245,40 @@ def test_state_pass_pair_splits_varlen(split, monkeypatch):
     monkeypatch.setenv("M2_STATES_KERNEL", split)
     cfg = dataclasses.replace(configs.CONFIGS["c3"], seqlen=2048, nheads=32, min_seqlen=64)
     _run_and_check(cfg, varlen=True)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_graph_replays_match_eager(dtype):
+    """The combined forward captured in a HIP graph (fp32: the staged kernels,
+    bf16: the fused ones).  Every replay (eager calls and synchronisations in
+    between, outputs cleared first) equals the eager result bit for bit."""
+    announce("combined forward graph replays", dtype)
+    cfg = dataclasses.replace(configs.CONFIGS["c0"], seqlen=1000, dtype=dtype)
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, dtype)
+    for k in ("cu_seqlens", "seq_idx", "z"):
+        t.pop(k)
+    kw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True)
+    want = mamba_chunk_scan_combined_fwd(**t, **kw)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mamba_chunk_scan_combined_fwd(**t, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y, fin = mamba_chunk_scan_combined_fwd(**t, **kw)
+    for r in range(3):
+        ye, fe = mamba_chunk_scan_combined_fwd(**t, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(ye, want[0]) and torch.equal(fe, want[1]), f"eager call {r}"
+        y.fill_(float("nan"))
+        fin.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want[0]), f"replay {r}: out"
+        assert torch.equal(fin, want[1]), f"replay {r}: final_states"
+    check(want[0], O.ssd_combined(io_dtype=dtype, **dict(d, cu_seqlens=None, seq_idx=None, z=None),
+                                  **kw)[0], TOL[dtype], "out vs oracle")
