@@ -2,7 +2,9 @@
 // (Q x Q output, contraction over K = dstate).
 //
 // bf16 operands at the usual sizes take k_bmm_chunk_lds (one workgroup per
-// chunk and group, operands staged in LDS once).  Otherwise: both operands are
+// chunk and group, operands staged in LDS once), fp32 operands on shapes with
+// enough (chunk, group) blocks k_bmm_chunk_lds_f32 (the same, operands staged
+// as bf16 hi / lo planes, each product three MFMAs).  Otherwise: both operands are
 // K-contiguous in HBM ([.., L, G, K] rows), which is exactly
 // the per-lane layout MFMA wants, so every fragment is one 16-byte global load
 // (bf16) straight into VGPRs -- no LDS round trip.  A workgroup owns a 64 x 64
@@ -183,6 +185,136 @@ k_bmm_chunk_lds(const bf16* __restrict__ a, const bf16* __restrict__ b,
     }
 }
 
+// fp32 operands: one workgroup per (b, c, g) as above, both row blocks
+// staged once as bf16 hi / lo planes (v = hi + lo; a product is
+// hi.hi + hi.lo + lo.hi, ~2^-16 relative), rows row-major with the 16-byte
+// chunks XOR-swizzled by row.  Every fp32 row is loaded into registers
+// before the first is split, so one round trip brings the whole block in.
+template <typename TO, int QT, int KC>
+__global__ void __launch_bounds__(LDS_THREADS)
+k_bmm_chunk_lds_f32(const float* __restrict__ a, const float* __restrict__ b,
+                    const int32_t* __restrict__ seq_idx, TO* __restrict__ out, int L, int G, int nc,
+                    int causal) {
+    constexpr int Q = 16 * QT, K = 8 * KC;                 // KC 16-byte bf16 chunks per row
+    extern __shared__ __align__(16) char smem[];
+    bf16* ah = reinterpret_cast<bf16*>(smem);              // [Q][K] planes
+    bf16* al = ah + Q * K;
+    bf16* bh = al + Q * K;
+    bf16* bl = bh + Q * K;
+    int* seqs = reinterpret_cast<int*>(bl + Q * K);        // [Q]
+    const int work = blockIdx.x;
+    const int g = work % G, c = (work / G) % nc, bi = work / (G * nc);
+    const int64_t tbase = (int64_t)bi * L + (int64_t)c * Q;
+    const int valid = min(Q, L - c * Q);
+    // ---- both row blocks into registers, then split into the planes; rows
+    // past the end are zero
+    {
+        typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+        constexpr int VPR = K / 4, NV = Q * VPR / LDS_THREADS;   // float4 per row, per thread
+        static_assert(Q * VPR % LDS_THREADS == 0, "even staging split");
+        float4 va[NV], vb[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int idx = threadIdx.x + i * LDS_THREADS, r = idx / VPR, v = idx % VPR;
+            const int64_t go = ((tbase + min(r, valid - 1)) * G + g) * K + 4 * v;
+            va[i] = *reinterpret_cast<const float4*>(a + go);
+            vb[i] = *reinterpret_cast<const float4*>(b + go);
+        }
+        for (int q = threadIdx.x; q < Q; q += LDS_THREADS)
+            seqs[q] = (seq_idx && q < valid) ? seq_idx[tbase + q] : -1;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int idx = threadIdx.x + i * LDS_THREADS, r = idx / VPR, v = idx % VPR;
+            const int so = r * K + 8 * ((v >> 1) ^ (r & (KC - 1) & 15)) + 4 * (v & 1);
+            const float4 x = r < valid ? va[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 y = r < valid ? vb[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            uint32_t h01, l01, h23, l23;
+            split2(x.x, x.y, h01, l01);
+            split2(x.z, x.w, h23, l23);
+            *reinterpret_cast<u2*>(ah + so) = u2{h01, h23};
+            *reinterpret_cast<u2*>(al + so) = u2{l01, l23};
+            split2(y.x, y.y, h01, l01);
+            split2(y.z, y.w, h23, l23);
+            *reinterpret_cast<u2*>(bh + so) = u2{h01, h23};
+            *reinterpret_cast<u2*>(bl + so) = u2{l01, l23};
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, w = wave_id();
+    const int ln = lane & 15, kg = lane >> 4;
+    TO* op = out + ((((int64_t)bi * nc + c) * G + g) * Q) * Q;
+    for (int rt = w; rt < QT; rt += LDS_THREADS / 64) {
+        const int row = 16 * rt + ln;                      // this lane's output row (a row)
+        f32x4 acc[QT];
+#pragma unroll
+        for (int ct = 0; ct < QT; ++ct) acc[ct] = zero4();
+#pragma unroll
+        for (int ks = 0; ks < KC / 4; ++ks) {
+            const int ch = 4 * ks + kg;
+            const int ro = row * K + 8 * (ch ^ (row & (KC - 1) & 15));
+            const bf16x8 afh = *reinterpret_cast<const bf16x8*>(ah + ro);
+            const bf16x8 afl = *reinterpret_cast<const bf16x8*>(al + ro);
+#pragma unroll
+            for (int ct = 0; ct < QT; ++ct) {
+                const int col = 16 * ct + ln;
+                const int co = col * K + 8 * (ch ^ (col & (KC - 1) & 15));
+                const bf16x8 bfh = *reinterpret_cast<const bf16x8*>(bh + co);
+                const bf16x8 bfl = *reinterpret_cast<const bf16x8*>(bl + co);
+                // transposed product (A = b rows, B = a rows): lane (ln, kg)
+                // ends with row 16 rt + ln, columns 16 ct + 4 kg + i
+                f32x4 t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfl, afh, acc[ct], 0, 0, 0);
+                t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfh, afl, t, 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfh, afh, t, 0, 0, 0);
+            }
+        }
+        const int srow = seqs[row];
+#pragma unroll
+        for (int ct = 0; ct < QT; ++ct) {
+            const int col0 = 16 * ct + 4 * kg;
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int col = col0 + i;
+                v[i] = acc[ct][i];
+                if (causal && col > row) v[i] = 0.f;
+                if (seq_idx && srow != seqs[col]) v[i] = 0.f;
+            }
+            TO* dst = op + (int64_t)row * Q + col0;
+            if constexpr (sizeof(TO) == 4) {
+                *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                const bf16x4 o = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+                *reinterpret_cast<bf16x4*>(dst) = o;
+            }
+        }
+    }
+}
+
+// the fp32 LDS kernel where it applies: chunk 64 / 128, K 64 / 128, and at
+// least 128 (chunk, group) blocks (fewer leave most CUs idle: the tiled
+// kernel spreads small problems wider)
+template <typename TO>
+bool launch_lds_f32(const m2_bmm_chunk_args& a, hipStream_t s) {
+    const int Q = (int)a.chunk_size, K = (int)a.k;
+    const int nc = (int)((a.seqlen + Q - 1) / Q);
+    const int64_t nblocks = a.batch * nc * a.ngroups;
+    if (nblocks < 128 || nblocks >= (1ll << 31)) return false;
+    void (*kern)(const float*, const float*, const int32_t*, TO*, int, int, int, int) = nullptr;
+#define M2_BMMF_CASE(QV, KV) if (Q == QV && K == KV) kern = k_bmm_chunk_lds_f32<TO, QV / 16, KV / 8>;
+    M2_BMMF_CASE(64, 64) M2_BMMF_CASE(64, 128) M2_BMMF_CASE(128, 64) M2_BMMF_CASE(128, 128)
+#undef M2_BMMF_CASE
+    if (!kern) return false;
+    const size_t shm = (size_t)8 * Q * K + (size_t)Q * 4;
+    if (shm > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return false;
+    kern<<<(unsigned)nblocks, LDS_THREADS, shm, s>>>((const float*)a.a, (const float*)a.b, a.seq_idx,
+                                                      (TO*)a.out, (int)a.seqlen, (int)a.ngroups, nc,
+                                                      a.causal);
+    return true;
+}
+
 template <typename TO>
 bool launch_lds(const m2_bmm_chunk_args& a, hipStream_t s) {
     const int Q = (int)a.chunk_size, K = (int)a.k;
@@ -205,6 +337,8 @@ template <typename T, typename TO>
 int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
     if constexpr (sizeof(T) == 2) {
         if (launch_lds<TO>(a, s)) return m2::check_launch("bmm_chunk");
+    } else {
+        if (launch_lds_f32<TO>(a, s)) return m2::check_launch("bmm_chunk");
     }
     const int Q = (int)a.chunk_size;
     const int nc = (int)((a.seqlen + Q - 1) / Q);

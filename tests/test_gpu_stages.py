@@ -163,6 +163,10 @@ BMM_CFGS = [
     (2, 512, 1, 64, 128, True, [[256, 256], [128, 384]]),
     (2, 512, 8, 64, 64, True, [[64, 192, 256], [128, 128, 256]]),
     (1, 256, 1, 64, 64, False, [[64, 64, 64, 64]]),
+    # >= 128 (chunk, group) blocks: the LDS-staged kernels (fp32 and bf16)
+    (1, 4096, 8, 128, 128, False, None),             # c2 shape
+    (1, 4000, 8, 128, 128, True, [[1000, 3000]]),    # L % Q != 0, seq_idx
+    (2, 2048, 4, 64, 64, True, [[700, 1348], [2048]]),
 ]
 
 
