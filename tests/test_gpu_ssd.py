@@ -282,3 +282,23 @@ def test_graph_replays_match_eager(dtype):
         assert torch.equal(fin, want[1]), f"replay {r}: final_states"
     check(want[0], O.ssd_combined(io_dtype=dtype, **dict(d, cu_seqlens=None, seq_idx=None, z=None),
                                   **kw)[0], TOL[dtype], "out vs oracle")
+
+
+_F32_WIDE_CASES = {
+    # fp32 with >= 128 (chunk, group) blocks at chunk 128: the LDS-staged fp32
+    # bmm_chunk and chunk_cumsum folded into the fp32 chunk_state kernel
+    "c2_heads32": (dataclasses.replace(configs.CONFIGS["c2"], dtype="f32", nheads=32), {}),
+    "n64_ragged_z_Dhdim": (dataclasses.replace(configs.CONFIGS["c2"], dtype="f32", seqlen=4000,
+                                               nheads=16, ngroups=4, dstate=64),
+                           dict(with_z=True, Dhp=True)),
+    "packed_varlen": (dataclasses.replace(configs.CONFIGS["c3"], dtype="f32", seqlen=4096,
+                                          nheads=32, dstate=128, min_seqlen=64),
+                      dict(varlen=True)),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_F32_WIDE_CASES))
+def test_fp32_wide_shapes(case):
+    announce("fp32 wide shape", case)
+    cfg, kw = _F32_WIDE_CASES[case]
+    _run_and_check(cfg, **kw)
