@@ -1,6 +1,7 @@
 """Benchmark: one Mamba2 SSD layer forward at the nemotron-h-8b shape on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--dtype f32|bf16]
+                    [--no-cpu-baseline]
     python bench.py --ops [--lm 130m,2.7b]     (the ops around the SSD, LM decode)
 
 A step is one call of mamba2_jax.kernels.mamba_chunk_scan_combined_fwd on
@@ -578,6 +579,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", default="c2")
+    ap.add_argument("--dtype", choices=("f32", "bf16"), default=None,
+                    help="run --config with these input dtypes (default: the config's own)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
@@ -610,6 +613,10 @@ def main(argv=None):
     from mamba2_jax import configs
 
     cfg = configs.CONFIGS[args.config]
+    own_dtype = args.dtype is None or args.dtype == cfg.dtype
+    if not own_dtype:
+        import dataclasses
+        cfg = dataclasses.replace(cfg, dtype=args.dtype)
     if args.stage_ops:
         print(json.dumps({"stage_operators": bench_stage_operators(cfg), "config": args.config}))
         return 0
@@ -623,7 +630,7 @@ def main(argv=None):
     # idle gap: besides their own figures they keep the GPU at its steady
     # clocks, which an idle GPU drops (measured at the headline shape: 0.126 ms
     # per layer after 5 warm-up steps on an idle GPU, 0.107 ms when busy).
-    if args.config == "c2" and not args.no_configs:
+    if args.config == "c2" and own_dtype and not args.no_configs:
         res_extra["configs"] = {c: bench_other_config(c) for c in ("c0", "c1", "c3")}
         res_extra["fp32_same_shape"] = bench_fp32_same_shape(cfg)
         res_extra["stage_operators"] = bench_stage_operators(cfg)
@@ -645,7 +652,8 @@ def main(argv=None):
     # timed region (value): W warm-up steps, then K back-to-back steps
     ms, wall_ms = time_layer(kw, K, args.warmup)
     stages, dom, roof, stages_ms_total, tot_by = finish()
-    traffic = measured_traffic(args.config)
+    # measured traffic is kept for each config at its own dtype
+    traffic = measured_traffic(args.config) if own_dtype else {}
     roof["traffic"] = traffic.get(dom)
     if traffic:
         roof["traffic_source"] = traffic.get("source")
@@ -654,7 +662,8 @@ def main(argv=None):
         "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": ms,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": cfg.dtype, "data": "synthetic",
-        "config": {"workload": f"{cfg.name} SSD layer forward ({args.config})",
+        "config": {"workload": f"{cfg.name} SSD layer forward ({args.config}"
+                               f"{'' if own_dtype else ', ' + cfg.dtype + ' inputs'})",
                    "batch": cfg.batch, "seq_len": cfg.seqlen, "nheads": cfg.nheads,
                    "ngroups": cfg.ngroups, "headdim": cfg.headdim, "dstate": cfg.dstate,
                    "chunk_size": cfg.chunk_size, "parallelism": "single-gpu"},
@@ -670,7 +679,7 @@ def main(argv=None):
     torch.cuda.synchronize()
     # CPU baselines last (host only): the full c2 workload, bounded samples of the others
     if not args.no_cpu_baseline:
-        full = args.config == "c2" and args.cpu_heads == 0
+        full = args.config == "c2" and own_dtype and args.cpu_heads == 0
         res["cpu_baseline"] = cpu_baseline(cfg, cfg.nheads if full else (args.cpu_heads or 32))
         for c, sample_heads in (("c0", 24), ("c1", 16), ("c3", 32)):
             if c in res.get("configs", {}):
