@@ -1,7 +1,7 @@
 """Parity of the whole SSD forward (mamba_chunk_scan_combined_fwd) on the GPU.
 
-* against the CPU oracle (float64) at the benchmark shapes: c0 and c2 in full,
-  c1 / c3 with fewer heads or tokens (the oracle's memory grows with L*H*Q);
+* against the CPU oracle (float64) at the benchmark shapes: c0, c1 and c2 in
+  full, c3 with fewer heads or tokens (the oracle's memory grows with L*H*Q);
 * at the full c1 / c3 sizes through size-independent properties: agreement
   with the naive formulation run on the GPU (c1) and packed == per-sequence
   runs (c3);
@@ -127,6 +127,13 @@ def test_headdim_128_dstate_256_chunk_64():
     announce("P=128 N=256 Q=64")
     cfg = configs.SSDConfig("wide", 1, 256, 8, 2, 128, 256, 64, "bf16", seed=22)
     _run_and_check(cfg)
+
+
+def test_c1_full_vs_oracle():
+    """Full c1 (batch 4, L 2048, 80 heads, chunk 256, initial state) against the
+    CPU oracle."""
+    announce("c1 full vs oracle")
+    _run_and_check(configs.CONFIGS["c1"])
 
 
 def test_c1_full_vs_naive_on_gpu():

@@ -3,7 +3,8 @@
 * one step against the oracle's closed form at the c4 shape and with every
   parameter-shape variant the reference supports;
 * 256 consecutive in-place steps against the oracle's float64 trajectory and
-  against the HIP prefill over the same tokens (decode == prefill);
+  against the HIP prefill over the same tokens (decode == prefill), and 32
+  steps at the full c4 batch of 64 against the oracle;
 * functional (default) / in-place semantics, and the reference's own usage
   pattern (expected values computed from the state after the call).
 """
@@ -100,6 +101,31 @@ def test_256_steps_trajectory_and_prefill():
         initial_states=s0, dt_softplus=True, return_final_states=True)
     check(Y, host(yp), TOL["bf16"], "decode == prefill (outputs)")
     check(state, host(fp), TOL["bf16"], "decode == prefill (final state)")
+
+
+def test_full_batch_trajectory():
+    """c4 at its full batch of 64: 32 in-place steps == the oracle's float64
+    trajectory (outputs of every step and the state after the last)."""
+    cfg = configs.DecodeConfig("c4-b64", 64, 128, 8, 64, 128, 32)
+    announce("ssu full batch, 32 steps", cfg)
+    d = configs.make_decode_inputs(cfg)
+    state = dev(d["state"])
+    ref = d["state"].astype(np.float64)
+    ys, wys = [], []
+    A, D, bias = dev(d["A"]), dev(d["D"]), dev(d["dt_bias"])
+    for t in range(cfg.steps):
+        new, y = selective_state_update(state, dev(d["x"][t], torch.bfloat16), dev(d["dt"][t]), A,
+                                        dev(d["B"][t], torch.bfloat16), dev(d["C"][t], torch.bfloat16),
+                                        D=D, z=dev(d["z"][t], torch.bfloat16), dt_bias=bias,
+                                        dt_softplus=True, inplace=True)
+        ys.append(y)
+        ref, wy = O.selective_state_update(ref, d["x"][t], d["dt"][t], d["A"], d["B"][t],
+                                           d["C"][t], D=d["D"], z=d["z"][t],
+                                           dt_bias=d["dt_bias"], dt_softplus=True,
+                                           round_fn=O.round_fn_for("bf16"))
+        wys.append(wy)
+    check(state, ref, 1e-4, "state after 32 steps")
+    check(torch.stack(ys, dim=1), np.stack(wys, axis=1), 1e-4, "outputs of 32 steps")
 
 
 def test_inplace_and_copy_semantics():
