@@ -44,9 +44,12 @@ STAGES = ["chunk_cumsum", "chunk_state", "state_passing", "bmm_chunk", "chunk_sc
 
 
 def internal_chunk(cfg):
-    """The chunk size the combined path runs: bf16 chunks of 256 run as chunks of
-    128 when both fused kernels then apply (m2_ssd_combined's internal_args)."""
-    if cfg.dtype == "bf16" and cfg.chunk_size == 256:
+    """The chunk size the combined path runs (m2_ssd_combined's internal_args):
+    bf16 chunks of 256 run as chunks of 128 when both fused kernels then apply,
+    fp32 chunks of 256 always."""
+    if cfg.chunk_size == 256:
+        if cfg.dtype == "f32":
+            return 128
         import dataclasses
         c = dataclasses.replace(cfg, chunk_size=128)
         if states_is_fused(c) and scan_is_fused(c):
@@ -81,6 +84,12 @@ def stage_work(cfg, with_init=False, with_z=False):
         cb_bytes = s * b * nc * G * Q * Q
         by, fl = w.pop("chunk_scan")
         w["bmm_chunk+chunk_scan"] = (by - cb_bytes + b * L * G * N * s, fl + sf)
+    if cumsum_in_state(cfg):
+        # fp32: chunk_cumsum inside the chunk_state kernel, which reads the raw
+        # dt and writes dA_cumsum / dt' for the later stages (no weights read)
+        cb_, cf_ = w.pop("chunk_cumsum")
+        sb_, sf_ = w.pop("chunk_state")
+        w[FUSED_CUMSUM] = (sb_ - 8 * cq + b * L * H * s + 8 * cq, sf_ + cf_)
     if states_is_fused(cfg):
         # chunk_cumsum also writes the chunk-state weights and the chunk decay;
         # one chunk-sequential kernel then reads x, B and the weights and writes
@@ -95,6 +104,15 @@ def stage_work(cfg, with_init=False, with_z=False):
 
 
 FUSED_STATES = "chunk_state+state_passing"
+FUSED_CUMSUM = "chunk_cumsum+chunk_state"
+
+
+def cumsum_in_state(cfg):
+    """The combined path runs chunk_cumsum inside the fp32 chunk_state kernel
+    for fp32, headdim 64, dstate a multiple of 128 and chunk_size 64 / 128
+    (m2::chunk_state_cumsum_supported)."""
+    return (cfg.dtype == "f32" and cfg.headdim == 64 and cfg.dstate % 128 == 0
+            and cfg.chunk_size in (64, 128) and cfg.nheads % cfg.ngroups == 0)
 
 
 def states_is_fused(cfg):
@@ -480,7 +498,8 @@ def stage_events(cfg, steps):
     hev = HipEvents()
     icfg = dataclasses.replace(cfg, chunk_size=internal_chunk(cfg))
     fs, fc = states_is_fused(icfg), scan_is_fused(icfg)
-    keep = [True, True, True, not fs, not fc, True]
+    fcs = cumsum_in_state(icfg)
+    keep = [True, not fcs, True, not fs, not fc, True]
     evs = [[hev.new() if k else None for k in keep] for _ in range(steps)]
     return hev, evs, keep, fs, fc
 
@@ -504,6 +523,9 @@ def _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc):
     if fs:
         stage_ms["chunk_cumsum"] = slots["chunk_cumsum"]
         stage_ms[FUSED_STATES] = slots["chunk_state"]
+    elif not keep[1]:
+        stage_ms[FUSED_CUMSUM] = slots["chunk_state"]
+        stage_ms["state_passing"] = slots["state_passing"]
     else:
         stage_ms.update({k: slots[k] for k in STAGES[:3]})
     if fc:
