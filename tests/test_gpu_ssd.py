@@ -309,3 +309,18 @@ def test_fp32_wide_shapes(case):
     announce("fp32 wide shape", case)
     cfg, kw = _F32_WIDE_CASES[case]
     _run_and_check(cfg, **kw)
+
+
+@pytest.mark.parametrize("H,G,N,Q,L,packed", [
+    (6, 2, 256, 64, 1000, True),     # 3 heads a group: one head per workgroup; 2 column blocks
+    (8, 2, 128, 128, 777, False),    # head pairs, ragged length
+    (4, 4, 256, 128, 640, True),     # one head a group
+])
+def test_fp32_cumsum_in_chunk_state(H, G, N, Q, L, packed):
+    """fp32 with chunk_cumsum folded into the chunk_state kernel (dstate a
+    multiple of 128, chunk 64 / 128): its dA_cumsum / dt' feed state passing
+    and the scan; against the oracle, with D per head-dim and z."""
+    announce("fp32 cumsum in chunk_state", H, G, N, Q, L, packed)
+    cfg = configs.SSDConfig("f32cs", 1, L, H, G, 64, N, Q, "f32", nseq=3 if packed else 0,
+                            min_seqlen=64, seed=H + N + L)
+    _run_and_check(cfg, with_z=True, Dhp=True, varlen=packed)
