@@ -69,14 +69,16 @@ struct StateArgs {
     int states_bf16;             // varlen only: dtype of chunk_states
     float* out;
     int L, H, G, P, N, Q, nc, nblocks;
-    // chunk_cumsum folded in (k_chunk_state_f32<..., true>): the raw dt and its
-    // processing; dA / dt above are then outputs (written by the first dstate
-    // block of each chunk and head)
+    // chunk_cumsum folded in (k_chunk_state_f32<..., true>): the raw dt, its
+    // processing, and where dA_cumsum / dt' go (written by the first dstate
+    // block of each chunk and head; dA / dt above are not read)
     const void* dt_raw;
     int dt_bf16, softplus;
     const float* A;
     const float* dt_bias;
     float dt_lo, dt_hi;
+    float* dA_out;
+    float* dt_out;
 };
 
 template <typename T, int PT, int CTW, bool VARLEN>
@@ -335,8 +337,8 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
             for (int j = 0; j < PPL; ++j) {
                 const int q = lane + 64 * j;
                 if (nb == 0) {
-                    const_cast<float*>(a.dA)[row + q] = dA[j];
-                    const_cast<float*>(a.dt)[row + q] = v[j];
+                    a.dA_out[row + q] = dA[j];
+                    a.dt_out[row + q] = v[j];
                 }
                 float wv = q < qhi ? __builtin_amdgcn_exp2f(fminf(total - dA[j], 0.f) * LOG2E_CS) * v[j] : 0.f;
                 if (a.seq_idx && (se < 0 || sq[j] != se)) wv = 0.f;
@@ -549,6 +551,7 @@ int launch_chunk_state_cumsum(const m2_chunk_cumsum_args& c1, const m2_chunk_sta
     sa.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
     sa.dt_raw = c1.dt; sa.dt_bf16 = c1.dt_dtype == M2_BF16; sa.softplus = c1.dt_softplus;
     sa.A = c1.A; sa.dt_bias = c1.dt_bias; sa.dt_lo = c1.dt_min; sa.dt_hi = c1.dt_max;
+    sa.dA_out = c1.dA_cumsum; sa.dt_out = c1.dt_out;
     const int64_t nblocks = a.batch * sa.nc * a.nheads;
     if (nblocks >= (1ll << 31)) return M2_ERR_UNSUPPORTED;
     return launch_chunk_state_f32(sa, nblocks, s, true);
