@@ -84,6 +84,11 @@ def stage_work(cfg, with_init=False, with_z=False):
         cb_bytes = s * b * nc * G * Q * Q
         by, fl = w.pop("chunk_scan")
         w["bmm_chunk+chunk_scan"] = (by - cb_bytes + b * L * G * N * s, fl + sf)
+    if pass_bmm_fused(cfg):
+        # fp32 with the tiled bmm_chunk kernel: state_passing and bmm_chunk in one launch
+        pb, pf = w.pop("state_passing")
+        mb, mf = w.pop("bmm_chunk")
+        w[FUSED_PASS_BMM] = (pb + mb, pf + mf)
     if cumsum_in_state(cfg):
         # fp32: chunk_cumsum inside the chunk_state kernel, which reads the raw
         # dt and writes dA_cumsum / dt' for the later stages (no weights read)
@@ -105,6 +110,18 @@ def stage_work(cfg, with_init=False, with_z=False):
 
 FUSED_STATES = "chunk_state+state_passing"
 FUSED_CUMSUM = "chunk_cumsum+chunk_state"
+FUSED_PASS_BMM = "state_passing+bmm_chunk"
+
+
+def pass_bmm_fused(cfg):
+    """fp32 inputs whose bmm_chunk takes the tiled kernel (fewer than 128
+    (chunk, group) blocks, or chunk / dstate outside 64 / 128): state_passing
+    and bmm_chunk run in one launch (m2::state_passing_bmm_supported)."""
+    if cfg.dtype != "f32" or states_is_fused(cfg):
+        return False
+    Q, K = cfg.chunk_size, cfg.dstate
+    nblocks = cfg.batch * math.ceil(cfg.seqlen / Q) * cfg.ngroups
+    return not (nblocks >= 128 and Q in (64, 128) and K in (64, 128))
 
 
 def cumsum_in_state(cfg):
@@ -498,8 +515,8 @@ def stage_events(cfg, steps):
     hev = HipEvents()
     icfg = dataclasses.replace(cfg, chunk_size=internal_chunk(cfg))
     fs, fc = states_is_fused(icfg), scan_is_fused(icfg)
-    fcs = cumsum_in_state(icfg)
-    keep = [True, not fcs, True, not fs, not fc, True]
+    fcs, fpb = cumsum_in_state(icfg), pass_bmm_fused(icfg)
+    keep = [True, not fcs, True, not (fs or fpb), not fc, True]
     evs = [[hev.new() if k else None for k in keep] for _ in range(steps)]
     return hev, evs, keep, fs, fc
 
@@ -519,19 +536,21 @@ def _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc):
     total = float(np.mean([hev.elapsed_ms(evs[i][0], evs[i][5]) for i in range(steps)]))
     work = stage_work(cfg, with_init=kw["initial_states"] is not None)
     slots = dict(zip(STAGES, slot_ms))
-    stage_ms = {}
     if fs:
-        stage_ms["chunk_cumsum"] = slots["chunk_cumsum"]
-        stage_ms[FUSED_STATES] = slots["chunk_state"]
+        first = {"chunk_cumsum": slots["chunk_cumsum"], FUSED_STATES: slots["chunk_state"]}
     elif not keep[1]:
-        stage_ms[FUSED_CUMSUM] = slots["chunk_state"]
-        stage_ms["state_passing"] = slots["state_passing"]
+        first = {FUSED_CUMSUM: slots["chunk_state"], "state_passing": slots["state_passing"]}
     else:
-        stage_ms.update({k: slots[k] for k in STAGES[:3]})
+        first = {k: slots[k] for k in STAGES[:3]}
     if fc:
-        stage_ms["bmm_chunk+chunk_scan"] = slots["chunk_scan"]
+        second = {"bmm_chunk+chunk_scan": slots["chunk_scan"]}
     else:
-        stage_ms.update({k: slots[k] for k in STAGES[3:]})
+        second = {k: slots[k] for k in STAGES[3:]}
+    if not fs and not keep[3]:
+        # state_passing and bmm_chunk in one launch (its time: the bmm interval)
+        first.pop("state_passing")
+        first[FUSED_PASS_BMM] = second.pop("bmm_chunk")
+    stage_ms = {**first, **second}
     peak_mfma = PEAK_MFMA_TFLOPS[cfg.dtype]
     stages = {}
     for s in stage_ms:

@@ -17,89 +17,15 @@
 // Follows reference kernels/bmm_chunk_fwd.py:87-154 (product), :348-372
 // (masks; positions past the end carry seq id -1) and ops/ssd_naive.py:189-216.
 #include "m2_internal.h"
+#include "bmm_tile.h"
 
 namespace {
 
 constexpr int THREADS = 256;
 
 template <typename T, typename TO, int CT>
-__global__ void __launch_bounds__(THREADS)
-k_bmm_chunk(const T* __restrict__ a, const T* __restrict__ b,
-            const int32_t* __restrict__ seq_idx, TO* __restrict__ out, int L, int G,
-            int K, int Q, int nc, int causal, int rowblocks, int colblocks, int nblocks) {
-    typedef MF<T> M;
-    const int work = xcd_remap(blockIdx.x, nblocks);
-    const int cb = work % colblocks;                     // (16 CT)-column block
-    const int rb = (work / colblocks) % rowblocks;       // 64-row block
-    int rest = work / (rowblocks * colblocks);
-    const int g = rest % G;
-    rest /= G;
-    const int c = rest % nc;
-    const int bi = rest / nc;
-    const int lane = threadIdx.x & 63, w = wave_id();
-    const int r0 = rb * 64 + w * 16;
-    if (r0 >= Q) return;
-    const int ln = lane & 15, kg = lane >> 4;
-
-    const int arow = r0 + ln;
-    const int64_t tbase = (int64_t)bi * L + (int64_t)c * Q;
-    const bool arow_ok = (c * Q + arow) < L;
-    const T* ap = a + ((tbase + arow) * G + g) * K + kg * M::KPL;
-    const T* bp[CT];
-    bool bok[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-        const int col = cb * 16 * CT + ct * 16 + ln;
-        bok[ct] = (c * Q + col) < L && col < Q;
-        bp[ct] = b + ((tbase + min(col, Q - 1)) * G + g) * K + kg * M::KPL;
-    }
-    f32x4 acc[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) acc[ct] = zero4();
-
-    typename M::frag zf;
-#pragma unroll
-    for (int j = 0; j < M::KPL; ++j) M::set(zf, j, 0.f);
-
-#pragma unroll 8
-    for (int k0 = 0; k0 < K; k0 += M::K) {
-        const typename M::frag af = arow_ok ? load_frag(ap + k0) : zf;
-        typename M::frag bf[CT];
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) bf[ct] = bok[ct] ? load_frag(bp[ct] + k0) : zf;
-        // transposed product (A = b rows, B = a rows): lane (ln, kg) ends with
-        // row r0 + ln, columns 16 ct + 4 kg + i -- four consecutive outputs
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[ct] = M::mma(bf[ct], af, acc[ct]);
-    }
-
-    TO* op = out + ((((int64_t)bi * nc + c) * G + g) * Q) * Q;
-    const int row = arow;
-    int srow = 0;
-    if (seq_idx) srow = (c * Q + row) < L ? seq_idx[tbase + row] : -1;
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-        const int col0 = cb * 16 * CT + ct * 16 + 4 * kg;
-        if (col0 >= Q) continue;
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int col = col0 + i;
-            v[i] = acc[ct][i];
-            if (causal && col > row) v[i] = 0.f;
-            if (seq_idx) {
-                const int scol = (c * Q + col) < L ? seq_idx[tbase + col] : -1;
-                if (srow != scol) v[i] = 0.f;
-            }
-        }
-        TO* dst = op + (int64_t)row * Q + col0;
-        if constexpr (sizeof(TO) == 4) {
-            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-            const bf16x4 o = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
-            *reinterpret_cast<bf16x4*>(dst) = o;
-        }
-    }
+__global__ void __launch_bounds__(THREADS) k_bmm_chunk(m2::BmmTileArgs p) {
+    m2::bmm_tile<T, TO, CT>(p, xcd_remap(blockIdx.x, p.nblocks));
 }
 
 // One workgroup per (b, c, g) for bf16 operands whose two Q x K row blocks fit
@@ -340,22 +266,14 @@ int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
     } else {
         if (launch_lds_f32<TO>(a, s)) return m2::check_launch("bmm_chunk");
     }
-    const int Q = (int)a.chunk_size;
-    const int nc = (int)((a.seqlen + Q - 1) / Q);
-    const int rowblocks = (Q + 63) / 64;
-    // 64 x 64 tiles; narrower column blocks (more workgroups) when there are
-    // too few tiles to fill the CUs
-    int ct = Q < 64 ? Q / 16 : 4;
-    const int64_t items = a.batch * nc * a.ngroups * rowblocks;
-    while (ct > 1 && items * ((Q + 16 * ct - 1) / (16 * ct)) < 512 && Q % (16 * (ct / 2)) == 0) ct /= 2;
-    const int colblocks = (Q + 16 * ct - 1) / (16 * ct);
-    const int64_t nblocks = items * colblocks;
-    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "bmm_chunk: too many blocks");
+    m2::BmmTileArgs p;
+    const int ct = m2::bmm_tile_plan(a, p);
+    M2_REQUIRE(p.nblocks > 0, M2_ERR_UNSUPPORTED, "bmm_chunk: too many blocks");
+    const int64_t nblocks = p.nblocks;
+    const int Q = p.Q;
 #define M2_BMM_CASE(CTV)                                                                  \
     case CTV:                                                                             \
-        k_bmm_chunk<T, TO, CTV><<<(unsigned)nblocks, THREADS, 0, s>>>(                     \
-            (const T*)a.a, (const T*)a.b, a.seq_idx, (TO*)a.out, (int)a.seqlen,           \
-            (int)a.ngroups, (int)a.k, Q, nc, a.causal, rowblocks, colblocks, (int)nblocks); \
+        k_bmm_chunk<T, TO, CTV><<<(unsigned)nblocks, THREADS, 0, s>>>(p);                  \
         break;
     switch (ct) {
         M2_BMM_CASE(1) M2_BMM_CASE(2) M2_BMM_CASE(3) M2_BMM_CASE(4)
@@ -368,6 +286,26 @@ int launch_typed(const m2_bmm_chunk_args& a, hipStream_t s) {
 }  // namespace
 
 namespace m2 {
+
+// launch_bmm_chunk takes the tiled kernel (the LDS kernels do not apply)
+bool bmm_uses_tiles(const m2_bmm_chunk_args& a) {
+    const int64_t Q = a.chunk_size, K = a.k;
+    const int64_t nblocks = a.batch * ((a.seqlen + Q - 1) / Q) * a.ngroups;
+    if (a.dtype == M2_BF16)
+        return !((Q == 64 || Q == 128) && (K == 64 || K == 128 || K == 256) && nblocks < (1ll << 31));
+    return !(nblocks >= 128 && nblocks < (1ll << 31) && (Q == 64 || Q == 128) && (K == 64 || K == 128));
+}
+
+int check_bmm_chunk_args(const m2_bmm_chunk_args& a) {
+    M2_REQUIRE(a.a && a.b && a.out, M2_ERR_INVALID, "bmm_chunk: a, b and out are required");
+    M2_REQUIRE(a.batch > 0 && a.seqlen > 0 && a.ngroups > 0 && a.k > 0 && a.chunk_size > 0,
+               M2_ERR_INVALID, "bmm_chunk: sizes must be positive");
+    M2_REQUIRE(a.chunk_size % 16 == 0 && a.chunk_size <= 256, M2_ERR_UNSUPPORTED,
+               "bmm_chunk: chunk_size must be a multiple of 16 and <= 256 (got %lld)",
+               (long long)a.chunk_size);
+    M2_REQUIRE(a.k % 32 == 0, M2_ERR_UNSUPPORTED, "bmm_chunk: k %% 32 != 0");
+    return M2_OK;
+}
 
 int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t s) {
     M2_REQUIRE(a.a && a.b && a.out, M2_ERR_INVALID, "bmm_chunk: a, b and out are required");

@@ -148,6 +148,7 @@ int m2::ssd_combined_on(const m2_ssd_combined_args& a0, void* workspace, size_t 
     void* cb = ws + l.cb;
     const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
     int rc;
+    bool cb_done = false;                   // CB already computed (with state_passing)
     if ((rc = record(a.stage_events, 0, s))) return rc;
 
     if (m2::states_fused_supported(a)) {
@@ -194,8 +195,21 @@ int m2::ssd_combined_on(const m2_ssd_combined_args& a0, void* workspace, size_t 
         c3.final_states = a.final_states;
         c3.batch = a.batch; c3.nchunks = nc; c3.nheads = a.nheads; c3.dim = a.headdim * a.dstate;
         c3.seqlen = a.seqlen; c3.chunk_size = a.chunk_size; c3.out_dtype = a.dtype;
-        if ((rc = m2::launch_state_passing(c3, s))) return rc;
-        if ((rc = record(a.stage_events, 3, s))) return rc;
+        // fp32 with the tiled bmm_chunk kernel: bmm_chunk (independent of the
+        // state chain) in the same launch as state_passing; its time lands in
+        // the bmm_chunk event interval
+        m2_bmm_chunk_args c4{};
+        c4.a = a.C; c4.b = a.B; c4.seq_idx = a.seq_idx; c4.out = cb;
+        c4.batch = a.batch; c4.seqlen = a.seqlen; c4.ngroups = a.ngroups; c4.k = a.dstate;
+        c4.chunk_size = a.chunk_size; c4.dtype = a.dtype; c4.out_dtype = a.dtype; c4.causal = 0;
+        if (m2::state_passing_bmm_supported(c3, c4)) {
+            if ((rc = record(a.stage_events, 3, s))) return rc;
+            if ((rc = m2::launch_state_passing_bmm(c3, c4, s))) return rc;
+            cb_done = true;
+        } else {
+            if ((rc = m2::launch_state_passing(c3, s))) return rc;
+            if ((rc = record(a.stage_events, 3, s))) return rc;
+        }
     }
 
     if (a.dtype == M2_BF16 && m2::scan_fused_supported(a.headdim, a.dstate, a.chunk_size)) {
@@ -204,11 +218,13 @@ int m2::ssd_combined_on(const m2_ssd_combined_args& a0, void* workspace, size_t 
         if ((rc = m2::launch_scan_fused(a, dA, dto, passed, s))) return rc;
         if ((rc = record(a.stage_events, 5, s))) return rc;
     } else {
-        m2_bmm_chunk_args c4{};
-        c4.a = a.C; c4.b = a.B; c4.seq_idx = a.seq_idx; c4.out = cb;
-        c4.batch = a.batch; c4.seqlen = a.seqlen; c4.ngroups = a.ngroups; c4.k = a.dstate;
-        c4.chunk_size = a.chunk_size; c4.dtype = a.dtype; c4.out_dtype = a.dtype; c4.causal = 0;
-        if ((rc = m2::launch_bmm_chunk(c4, s))) return rc;
+        if (!cb_done) {
+            m2_bmm_chunk_args c4{};
+            c4.a = a.C; c4.b = a.B; c4.seq_idx = a.seq_idx; c4.out = cb;
+            c4.batch = a.batch; c4.seqlen = a.seqlen; c4.ngroups = a.ngroups; c4.k = a.dstate;
+            c4.chunk_size = a.chunk_size; c4.dtype = a.dtype; c4.out_dtype = a.dtype; c4.causal = 0;
+            if ((rc = m2::launch_bmm_chunk(c4, s))) return rc;
+        }
         if ((rc = record(a.stage_events, 4, s))) return rc;
 
         m2_chunk_scan_args c5{};

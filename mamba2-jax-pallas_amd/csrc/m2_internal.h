@@ -17,6 +17,12 @@ int launch_chunk_state_cumsum(const m2_chunk_cumsum_args& c1, const m2_chunk_sta
                               hipStream_t stream);
 int launch_state_passing(const m2_state_passing_args& a, hipStream_t stream);
 int launch_bmm_chunk(const m2_bmm_chunk_args& a, hipStream_t stream);
+bool bmm_uses_tiles(const m2_bmm_chunk_args& a);
+int check_bmm_chunk_args(const m2_bmm_chunk_args& a);
+// state_passing (fp32 out) and bmm_chunk (fp32 in and out, tiled kernel) in one launch
+bool state_passing_bmm_supported(const m2_state_passing_args& p, const m2_bmm_chunk_args& m);
+int launch_state_passing_bmm(const m2_state_passing_args& p, const m2_bmm_chunk_args& m,
+                             hipStream_t stream);
 int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t stream);
 int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t stream);
 int launch_ssu(const m2_ssu_args& a, hipStream_t stream);

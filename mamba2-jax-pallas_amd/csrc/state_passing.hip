@@ -23,6 +23,7 @@
 // :208-225 (seq_idx reset: end-of-chunk id differs from the previous chunk's,
 // previous id of chunk 0 is 0) and ops/ssd_naive.py:135-182.
 #include "m2_internal.h"
+#include "bmm_tile.h"
 
 namespace {
 
@@ -53,16 +54,33 @@ template <> struct Vec<1> {
     M2_DEV void store(bf16* p) const { *p = (bf16)v[0]; }
 };
 
+struct PassArgs {
+    const float* states;
+    const float* dAc;
+    int64_t sb, sh, sc;
+    const float* init;
+    const int32_t* seq_idx;
+    void* out;
+    float* fin;
+    int nc, H;
+    int64_t D;
+    int L, Q, blocks_per_row;
+};
+
+// the walk of block `block` (blockDim.x threads, `scl` nc floats of LDS)
 template <typename TO, int VW, bool ONE_BATCH>
-__global__ void __launch_bounds__(THREADS)
-k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
-                int64_t sb, int64_t sh, int64_t sc, const float* __restrict__ init,
-                const int32_t* __restrict__ seq_idx, TO* __restrict__ out,
-                float* __restrict__ fin, int nc, int H, int64_t D, int L, int Q,
-                int blocks_per_row) {
-    extern __shared__ float scl[];                        // [nc] chunk decays
-    const int row = blockIdx.x / blocks_per_row;          // (batch, head)
-    const int blk = blockIdx.x % blocks_per_row;
+M2_DEV void pass_walk(const PassArgs& p, int block, float* scl) {
+    const float* __restrict__ states = p.states;
+    const float* __restrict__ dAc = p.dAc;
+    const int64_t sb = p.sb, sh = p.sh, sc = p.sc;
+    const float* __restrict__ init = p.init;
+    const int32_t* __restrict__ seq_idx = p.seq_idx;
+    TO* __restrict__ out = static_cast<TO*>(p.out);
+    float* __restrict__ fin = p.fin;
+    const int nc = p.nc, H = p.H, L = p.L, Q = p.Q, blocks_per_row = p.blocks_per_row;
+    const int64_t D = p.D;
+    const int row = block / blocks_per_row;               // (batch, head)
+    const int blk = block % blocks_per_row;
     const int bi = row / H, h = row % H;
     const int64_t d0 = ((int64_t)blk * blockDim.x + threadIdx.x) * VW;
     const bool active = d0 < D;
@@ -137,6 +155,33 @@ k_state_passing(const float* __restrict__ states, const float* __restrict__ dAc,
     if (fin) run.store(fin + ((int64_t)bi * H + h) * D + d0);
 }
 
+template <typename TO, int VW, bool ONE_BATCH>
+__global__ void __launch_bounds__(THREADS) k_state_passing(PassArgs p) {
+    extern __shared__ float scl[];                        // [nc] chunk decays
+    pass_walk<TO, VW, ONE_BATCH>(p, blockIdx.x, scl);
+}
+
+// state_passing and the independent bmm_chunk of the same forward in one
+// launch of 256-thread blocks: blocks below npass walk states, the others
+// compute CB tiles (one launch less on the path, and the CB tiles fill the
+// CUs the walk leaves idle)
+template <int VW, bool ONE_BATCH, int CT>
+__global__ void __launch_bounds__(THREADS) k_pass_bmm(PassArgs p, m2::BmmTileArgs m, int npass) {
+    extern __shared__ float scl[];
+    if ((int)blockIdx.x < npass) pass_walk<float, VW, ONE_BATCH>(p, blockIdx.x, scl);
+    else m2::bmm_tile<float, float, CT>(m, xcd_remap(blockIdx.x - npass, m.nblocks));
+}
+
+PassArgs pass_args(const m2_state_passing_args& a, int bpr) {
+    PassArgs p{};
+    p.states = a.states; p.dAc = a.dA_chunk_cumsum;
+    p.sb = a.dA_stride_batch; p.sh = a.dA_stride_head; p.sc = a.dA_stride_chunk;
+    p.init = a.initial_states; p.seq_idx = a.seq_idx; p.out = a.out; p.fin = a.final_states;
+    p.nc = (int)a.nchunks; p.H = (int)a.nheads; p.D = a.dim; p.L = (int)a.seqlen;
+    p.Q = (int)a.chunk_size; p.blocks_per_row = bpr;
+    return p;
+}
+
 template <typename TO>
 int launch_typed(const m2_state_passing_args& a, hipStream_t s) {
     const int vw = (a.dim % 4 == 0) ? 4 : 1;
@@ -154,10 +199,7 @@ int launch_typed(const m2_state_passing_args& a, hipStream_t s) {
     const bool one = a.nchunks <= DEPTH;
     auto kern = vw == 4 ? (one ? k_state_passing<TO, 4, true> : k_state_passing<TO, 4, false>)
                         : (one ? k_state_passing<TO, 1, true> : k_state_passing<TO, 1, false>);
-    kern<<<(unsigned)nblocks, bs, shm, s>>>(
-        a.states, a.dA_chunk_cumsum, a.dA_stride_batch, a.dA_stride_head, a.dA_stride_chunk,
-        a.initial_states, a.seq_idx, (TO*)a.out, a.final_states, (int)a.nchunks,
-        (int)a.nheads, a.dim, (int)a.seqlen, (int)a.chunk_size, bpr);
+    kern<<<(unsigned)nblocks, bs, shm, s>>>(pass_args(a, bpr));
     return m2::check_launch("state_passing");
 }
 
@@ -165,7 +207,7 @@ int launch_typed(const m2_state_passing_args& a, hipStream_t s) {
 
 namespace m2 {
 
-int launch_state_passing(const m2_state_passing_args& a, hipStream_t s) {
+int check_state_passing_args(const m2_state_passing_args& a) {
     M2_REQUIRE(a.states && a.dA_chunk_cumsum && a.out, M2_ERR_INVALID,
                "state_passing: states, dA_chunk_cumsum and out are required");
     M2_REQUIRE(a.batch > 0 && a.nchunks > 0 && a.nheads > 0 && a.dim > 0, M2_ERR_INVALID,
@@ -175,6 +217,48 @@ int launch_state_passing(const m2_state_passing_args& a, hipStream_t s) {
                               a.seqlen <= a.nchunks * a.chunk_size),
                M2_ERR_INVALID, "state_passing: seq_idx needs chunk_size and a seqlen that "
                "spans nchunks chunks");
+    M2_REQUIRE(a.nchunks <= 16384, M2_ERR_UNSUPPORTED, "state_passing: more than 16384 chunks");
+    return M2_OK;
+}
+
+bool state_passing_bmm_supported(const m2_state_passing_args& p, const m2_bmm_chunk_args& m) {
+    return p.out_dtype == M2_F32 && m.dtype == M2_F32 && m.out_dtype == M2_F32 &&
+           bmm_uses_tiles(m);
+}
+
+int launch_state_passing_bmm(const m2_state_passing_args& a, const m2_bmm_chunk_args& m,
+                             hipStream_t s) {
+    M2_REQUIRE(state_passing_bmm_supported(a, m), M2_ERR_UNSUPPORTED,
+               "state_passing + bmm_chunk: fp32 with the tiled bmm_chunk kernel only");
+    int rc;
+    if ((rc = check_state_passing_args(a)) || (rc = check_bmm_chunk_args(m))) return rc;
+    BmmTileArgs mt;
+    const int ct = bmm_tile_plan(m, mt);
+    const int vw = (a.dim % 4 == 0) ? 4 : 1;
+    const int64_t per_block = (int64_t)THREADS * vw;
+    const int bpr = (int)((a.dim + per_block - 1) / per_block);
+    const int64_t npass = a.batch * a.nheads * bpr;
+    M2_REQUIRE(mt.nblocks > 0 && npass + mt.nblocks < (1ll << 31), M2_ERR_UNSUPPORTED,
+               "state_passing + bmm_chunk: too many blocks");
+    const bool one = a.nchunks <= DEPTH;
+    void (*kern)(PassArgs, BmmTileArgs, int) = nullptr;
+#define M2_PB_CASE(VWV, ONEV, CTV) \
+    if (vw == VWV && one == ONEV && ct == CTV) kern = k_pass_bmm<VWV, ONEV, CTV>;
+#define M2_PB_CT(VWV, ONEV) M2_PB_CASE(VWV, ONEV, 1) M2_PB_CASE(VWV, ONEV, 2) \
+                            M2_PB_CASE(VWV, ONEV, 3) M2_PB_CASE(VWV, ONEV, 4)
+    M2_PB_CT(4, true) M2_PB_CT(4, false) M2_PB_CT(1, true) M2_PB_CT(1, false)
+#undef M2_PB_CT
+#undef M2_PB_CASE
+    M2_REQUIRE(kern, M2_ERR_UNSUPPORTED, "state_passing + bmm_chunk: chunk_size %lld",
+               (long long)m.chunk_size);
+    const size_t shm = (size_t)a.nchunks * sizeof(float);
+    kern<<<(unsigned)(npass + mt.nblocks), THREADS, shm, s>>>(pass_args(a, bpr), mt, (int)npass);
+    return check_launch("state_passing + bmm_chunk");
+}
+
+int launch_state_passing(const m2_state_passing_args& a, hipStream_t s) {
+    int rc;
+    if ((rc = check_state_passing_args(a))) return rc;
     if (a.out_dtype == M2_F32) return launch_typed<float>(a, s);
     if (a.out_dtype == M2_BF16) return launch_typed<bf16>(a, s);
     return set_error(M2_ERR_UNSUPPORTED, "state_passing: out dtype %d", a.out_dtype);

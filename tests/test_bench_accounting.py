@@ -60,11 +60,14 @@ def test_c0_fp32_stage_bytes_at_chunk_128():
     S = b * nc * H * P * N * 4                       # fp32 chunk states / passed states
     cb = b * nc * G * Q * Q * 4
     y = b * L * H * P * 4
+    final = b * H * P * N * 4
     w = bench.stage_work(configs.CONFIGS["c0"])
-    assert set(w) == {"chunk_cumsum+chunk_state", "state_passing", "bmm_chunk", "chunk_scan"}
+    assert set(w) == {"chunk_cumsum+chunk_state", "state_passing+bmm_chunk", "chunk_scan"}
     # chunk_cumsum inside chunk_state: dt, x, B in; dA_cumsum, dt', states out
     assert w["chunk_cumsum+chunk_state"][0] == dt + x + BC + 2 * rows + S
-    assert w["bmm_chunk"][0] == 2 * BC + cb
+    # state_passing (chunk states and chunk-end dA in; passed and final states
+    # out) and bmm_chunk (C, B in; CB out) in one launch
+    assert w["state_passing+bmm_chunk"][0] == 2 * S + b * H * nc * 4 + final + 2 * BC + cb
     assert w["chunk_scan"][0] == cb + x + 2 * rows + BC + S + 4 * H + y
     # flops of the chunk-128 algorithm: intra-chunk (k <= m) and carried-state terms
     assert w["chunk_scan"][1] == b * nc * H * P * Q * (Q + 1) + 2 * b * L * H * N * P
