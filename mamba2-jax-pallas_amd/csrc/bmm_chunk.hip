@@ -4,15 +4,10 @@
 // bf16 operands at the usual sizes take k_bmm_chunk_lds (one workgroup per
 // chunk and group, operands staged in LDS once), fp32 operands on shapes with
 // enough (chunk, group) blocks k_bmm_chunk_lds_f32 (the same, operands staged
-// as bf16 hi / lo planes, each product three MFMAs).  Otherwise: both operands are
-// K-contiguous in HBM ([.., L, G, K] rows), which is exactly
-// the per-lane layout MFMA wants, so every fragment is one 16-byte global load
-// (bf16) straight into VGPRs -- no LDS round trip.  A workgroup owns a 64 x 64
-// tile of one (b, c, g) block (64 x 32 or 64 x 16 when there are too few such
-// tiles to fill the CUs); each of its 4 wavefronts owns one 16-row tile and
-// the block's column tiles, with the K
-// loop unrolled so that several steps of loads are in flight.  Causal and
-// seq_idx masks are applied in the epilogue.
+// as bf16 hi / lo planes, each product three MFMAs).  Otherwise k_bmm_chunk:
+// 64 x (16 CT) output tiles with every fragment loaded straight into VGPRs
+// (the tile is bmm_tile.h's, which the fp32 combined forward also runs beside
+// state_passing in one launch).
 //
 // Follows reference kernels/bmm_chunk_fwd.py:87-154 (product), :348-372
 // (masks; positions past the end carry seq id -1) and ops/ssd_naive.py:189-216.
