@@ -127,18 +127,26 @@ def pass_bmm_fused(cfg):
 def cumsum_in_state(cfg):
     """The combined path runs chunk_cumsum inside the fp32 chunk_state kernel
     for fp32, headdim 64, dstate a multiple of 128 and chunk_size 64 / 128
-    (m2::chunk_state_cumsum_supported)."""
+    when the fused state pass does not apply (m2::chunk_state_cumsum_supported)."""
     return (cfg.dtype == "f32" and cfg.headdim == 64 and cfg.dstate % 128 == 0
-            and cfg.chunk_size in (64, 128) and cfg.nheads % cfg.ngroups == 0)
+            and cfg.chunk_size in (64, 128) and cfg.nheads % cfg.ngroups == 0
+            and not states_is_fused(cfg))
 
 
 def states_is_fused(cfg):
     """The combined path runs chunk_state and state_passing as one kernel for
-    bf16, headdim 64, dstate a multiple of 64 and chunk_size a multiple of 64 up
-    to 256 (m2::states_fused_supported)."""
-    return (cfg.dtype == "bf16" and cfg.headdim == 64 and cfg.dstate % 64 == 0
-            and cfg.chunk_size % 64 == 0 and cfg.chunk_size <= 256
-            and cfg.nheads % cfg.ngroups == 0)
+    headdim 64, dstate a multiple of 64 and chunk_size a multiple of 64 up to
+    256: always for bf16, for fp32 where the pass has at least 256 workgroups
+    (batch x heads x dstate / 64) or M2_F32_STATES=fused forces it
+    (m2::states_fused_supported)."""
+    shape = (cfg.headdim == 64 and cfg.dstate % 64 == 0 and cfg.chunk_size % 64 == 0
+             and cfg.chunk_size <= 256 and cfg.nheads % cfg.ngroups == 0)
+    if cfg.dtype == "bf16":
+        return shape
+    force = os.environ.get("M2_F32_STATES")
+    if not shape or force == "staged":
+        return False
+    return force == "fused" or cfg.batch * cfg.nheads * (cfg.dstate // 64) >= 256
 
 
 def scan_is_fused(cfg):

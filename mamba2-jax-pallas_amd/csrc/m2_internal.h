@@ -75,9 +75,14 @@ int launch_scan_fused(const m2_ssd_combined_args& a, const float* dA, const floa
 int ssd_combined_on(const m2_ssd_combined_args& a, void* ws, size_t ws_bytes, hipStream_t stream);
 
 // chunk_state + state_passing of the combined forward in one chunk-sequential
-// pass (bf16 inputs), from the weights / decay of launch_chunk_cumsum_ex;
-// writes the states entering each chunk (bf16) and the final states
+// pass, from the weights / decay of launch_chunk_cumsum_ex; writes the states
+// entering each chunk (in the input dtype) and the final states.  bf16 inputs
+// (csrc/ssd_states.hip), and fp32 inputs where the pass fills the CUs
+// (csrc/ssd_states_f32.hip; launch_states_fused dispatches on the dtype)
 bool states_fused_supported(const m2_ssd_combined_args& a);
 int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const float* scl,
                         void* states_passed, hipStream_t stream);
+bool states_fused_f32_supported(const m2_ssd_combined_args& a);
+int launch_states_fused_f32(const m2_ssd_combined_args& a, const float* wts, const float* scl,
+                            void* states_passed, hipStream_t stream);
 }  // namespace m2

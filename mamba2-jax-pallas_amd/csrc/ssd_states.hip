@@ -543,6 +543,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
 namespace m2 {
 
 bool states_fused_supported(const m2_ssd_combined_args& a) {
+    if (a.dtype == M2_F32) return states_fused_f32_supported(a);
     return a.dtype == M2_BF16 && a.headdim == P && a.dstate % NB == 0 &&
            a.chunk_size % 64 == 0 && a.chunk_size <= 256 && a.ngroups > 0 &&
            a.nheads % a.ngroups == 0;
@@ -576,6 +577,7 @@ StatesSplit states_split(const m2_ssd_combined_args& a) {
 
 int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const float* scl,
                         void* passed, hipStream_t s) {
+    if (a.dtype == M2_F32) return launch_states_fused_f32(a, wts, scl, passed, s);
     M2_REQUIRE(states_fused_supported(a), M2_ERR_UNSUPPORTED,
                "ssd_states: unsupported shape / dtype");
     StatesArgs sa{};

@@ -94,3 +94,54 @@ def test_more_than_one_gpu_is_refused():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def _workspace_bytes(cfg):
+    """m2_ssd_combined_workspace_size for cfg (host arithmetic only)."""
+    import ctypes
+    from mamba2_jax import _lib as L
+    a = L.SsdCombinedArgs(batch=cfg.batch, seqlen=cfg.seqlen, nheads=cfg.nheads,
+                          headdim=cfg.headdim, ngroups=cfg.ngroups, dstate=cfg.dstate,
+                          chunk_size=cfg.chunk_size, dtype=0 if cfg.dtype == "f32" else 1,
+                          dt_dtype=0 if cfg.dtype == "f32" else 1)
+    return L.load_library().m2_ssd_combined_workspace_size(ctypes.byref(a))
+
+
+def _expected_workspace(cfg, fused):
+    """The combined forward's workspace written out per slot: dA_cumsum and dt'
+    always; the weights and the chunk decay (fused state pass) or the fp32 chunk
+    states (staged); the states entering each chunk in the input dtype; CB
+    unless bmm_chunk runs inside the scan."""
+    al = lambda v: (v + 255) // 256 * 256
+    Q = bench.internal_chunk(cfg)
+    c = dataclasses.replace(cfg, chunk_size=Q)
+    es = 4 if cfg.dtype == "f32" else 2
+    nc = -(-cfg.seqlen // Q)
+    cq = cfg.batch * cfg.nheads * nc * Q
+    S = cfg.batch * nc * cfg.nheads * cfg.headdim * cfg.dstate
+    tot = 2 * al(4 * cq) + al(S * es)
+    tot += al(4 * cq) + al(4 * cfg.batch * cfg.nheads * nc) if fused else al(4 * S)
+    if not bench.scan_is_fused(c):
+        tot += al(es * cfg.batch * nc * cfg.ngroups * Q * Q)
+    return tot
+
+
+@pytest.mark.parametrize("name,dtype,force,fused", [
+    ("c2", "bf16", None, True),
+    ("c2", "f32", None, True),           # 256 workgroups: the fp32 fused state pass
+    ("c2", "f32", "staged", False),
+    ("c0", "f32", None, False),          # 48 workgroups: the staged kernels
+    ("c0", "f32", "fused", True),
+    ("c1", "bf16", None, True),
+])
+def test_state_pass_choice_matches_the_library(name, dtype, force, fused, monkeypatch):
+    """bench.states_is_fused (which names the stages the bench reports) agrees
+    with the library's own choice, read from the workspace it asks for."""
+    if force:
+        monkeypatch.setenv("M2_F32_STATES", force)
+    else:
+        monkeypatch.delenv("M2_F32_STATES", raising=False)
+    cfg = dataclasses.replace(configs.CONFIGS[name], dtype=dtype)
+    c = dataclasses.replace(cfg, chunk_size=bench.internal_chunk(cfg))
+    assert bench.states_is_fused(c) == fused
+    assert _workspace_bytes(cfg) == _expected_workspace(cfg, fused)

@@ -324,3 +324,65 @@ def test_fp32_cumsum_in_chunk_state(H, G, N, Q, L, packed):
     cfg = configs.SSDConfig("f32cs", 1, L, H, G, 64, N, Q, "f32", nseq=3 if packed else 0,
                             min_seqlen=64, seed=H + N + L)
     _run_and_check(cfg, with_z=True, Dhp=True, varlen=packed)
+
+
+# fp32 through the fused state pass (chosen from 256 workgroups up, forced by
+# M2_F32_STATES=fused on these smaller shapes): initial states, batch > 1,
+# ragged lengths, sequence resets with varlen states, dstate 64 / 256, chunk
+# 64 and 256 (run as 128), z and D per head-dim
+_F32_FUSED_CASES = {
+    "init_b2": configs.SSDConfig("f32fs", 2, 1024, 8, 2, 64, 128, 128, "f32", init_state=True, seed=41),
+    "ragged_q64": configs.SSDConfig("f32fs", 1, 5 * 64 - 19, 16, 4, 64, 128, 64, "f32", seed=42),
+    "n64_init": configs.SSDConfig("f32fs", 1, 256, 8, 1, 64, 64, 128, "f32", init_state=True, seed=43),
+    "seq_resets": configs.SSDConfig("f32fs", 1, 1536, 8, 2, 64, 128, 128, "f32", nseq=5, min_seqlen=100, seed=44),
+    "n256_q256": configs.SSDConfig("f32fs", 1, 777, 8, 2, 64, 256, 256, "f32", init_state=True, seed=45),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_F32_FUSED_CASES))
+def test_fp32_fused_state_pass(case, monkeypatch):
+    announce("fp32 fused state pass", case)
+    monkeypatch.setenv("M2_F32_STATES", "fused")
+    cfg = _F32_FUSED_CASES[case]
+    _run_and_check(cfg, with_z=True, Dhp=True, varlen=cfg.nseq > 0)
+
+
+def test_c2_full_fp32():
+    """The headline shape with fp32 inputs (the reference's published
+    conditions), where the fp32 fused state pass runs, against the oracle."""
+    announce("c2 full, fp32")
+    _run_and_check(dataclasses.replace(configs.CONFIGS["c2"], dtype="f32"))
+
+
+def test_fp32_fused_state_pass_graph_replays(monkeypatch):
+    """The fp32 fused state pass inside a captured combined forward: replays
+    equal the eager result bit for bit."""
+    announce("fp32 fused state pass, graph replays")
+    monkeypatch.setenv("M2_F32_STATES", "fused")
+    cfg = dataclasses.replace(configs.CONFIGS["c0"], seqlen=1000, init_state=True)
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, "f32")
+    for k in ("cu_seqlens", "seq_idx", "z"):
+        t.pop(k)
+    kw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True)
+    want = mamba_chunk_scan_combined_fwd(**t, **kw)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mamba_chunk_scan_combined_fwd(**t, **kw)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y, fin = mamba_chunk_scan_combined_fwd(**t, **kw)
+    for r in range(3):
+        y.fill_(float("nan"))
+        fin.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want[0]), f"replay {r}: out"
+        assert torch.equal(fin, want[1]), f"replay {r}: final_states"
+    ref = O.ssd_combined(io_dtype="f32", **dict(d, cu_seqlens=None, seq_idx=None, z=None), **kw)
+    check(want[0], ref[0], TOL["f32"], "out vs oracle")
+    check(want[1], ref[1], TOL["f32"], "final_states vs oracle")
