@@ -65,6 +65,7 @@ STATE_CFGS = [
     (2, 200, 8, 64, 128, 2, 64),     # L % Q != 0, batch 2, one-shot bf16 kernel
     (1, 100, 8, 64, 128, 2, 32),     # chunk 32, L % Q != 0
     (1, 4096, 128, 64, 128, 8, 128), # nemotron-h-8b layer shape
+    (1, 256, 6, 64, 128, 2, 128),    # 3 heads per group: one head per workgroup
 ]
 
 
@@ -316,6 +317,7 @@ def test_chunk_scan_large_decay_is_stable():
     (5, 8, 64, 64, 8, 64, "bf16", False),
     (6, 16, 64, 256, 8, 128, "bf16", False),     # c3-like
     (5, 8, 64, 128, 2, 256, "bf16", True),       # chunk 256, an empty sequence
+    (6, 8, 64, 128, 2, 128, "bf16", True),       # two heads per workgroup, an empty sequence
     (7, 4, 32, 64, 1, 64, "bf16", True),         # head dim 32 (general kernel)
 ])
 def test_chunk_state_varlen(nseq, H, P, N, G, Q, states_dtype, empty):
