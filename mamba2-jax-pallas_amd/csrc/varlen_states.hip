@@ -37,6 +37,9 @@
 //
 // Follows reference kernels/chunk_state_fwd.py:104-187 (product), :239-269
 // (weights, seq_idx rule) and :448-597 (varlen states).
+#include <stdlib.h>
+#include <string.h>
+
 #include "m2_internal.h"
 
 namespace {
@@ -251,8 +254,13 @@ __global__ void __launch_bounds__(256 * HPW) k_varlen_states(VarlenArgs a) {
 int block_cols(int64_t N) { return N % 128 == 0 ? 128 : 64; }
 
 // heads per workgroup: two (sharing the B rows) when a group's heads pair up
-// and the tiles of two heads leave room for two workgroups per CU (Q <= 128)
-int heads_per_wg(const VarlenArgs& k) { return (k.H / k.G) % 2 == 0 && k.Q <= 128 ? 2 : 1; }
+// and the tiles of two heads leave room for two workgroups per CU (Q <= 128),
+// else one; M2_ONESHOT_HEADS=1 forces one head (tests, A/B timing)
+int heads_per_wg(const VarlenArgs& k) {
+    const char* e = getenv("M2_ONESHOT_HEADS");
+    if (e && !strcmp(e, "1")) return 1;
+    return (k.H / k.G) % 2 == 0 && k.Q <= 128 ? 2 : 1;
+}
 
 template <bool CHUNK>
 int launch_k(VarlenArgs k, int64_t units, hipStream_t s, const char* who) {
