@@ -48,6 +48,7 @@
 // kernels/state_passing_fwd.py:108-151 (recurrence) and ops/ssd_naive.py:77-182.
 #include <stdlib.h>
 #include <string.h>
+#include <type_traits>
 
 #include "m2_internal.h"
 
@@ -205,116 +206,124 @@ __global__ void __launch_bounds__(THREADS) k_ssd_states(StatesArgs a) {
         return;
     }
 
-    // this half's K steps ks: tile rows (KB/2) kh + 32 ks + ...; the row swizzle
-    // repeats every 8 rows, so step ks is step 0 moved by 32 rows
-    const int rA = (KB / 2) * kh + 4 * kg + (ln >> 2);   // rows of MFMA k = 0..3 (+16: 4..7)
-    const int c1 = ln & 3;                         // 8-byte column group of the read
-    const int cb = 8 * (c1 & 1);
-    const int wpos = (KB / 2) * kh + (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // k index ln & 7
-    const int xo0 = rA * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
-    const int xo1 = (rA + 16) * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
-    int bo0[4], bo1[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
-        bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
-    }
-    // this wavefront's part of the tiles the other half sums; the sums of its
-    // own two tiles (columns 32 kh .. 32 kh + 31)
-    auto give = [&](int par) {
-        if (kh == 0) {
-            xchg[par][w][0][lane] = acc[2];
-            xchg[par][w][1][lane] = acc[3];
-        } else {
-            xchg[par][w][0][lane] = acc[0];
-            xchg[par][w][1][lane] = acc[1];
+    // The compute path, instantiated per position half (kh is uniform in a
+    // wavefront; as a compile-time constant the exchange's selects go away).
+    auto compute_half = [&](auto KHC) {
+        constexpr int kh = decltype(KHC)::value;
+        // this half's K steps ks: tile rows (KB/2) kh + 32 ks + ...; the row swizzle
+        // repeats every 8 rows, so step ks is step 0 moved by 32 rows
+        const int rA = (KB / 2) * kh + 4 * kg + (ln >> 2);   // rows of MFMA k = 0..3 (+16: 4..7)
+        const int c1 = ln & 3;                         // 8-byte column group of the read
+        const int cb = 8 * (c1 & 1);
+        const int wk = (KB / 2) * kh + 4 * kg;      // weight of k index 0 (4..7: 16 more)
+        const int xo0 = rA * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
+        const int xo1 = (rA + 16) * (2 * P) + (((2 * pw + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
+        int bo0[4], bo1[4];
+    #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bo0[j] = XB + rA * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA)) * 16) + cb;
+            bo1[j] = XB + (rA + 16) * (2 * NB) + (((2 * j + (c1 >> 1)) ^ swz(rA + 16)) * 16) + cb;
+        }
+        // this wavefront's part of the tiles the other half sums; the sums of its
+        // own two tiles (columns 32 kh .. 32 kh + 31)
+        auto give = [&](int par) {
+            if (kh == 0) {
+                xchg[par][w][0][lane] = acc[2];
+                xchg[par][w][1][lane] = acc[3];
+            } else {
+                xchg[par][w][0][lane] = acc[0];
+                xchg[par][w][1][lane] = acc[1];
+            }
+        };
+        auto take = [&](int par, f32x4& s0, f32x4& s1) {
+            const f32x4 o0 = xchg[par][w ^ 4][0][lane], o1 = xchg[par][w ^ 4][1][lane];
+            s0 = (kh == 0 ? acc[0] : acc[2]) + o0;
+            s1 = (kh == 0 ? acc[1] : acc[3]) + o1;
+        };
+        give(0);                                         // the parts of h_0
+        for (int s = 0; s < S; ++s) {
+            const int k = s % DEPTH;
+            const int c = s / SPC, kb = s - c * SPC;
+            lds_barrier();                               // slot k complete (load wavefront),
+                                                         // at chunk starts the second half's part
+            const char* slot = ring + k * SLOT;
+            const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
+            // h_c (sum of the halves) is the state entering chunk c: this half's
+            // two tiles of it are summed, rounded to bf16 and staged after the
+            // stage's MFMA steps are issued (whose latency hides the reads of the
+            // other half's part); both halves continue with h <- scl[c] h
+            f32x4 h0, h1;
+            if (kb == 0) {
+                take(c & 1, h0, h1);
+                const float sc = aux[KB];
+    #pragma unroll
+                for (int j = 0; j < 4; ++j)
+    #pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[j][r] *= sc;
+            }
+            // acc += B^T (w x) over this half's KB/2 positions.  In step ks, MFMA k
+            // index j < 4 is position (KB/2) kh + 32 ks + 4 kg + j, j >= 4 is 16 more.
+            // Lane j < 8 of each row reads the weight of k index j; the row shares them.
+            // every LDS operand of the stage is read first, so that the reads'
+            // latencies overlap (left to itself the scheduler reuses one register
+            // set and waits for each B fragment before its MFMAs)
+            float4 wa[C::KS], wb[C::KS];
+            bf16x4 xa[C::KS], xb[C::KS], ba[C::KS][4], bb[C::KS][4];
+    #pragma unroll
+            for (int ks = 0; ks < C::KS; ++ks) {
+                // the weights of the lane's k indices 0..3 and 4..7 (16 lanes read
+                // each address: broadcast reads, no lane moves)
+                wa[ks] = *reinterpret_cast<const float4*>(aux + wk + 32 * ks);
+                wb[ks] = *reinterpret_cast<const float4*>(aux + wk + 32 * ks + 16);
+                xa[ks] = ds_read_tr(slot + xo0 + ks * 32 * (2 * P));
+                xb[ks] = ds_read_tr(slot + xo1 + ks * 32 * (2 * P));
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    ba[ks][j] = ds_read_tr(slot + bo0[j] + ks * 32 * (2 * NB));
+                    bb[ks][j] = ds_read_tr(slot + bo1[j] + ks * 32 * (2 * NB));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+            for (int ks = 0; ks < C::KS; ++ks) {
+                const float wv[8] = {wa[ks].x, wa[ks].y, wa[ks].z, wa[ks].w, wb[ks].x, wb[ks].y, wb[ks].z, wb[ks].w};
+                // w x of the lane's 8 k indices as packed bf16 hi / lo pairs
+                typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+                const u2 pa = __builtin_bit_cast(u2, xa[ks]), pb = __builtin_bit_cast(u2, xb[ks]);
+                uint32_t h[4], l[4];
+                split2(bf16_lo(pa[0]) * wv[0], bf16_hi(pa[0]) * wv[1], h[0], l[0]);
+                split2(bf16_lo(pa[1]) * wv[2], bf16_hi(pa[1]) * wv[3], h[1], l[1]);
+                split2(bf16_lo(pb[0]) * wv[4], bf16_hi(pb[0]) * wv[5], h[2], l[2]);
+                split2(bf16_lo(pb[1]) * wv[6], bf16_hi(pb[1]) * wv[7], h[3], l[3]);
+                const bf16x8 xh = as_bf16x8(h[0], h[1], h[2], h[3]), xl = as_bf16x8(l[0], l[1], l[2], l[3]);
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bf16x8 bf = __builtin_shufflevector(ba[ks][j], bb[ks][j], 0, 1, 2, 3, 4, 5, 6, 7);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
+                }
+            }
+            if (kb == 0) {
+                // lane (ln, kg): 4 columns of staging row ln
+                bf16* pr = &pst[c & 1][pw][ln][32 * kh + 4 * kg];
+                const bf16x4 o0 = {(bf16)h0[0], (bf16)h0[1], (bf16)h0[2], (bf16)h0[3]};
+                const bf16x4 o1 = {(bf16)h1[0], (bf16)h1[1], (bf16)h1[2], (bf16)h1[3]};
+                *reinterpret_cast<bf16x4*>(pr) = o0;
+                *reinterpret_cast<bf16x4*>(pr + 16) = o1;
+            }
+            if ((s + 1) % SPC == 0) give((c + 1) & 1);  // the end of chunk c: parts of h_{c+1}
+        }
+        __syncthreads();
+        if (a.fin) {
+            f32x4 s0, s1;
+            take(nc & 1, s0, s1);
+            const int n = NB * nb + 32 * kh + 4 * kg;
+            *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n) = make_float4(s0[0], s0[1], s0[2], s0[3]);
+            *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n + 16) = make_float4(s1[0], s1[1], s1[2], s1[3]);
         }
     };
-    auto take = [&](int par, f32x4& s0, f32x4& s1) {
-        const f32x4 o0 = xchg[par][w ^ 4][0][lane], o1 = xchg[par][w ^ 4][1][lane];
-        s0 = (kh == 0 ? acc[0] : acc[2]) + o0;
-        s1 = (kh == 0 ? acc[1] : acc[3]) + o1;
-    };
-    give(0);                                         // the parts of h_0
-    for (int s = 0; s < S; ++s) {
-        const int k = s % DEPTH;
-        const int c = s / SPC, kb = s - c * SPC;
-        lds_barrier();                               // slot k complete (load wavefront),
-                                                     // at chunk starts the second half's part
-        const char* slot = ring + k * SLOT;
-        const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
-        // h_c (sum of the halves) is the state entering chunk c: this half's
-        // two tiles of it are summed, rounded to bf16 and staged after the
-        // stage's MFMA steps are issued (whose latency hides the reads of the
-        // other half's part); both halves continue with h <- scl[c] h
-        f32x4 h0, h1;
-        if (kb == 0) {
-            take(c & 1, h0, h1);
-            const float sc = aux[KB];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[j][r] *= sc;
-        }
-        // acc += B^T (w x) over this half's KB/2 positions.  In step ks, MFMA k
-        // index j < 4 is position (KB/2) kh + 32 ks + 4 kg + j, j >= 4 is 16 more.
-        // Lane j < 8 of each row reads the weight of k index j; the row shares them.
-        // every LDS operand of the stage is read first, so that the reads'
-        // latencies overlap (left to itself the scheduler reuses one register
-        // set and waits for each B fragment before its MFMAs)
-        float wl[C::KS];
-        bf16x4 xa[C::KS], xb[C::KS], ba[C::KS][4], bb[C::KS][4];
-#pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
-            wl[ks] = aux[wpos + 32 * ks];
-            xa[ks] = ds_read_tr(slot + xo0 + ks * 32 * (2 * P));
-            xb[ks] = ds_read_tr(slot + xo1 + ks * 32 * (2 * P));
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ba[ks][j] = ds_read_tr(slot + bo0[j] + ks * 32 * (2 * NB));
-                bb[ks][j] = ds_read_tr(slot + bo1[j] + ks * 32 * (2 * NB));
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
-            const float w0 = wl[ks];
-            const float wv[8] = {row_bcast<0>(w0), row_bcast<1>(w0), row_bcast<2>(w0), row_bcast<3>(w0),
-                                 row_bcast<4>(w0), row_bcast<5>(w0), row_bcast<6>(w0), row_bcast<7>(w0)};
-            // w x of the lane's 8 k indices as packed bf16 hi / lo pairs
-            typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
-            const u2 pa = __builtin_bit_cast(u2, xa[ks]), pb = __builtin_bit_cast(u2, xb[ks]);
-            uint32_t h[4], l[4];
-            split2(bf16_lo(pa[0]) * wv[0], bf16_hi(pa[0]) * wv[1], h[0], l[0]);
-            split2(bf16_lo(pa[1]) * wv[2], bf16_hi(pa[1]) * wv[3], h[1], l[1]);
-            split2(bf16_lo(pb[0]) * wv[4], bf16_hi(pb[0]) * wv[5], h[2], l[2]);
-            split2(bf16_lo(pb[1]) * wv[6], bf16_hi(pb[1]) * wv[7], h[3], l[3]);
-            const bf16x8 xh = as_bf16x8(h[0], h[1], h[2], h[3]), xl = as_bf16x8(l[0], l[1], l[2], l[3]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bf16x8 bf = __builtin_shufflevector(ba[ks][j], bb[ks][j], 0, 1, 2, 3, 4, 5, 6, 7);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xh, acc[j], 0, 0, 0);
-                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
-            }
-        }
-        if (kb == 0) {
-            // lane (ln, kg): 4 columns of staging row ln
-            bf16* pr = &pst[c & 1][pw][ln][32 * kh + 4 * kg];
-            const bf16x4 o0 = {(bf16)h0[0], (bf16)h0[1], (bf16)h0[2], (bf16)h0[3]};
-            const bf16x4 o1 = {(bf16)h1[0], (bf16)h1[1], (bf16)h1[2], (bf16)h1[3]};
-            *reinterpret_cast<bf16x4*>(pr) = o0;
-            *reinterpret_cast<bf16x4*>(pr + 16) = o1;
-        }
-        if ((s + 1) % SPC == 0) give((c + 1) & 1);  // the end of chunk c: parts of h_{c+1}
-    }
-    __syncthreads();
-    if (a.fin) {
-        f32x4 s0, s1;
-        take(nc & 1, s0, s1);
-        const int n = NB * nb + 32 * kh + 4 * kg;
-        *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n) = make_float4(s0[0], s0[1], s0[2], s0[3]);
-        *reinterpret_cast<float4*>(a.fin + hoff + (int64_t)prow * N + n + 16) = make_float4(s1[0], s1[1], s1[2], s1[3]);
-    }
+    if (kh == 0) compute_half(std::integral_constant<int, 0>());
+    else compute_half(std::integral_constant<int, 1>());
 }
 
 // 16-byte chunk swizzle of a tile row R: 128-byte rows read at one chunk pair
