@@ -474,7 +474,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
     const int rA = 4 * kg + (ln >> 2);
     const int c1 = ln & 3;                           // 8-byte column group of the read
     const int cb = 8 * (c1 & 1);
-    const int wpos = (ln & 4 ? 16 : 0) + 4 * kg + (ln & 3);   // row of k index ln & 7
+    const int wk = 4 * kg;                           // row of k index 0 (4..7: 16 more)
     const int xch = 8 * hh + 2 * pw + (c1 >> 1);     // 16-byte chunk of the x row
     const int xo0 = rA * C::XROW + ((xch ^ rswz<C::XROW>(rA)) * 16) + cb;
     const int xo1 = (rA + 16) * C::XROW + ((xch ^ rswz<C::XROW>(rA + 16)) * 16) + cb;
@@ -492,11 +492,13 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
         const float* aux = reinterpret_cast<const float*>(slot + XB + BB);
         // every LDS operand of the stage is read first, so that the reads'
         // latencies overlap
-        float wl[C::KS];
+        float4 wa[C::KS], wb[C::KS];
         bf16x4 xa[C::KS], xb[C::KS], ba[C::KS][NT], bb[C::KS][NT];
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-            wl[ks] = aux[hh * KB + wpos + 32 * ks];
+            // the weights of the lane's k indices 0..3 and 4..7 (broadcast reads)
+            wa[ks] = *reinterpret_cast<const float4*>(aux + hh * KB + wk + 32 * ks);
+            wb[ks] = *reinterpret_cast<const float4*>(aux + hh * KB + wk + 32 * ks + 16);
             xa[ks] = ds_read_tr(slot + xo0 + ks * 32 * C::XROW);
             xb[ks] = ds_read_tr(slot + xo1 + ks * 32 * C::XROW);
 #pragma unroll
@@ -519,9 +521,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
         // so the weighted operand keeps near-fp32 accuracy
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-            const float w0 = wl[ks];
-            const float wv[8] = {row_bcast<0>(w0), row_bcast<1>(w0), row_bcast<2>(w0), row_bcast<3>(w0),
-                                 row_bcast<4>(w0), row_bcast<5>(w0), row_bcast<6>(w0), row_bcast<7>(w0)};
+            const float wv[8] = {wa[ks].x, wa[ks].y, wa[ks].z, wa[ks].w, wb[ks].x, wb[ks].y, wb[ks].z, wb[ks].w};
             typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
             const u2 pa = __builtin_bit_cast(u2, xa[ks]), pb = __builtin_bit_cast(u2, xb[ks]);
             uint32_t hi[4], lo[4];
