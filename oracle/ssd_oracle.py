@@ -375,12 +375,18 @@ def ssd_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
                  initial_states=None, seq_idx=None, cu_seqlens=None,
                  dt_softplus=False, dt_limit=(0.0, INF),
                  return_final_states=False, return_varlen_states=False,
-                 io_dtype="f32", pad="kernel", decay_clamp=False, acc=np.float64):
+                 io_dtype="f32", pad="kernel", decay_clamp=False, acc=np.float64,
+                 passed_jitter=0.0, jitter_seed=0):
     """The five-stage SSD forward with the reference's return arity.
 
     ``io_dtype`` names the dtype of x/B/C ('f32' or 'bf16'); the inputs must
     already hold values of that dtype.  It selects the rounding applied where
     the reference casts to C.dtype.  ``decay_clamp``: see chunk_state.
+    ``passed_jitter`` (tests only) multiplies the passed states by
+    1 + passed_jitter * N(0, 1) (seed ``jitter_seed``) before their rounding to
+    C.dtype: with a jitter far below any fp32 summation-order difference, the
+    change it causes measures how far one rounding flip at that point (which
+    the reference makes, kernels/ssd_combined.py:140) moves the results.
     """
     rf = round_fn_for(io_dtype)
     b, L, H, P = np.shape(x)
@@ -396,7 +402,10 @@ def ssd_combined(x, dt, A, B, C, chunk_size, D=None, z=None, dt_bias=None,
     sp, fin = state_passing(st.reshape(b, nc, H, P * N), dA[:, :, :, -1],
                             initial_states=init, seq_idx=seq_idx,
                             chunk_size=chunk_size, acc=acc)
-    sp = rf(sp.reshape(b, nc, H, P, N))          # out_dtype = C.dtype
+    sp = sp.reshape(b, nc, H, P, N)
+    if passed_jitter:
+        sp = sp * (1.0 + passed_jitter * np.random.default_rng(jitter_seed).standard_normal(sp.shape))
+    sp = rf(sp)                                  # out_dtype = C.dtype
     fin = fin.reshape(b, H, P, N)
     CB = bmm_chunk(C, B, chunk_size, seq_idx=seq_idx, round_fn=rf, acc=acc)
     out, _ = chunk_scan(CB, x, dto, dA, C, sp, D=D, z=z, seq_idx=seq_idx,

@@ -406,3 +406,28 @@ def test_bf16_rounding_points_are_small_but_present():
     e = O.rel_err(y1, y0)
     assert 1e-5 < e < 2e-2
     assert O.rel_err(f1, f0) == 0.0   # final states stay fp32
+
+
+def test_passed_jitter_is_a_measurement_knob_only():
+    """passed_jitter (a test-only knob of the oracle) leaves results untouched
+    at 0, and in fp32 (no rounding of the passed states) moves them by about
+    the jitter itself: it perturbs the passed states and nothing else."""
+    rng = np.random.default_rng(5)
+    b, L, H, G, P, N, Q = 1, 96, 2, 1, 8, 16, 32
+    x = rng.standard_normal((b, L, H, P)).astype(np.float32)
+    dt = (0.1 * rng.random((b, L, H))).astype(np.float32)
+    A = -rng.uniform(0.5, 2.0, H).astype(np.float32)
+    B = rng.standard_normal((b, L, G, N)).astype(np.float32)
+    C = rng.standard_normal((b, L, G, N)).astype(np.float32)
+    seq = np.repeat([0, 1], [40, 56])[None].astype(np.int32)
+    cu = np.array([0, 40, 96], np.int32)
+    kw = dict(chunk_size=Q, seq_idx=seq, cu_seqlens=cu, return_final_states=True,
+              return_varlen_states=True)
+    base = O.ssd_combined(x, dt, A, B, C, **kw)
+    same = O.ssd_combined(x, dt, A, B, C, **kw, passed_jitter=0.0, jitter_seed=7)
+    for a, c in zip(base, same):
+        assert np.array_equal(a, c)
+    jit = O.ssd_combined(x, dt, A, B, C, **kw, passed_jitter=1e-6, jitter_seed=7)
+    assert 0 < O.rel_err(jit[2], base[2]) < 1e-5        # varlen states use the passed states
+    assert O.rel_err(jit[0], base[0]) < 1e-5            # so do the outputs
+    assert np.array_equal(jit[1], base[1])              # the final states do not
