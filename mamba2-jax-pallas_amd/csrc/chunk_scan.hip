@@ -70,7 +70,11 @@ template <int KPL> M2_DEV void load_cb(const bf16* p, float* v) {
     }
 }
 
-template <typename T, typename TCB, int PT>
+// SG: the carried state is read from global memory (an L2-resident 32 KB per
+// head and chunk at head dim 128) instead of staged in LDS, for the shapes
+// whose x tile and state together exceed the LDS (fp32, head dim 128, chunk
+// 256); needs the state in x's dtype.
+template <typename T, typename TCB, int PT, bool SG>
 __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
     typedef MF<T> M;
     constexpr int KPL = M::KPL;
@@ -80,7 +84,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
     const int SX = P + ScanPad<T>::x, SS = N + ScanPad<T>::s;
     T* xs = reinterpret_cast<T*>(smem);                  // [Q][SX]
     T* ss = xs + Q * SX;                                  // [P][SS]
-    float* dAs = reinterpret_cast<float*>(ss + P * SS);   // [Q]
+    float* dAs = reinterpret_cast<float*>(ss + (SG ? 0 : P * SS));   // [Q]
     float* dts = dAs + Q;                                 // [Q]
     int* seqs = reinterpret_cast<int*>(dts + Q);          // [Q] (seq_idx only)
 
@@ -114,8 +118,8 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
             d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
         }
     }
-    {
-        const int64_t soff = (((int64_t)bi * nc + c) * H + h) * (int64_t)P * N;
+    const int64_t soff = (((int64_t)bi * nc + c) * H + h) * (int64_t)P * N;
+    if (!SG) {
         if (a.states_same) {
             constexpr int VE = 16 / sizeof(T);
             const T* src = reinterpret_cast<const T*>(a.states) + soff;
@@ -175,7 +179,9 @@ __global__ void __launch_bounds__(THREADS) k_chunk_scan(ScanArgs a) {
 #pragma unroll
                     for (int pt = 0; pt < PT; ++pt) {
                         const typename M::frag bfr =
-                            load_frag(ss + (pt * 16 + ln) * SS + k + kg * KPL);
+                            SG ? load_frag(reinterpret_cast<const T*>(a.states) + soff +
+                                           (int64_t)(pt * 16 + ln) * N + k + kg * KPL)
+                               : load_frag(ss + (pt * 16 + ln) * SS + k + kg * KPL);
                         acc[pt] = M::mma(af, bfr, acc[pt]);
                     }
                 }
@@ -535,14 +541,16 @@ int launch_f32(const ScanArgs& sa, hipStream_t s) {
 
 template <typename T, typename TCB>
 int launch_typed(const ScanArgs& sa, hipStream_t s) {
-    const size_t shm = (size_t)sa.Q * (sa.P + ScanPad<T>::x) * sizeof(T) +
-                       (size_t)sa.P * (sa.N + ScanPad<T>::s) * sizeof(T) +
-                       (size_t)sa.Q * 3 * sizeof(float);
+    const size_t xb = (size_t)sa.Q * (sa.P + ScanPad<T>::x) * sizeof(T) + (size_t)sa.Q * 3 * sizeof(float);
+    const size_t sb = (size_t)sa.P * (sa.N + ScanPad<T>::s) * sizeof(T);
+    // the state from global memory when x tile + state exceed the LDS
+    const bool sg = xb + sb > 160 * 1024 && sa.states_same;
+    const size_t shm = sg ? xb : xb + sb;
     void (*kern)(ScanArgs) = nullptr;
     switch (sa.P) {
-        case 32: kern = k_chunk_scan<T, TCB, 2>; break;
-        case 64: kern = k_chunk_scan<T, TCB, 4>; break;
-        case 128: kern = k_chunk_scan<T, TCB, 8>; break;
+        case 32: kern = sg ? k_chunk_scan<T, TCB, 2, true> : k_chunk_scan<T, TCB, 2, false>; break;
+        case 64: kern = sg ? k_chunk_scan<T, TCB, 4, true> : k_chunk_scan<T, TCB, 4, false>; break;
+        case 128: kern = sg ? k_chunk_scan<T, TCB, 8, true> : k_chunk_scan<T, TCB, 8, false>; break;
         default:
             return m2::set_error(M2_ERR_UNSUPPORTED,
                                  "chunk_scan: headdim %d not supported (32, 64, 128)", sa.P);

@@ -60,6 +60,13 @@ def selective_state_update(state, x, dt, A, B, C, D=None, z=None, dt_bias=None,
         bias_has_hdim = int(dt_bias.dim() == 2)
         L.require(tuple(dt_bias.shape) == ((nheads, headdim) if bias_has_hdim else (nheads,)),
                   f"dt_bias.shape={tuple(dt_bias.shape)}")
+        # the reference adds them by broadcasting (ops/selective_state_update.py:72),
+        # which aligns heads only for dt (b, H) + dt_bias (H,) and dt (b, H, P) +
+        # dt_bias (H, P); the mixed pairs fail there (or misalign when sizes coincide)
+        L.require(bias_has_hdim == dt_has_hdim,
+                  f"dt.shape={tuple(dt.shape)} with dt_bias.shape={tuple(dt_bias.shape)}: "
+                  "pass dt (batch, nheads) with dt_bias (nheads,), or dt (batch, nheads, headdim) "
+                  "with dt_bias (nheads, headdim)")
     if z is not None:
         L.require(tuple(z.shape) == tuple(x.shape), "z.shape != x.shape")
 

@@ -182,3 +182,16 @@ def test_reference_usage_pattern(with_extras):
         ref_out = (ref_out + D[None, :, None] * x) * torch.nn.functional.silu(z)
     assert (new - ref_state).abs().max().item() < 1e-5
     assert (out - ref_out).abs().max().item() < (1e-4 if with_extras else 1e-5)
+
+
+def test_mixed_dt_and_bias_layouts_are_rejected():
+    """dt (b, H) with dt_bias (H, P), or dt (b, H, P) with dt_bias (H,): the
+    reference adds dt and dt_bias by broadcasting (ops/selective_state_update.py
+    :72), which fails for these pairs (or misaligns heads when sizes coincide);
+    the drop-in raises."""
+    from mamba2_jax._lib import M2ShapeError
+    rng = np.random.default_rng(3)
+    for dt_hdim, bias_hdim in ((False, True), (True, False)):
+        d = _step_inputs(rng, 2, 4, 2, 32, 64, dt_hdim=dt_hdim, bias_hdim=bias_hdim)
+        with pytest.raises(M2ShapeError):
+            selective_state_update(**_dev(d), dt_softplus=True)

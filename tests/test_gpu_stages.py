@@ -212,6 +212,7 @@ SCAN_CFGS = [
     (1, 384, 8, 64, 256, 8, 128, True, False, None),
     (1, 300, 4, 32, 64, 2, 128, True, True, None),        # L % Q != 0, headdim 32
     (1, 256, 4, 128, 64, 1, 64, True, False, None),       # headdim 128
+    (1, 300, 4, 128, 128, 2, 256, True, True, None),      # headdim 128, chunk 256 (fp32: state read from L2)
     (2, 512, 8, 64, 64, 1, 64, False, False, [[200, 312], [100, 412]]),
     (2, 512, 8, 64, 64, 4, 128, True, True, [[256, 256], [128, 384]]),
 ]
