@@ -134,7 +134,7 @@ def test_conv_paths(case):
     got = causal_conv1d(xt, dev(w, wdt), dev(bias, bdt), act,
                         None if seq is None else dev(seq))
     assert NAME[got.dtype] == rdt
-    if layout == "cl":
+    if layout == "cl" and d > 1:   # (one channel: both layouts are the same memory order)
         assert got.stride(1) == 1, "the result keeps the channels-last layout"
     _close(got, want, rdt == "bfloat16", f"{layout} k={k}", _mag(x, w, bias))
 
@@ -274,3 +274,25 @@ def test_errors():
         causal_conv1d(x, torch.zeros((5, 3), device="cuda"))      # d mismatch
     with pytest.raises(ValueError):
         causal_conv1d(x.cpu(), torch.zeros((4, 3)))               # no CPU path
+
+
+def _sweep_cases(n=24, seed=91):
+    """Cases of test_conv_paths' form drawn once from a fixed seed: 1-3 rows,
+    1-96 channels, 1-400 tokens, widths 1-8, every layout, mixed dtypes, bias,
+    silu and sequence resets on and off."""
+    rng = np.random.default_rng(seed)
+    tys = ("bf16", "f32")
+    out = []
+    for _ in range(n):
+        L = int(rng.integers(1, 401))
+        out.append((int(rng.integers(1, 4)), int(rng.integers(1, 97)), L, int(rng.integers(1, 9)),
+                    str(rng.choice(["cl", "cf", "strided"])),
+                    tuple(str(rng.choice(tys)) for _ in range(3)), bool(rng.random() < 0.7),
+                    "silu" if rng.random() < 0.6 else None,
+                    min(int(rng.integers(0, 6)), L)))
+    return out
+
+
+@pytest.mark.parametrize("case", _sweep_cases())
+def test_conv_sweep(case):
+    test_conv_paths(case)

@@ -141,3 +141,26 @@ def test_residual_add_fused(hidden, xdt):
     assert np.array_equal(host(rt), (res + x.astype(np.float32)).astype(np.float64)), "residual += x in f32"
     want, _ = X.rms_norm_gated(summed.astype(np.float32), w, w_dtype="bfloat16")
     _close(got, bf16_round(want), True, "add + norm, bf16 store")
+
+
+def _sweep_cases(n=20, seed=92):
+    """Cases of test_norm_cases' form drawn once from a fixed seed: 1-3 leading
+    dims, 1-8 groups of 1-1500 elements (or one group), mixed dtypes, z on and
+    off, the norm before or after the gate."""
+    rng = np.random.default_rng(seed)
+    tys = ("bf16", "f32")
+    out = []
+    for _ in range(n):
+        gs = int(rng.integers(1, 1501))
+        ng = int(rng.integers(1, 9))
+        lead = tuple(int(v) for v in rng.integers(1, 5, int(rng.integers(1, 3))))
+        with_z = bool(rng.random() < 0.7)
+        out.append((lead + (gs * ng,), gs if rng.random() < 0.7 else None,
+                    (str(rng.choice(tys)), str(rng.choice(tys)) if with_z else None, str(rng.choice(tys))),
+                    with_z, bool(rng.random() < 0.5)))
+    return out
+
+
+@pytest.mark.parametrize("case", _sweep_cases())
+def test_norm_sweep(case):
+    test_norm_cases(case)
