@@ -182,15 +182,23 @@ class MixerDims:
         return self.d_ssm + 2 * self.ngroups * self.d_state
 
 
-def _proj(h, p, name):
+def _proj(h, p, name, out_dtype=None):
     """h @ p[name + "_kernel"] (+ bias).  A decode-sized h (<= 16 rows) with a
     K-contiguous bf16 copy p[name + "_t"] ([out, in], prepared by the caller)
-    runs the HIP skinny GEMM; anything else is a torch matmul (hipBLASLt)."""
+    runs the HIP skinny GEMM; anything else is a torch matmul (hipBLASLt).
+    out_dtype=torch.float32 with bf16 operands keeps the float32 accumulation
+    as the result (no rounding to bf16)."""
     wt, b = p.get(name + "_t"), p.get(name + "_bias")
     if wt is not None and h.dim() == 2 and _lin.preferred(h, wt):
-        return _lin.linear_skinny(h, wt, b, out_dtype=wt.dtype)
-    z = h @ p[name + "_kernel"]
-    return z if b is None else z + b
+        return _lin.linear_skinny(h, wt, b, out_dtype=out_dtype or wt.dtype)
+    w = p[name + "_kernel"]
+    if out_dtype == torch.float32 and h.dtype == torch.bfloat16 and w.dtype == torch.bfloat16:
+        z = torch.mm(h.reshape(-1, h.shape[-1]), w, out_dtype=torch.float32)
+        z = z.reshape(*h.shape[:-1], w.shape[-1])
+    else:
+        z = h @ w
+    z = z if b is None else z + b
+    return z if out_dtype is None else z.to(out_dtype)
 
 
 def _in_proj(h, p):
@@ -199,14 +207,17 @@ def _in_proj(h, p):
 
 def _mixer_out(y, z, z0, x0, p, d):
     """gated RMSNorm, the MLP bypass, out-projection (reference :400-414).
-    Without the MLP bypass the norm stores straight in the projection's dtype."""
+    Without the MLP bypass the norm stores straight in the projection's dtype.
+    The result is float32, as the reference's: its SSD output, and so the
+    norm's, is float32, and a float32 activation times a bf16 kernel promotes
+    to float32 (the activation itself goes to the bf16 GEMM in bf16)."""
     if d.rmsnorm:
         y = rms_norm_gated(y, p["norm_weight"], z=z, group_size=d.d_ssm // d.ngroups,
                            norm_before_gate=d.norm_before_gate,
                            out_dtype=p["out_proj_kernel"].dtype if d.d_mlp == 0 else None)
     if d.d_mlp > 0:
         y = torch.cat([torch.nn.functional.silu(z0) * x0, y.to(x0.dtype)], dim=-1)
-    return _proj(y.to(p["out_proj_kernel"].dtype), p, "out_proj")
+    return _proj(y.to(p["out_proj_kernel"].dtype), p, "out_proj", out_dtype=torch.float32)
 
 
 def _A(p):
@@ -303,8 +314,9 @@ def mamba2_block_step_fused(res, norm_weight, p, d, conv_state, ssm_state, eps=1
     """One decode token of a pre-norm residual block, res += mixer(rmsnorm(res))
     (reference models/mamba2_lm.py:205-211 around modules/mamba2.py:427-549),
     in four kernels: the block's RMSNorm runs in the in-projection's prologue,
-    the gated norm in the out-projection's, whose epilogue adds the output
-    (rounded to bf16, the projection's dtype) into res.  res (batch, d_model)
+    the gated norm in the out-projection's, whose epilogue adds the float32
+    output (the reference's promotion of a float32 activation times a bf16
+    kernel) into res.  res (batch, d_model)
     float32 and the states are updated in place; block_step_fusable must hold.
     The results equal mamba2_block_step's around rms_norm up to the rounding
     of the norms' sums of squares (summed in another order)."""
@@ -330,7 +342,7 @@ def mamba2_block_step_fused(res, norm_weight, p, d, conv_state, ssm_state, eps=1
         D=_D(p, d), dt_bias=p["dt_bias"], dt_softplus=True, inplace=True)
     _lin.linear_norm(y.view(batch, d.d_ssm), p["norm_weight"], p["out_proj_t"], z=z,
                      group_size=d.d_ssm // G, norm_before_gate=d.norm_before_gate,
-                     bias=p.get("out_proj_bias"), out_dtype=p["out_proj_t"].dtype, residual=res,
+                     bias=p.get("out_proj_bias"), out_dtype=torch.float32, residual=res,
                      store=False)
     return res, conv_state, ssm_state
 

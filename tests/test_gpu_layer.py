@@ -184,6 +184,9 @@ def test_layer_sweep(case):
     b, T0, T1 = int(rng.integers(1, 4)), int(rng.integers(1, 160)), 6
     u = dev(rng.standard_normal((b, T0 + T1, c["d_model"])).astype(np.float32), pd)
     full = m(u)
+    # float32 out, as the reference's layer (its float32 SSD output times the
+    # out-projection kernel promotes to float32, modules/mamba2.py:405-415)
+    assert full.dtype == torch.float32, full.dtype
     tol = TOL["bf16" if bf16 else "f32"]
     want, _, _ = X.mamba2_layer(_params(m), host(u), _cfg(m), dtype="bfloat16" if bf16 else "float32")
     exact = X.mamba2_layer(_params(m), host(u), _cfg(m))[0] if bf16 else want
@@ -196,8 +199,9 @@ def test_layer_sweep(case):
     outs = []
     for t in range(T0, T0 + T1):
         o, cache = m(u[:, t:t + 1], inference_params=cache, inplace=True)
+        assert o.dtype == torch.float32, o.dtype
         outs.append(o)
-    # bf16 decode: besides the bf16 GEMM inputs and outputs of the prefill, the
+    # bf16 decode: besides the bf16 GEMM inputs of the prefill, the
     # step rounds the conv output (x, B, C) to bf16 where the reference's float32
     # conv state promotes it to float32 (modules/mamba2.py:470-480); the layer's
     # bf16 choices (deliberate, for the bf16 GEMMs) then leave the step's outputs
