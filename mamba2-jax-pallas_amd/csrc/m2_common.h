@@ -165,7 +165,17 @@ M2_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); 
 // workgroup release/acquire fence and waits for every outstanding global load
 // and store (vmcnt(0)); barriers that only hand LDS tiles between wavefronts
 // use this one so that prefetches and output stores stay in flight.
-M2_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// The wait is also issued through the builtin (0xc07f: lgkmcnt(0), vmcnt and
+// expcnt left at their maxima), which the compiler's wait insertion sees: the
+// asm one alone leaves it believing that earlier scalar loads (which complete
+// out of order) and LDS accesses are still pending past the barrier, so its
+// next LDS wait drains every read in flight instead of waiting for the one it
+// needs.  The asm wait stays next to the barrier, where it orders the LDS
+// accesses.
+M2_DEV void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
 
