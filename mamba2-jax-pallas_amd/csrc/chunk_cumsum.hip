@@ -42,53 +42,68 @@ struct CumsumArgs {
     float lo, hi;
 };
 
-// PPL: positions per lane (Q <= 64 PPL)
-template <typename TD, int PPL>
+// PPL: positions per lane (Q <= 64 PPL); CPW: chunks per workgroup (1, or 2
+// where one chunk per workgroup would need more than one round of the CUs:
+// all loads of both chunks go out before the first wait, so the two load
+// round trips overlap instead of following each other)
+template <typename TD, int PPL, int CPW>
 __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
-    __shared__ float tile[QMAX][HB + 1];       // dt of the chunk, [position][head]
+    __shared__ float tile[CPW][QMAX][HB + 1];  // dt of the chunks, [position][head]
     // the head blocks of one (batch, chunk) read the same dt rows: they share
     // an XCD (and its L2)
     const int work = xcd_remap(blockIdx.x, a.nblocks);
-    const int hb = work % a.nhb, c = (work / a.nhb) % a.nc, bi = work / (a.nhb * a.nc);
+    const int ncw = (a.nc + CPW - 1) / CPW;
+    const int hb = work % a.nhb, cw = (work / a.nhb) % ncw, bi = work / (a.nhb * ncw);
     const int Q = a.Q, L = a.L, H = a.H;
-    const int qhi = min(Q, L - c * Q);              // valid positions of the chunk
-    const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
-
     const int lane = threadIdx.x & 63, w = wave_id();
     const int h = hb * HB + w;
     // every global load of the workgroup is issued before the first wait:
-    // the head's A / bias and the chunk's seq ids, then the dt tile
+    // the head's A / bias and the chunks' seq ids, then the dt tiles
     const float Ah = a.A[min(h, H - 1)];
     const float bias = a.bias ? a.bias[min(h, H - 1)] : 0.f;
-    int sq[PPL];
-    int se = 0, sprev = 0;
-    if (a.seq) {
+    int sq[CPW][PPL];
+    int se[CPW], sprev[CPW];
+    const int hh = threadIdx.x % HB, r0 = threadIdx.x / HB;
+    TD raw[CPW][PPL];
 #pragma unroll
-        for (int j = 0; j < PPL; ++j) sq[j] = a.seq[tok0 + min(lane + 64 * j, qhi - 1)];
-        se = a.seq[tok0 + qhi - 1];
-        if (c > 0) sprev = a.seq[tok0 - 1];
-    }
-    // ---- coalesced tile load: thread t -> head t % 16, rows t / 16 + 64 i;
-    // addresses clamped into the valid rows / heads (masked below)
-    {
-        const int hh = threadIdx.x % HB, r0 = threadIdx.x / HB;
+    for (int k = 0; k < CPW; ++k) {
+        // a workgroup's second chunk past the last one repeats the last (its
+        // loads stay in bounds; it stores nothing)
+        const int c = min(cw * CPW + k, a.nc - 1);
+        const int qhi = min(Q, L - c * Q);          // valid positions of the chunk
+        const int64_t tok0 = (int64_t)bi * L + (int64_t)c * Q;
+        se[k] = 0; sprev[k] = 0;
+        if (a.seq) {
+#pragma unroll
+            for (int j = 0; j < PPL; ++j) sq[k][j] = a.seq[tok0 + min(lane + 64 * j, qhi - 1)];
+            se[k] = a.seq[tok0 + qhi - 1];
+            if (c > 0) sprev[k] = a.seq[tok0 - 1];
+        }
+        // ---- coalesced tile load: thread t -> head t % 16, rows t / 16 + 64 i;
+        // addresses clamped into the valid rows / heads (masked below)
         const TD* dtp = reinterpret_cast<const TD*>(a.dt) + tok0 * H + min(hb * HB + hh, H - 1);
-        TD raw[PPL];
 #pragma unroll
-        for (int i = 0; i < PPL; ++i) raw[i] = dtp[(int64_t)min(r0 + 64 * i, qhi - 1) * H];
+        for (int i = 0; i < PPL; ++i) raw[k][i] = dtp[(int64_t)min(r0 + 64 * i, qhi - 1) * H];
+    }
+#pragma unroll
+    for (int k = 0; k < CPW; ++k)
 #pragma unroll
         for (int i = 0; i < PPL; ++i)
-            if (r0 + 64 * i < Q) tile[r0 + 64 * i][hh] = to_f32(raw[i]);
-    }
+            if (r0 + 64 * i < Q) tile[k][r0 + 64 * i][hh] = to_f32(raw[k][i]);
     __syncthreads();
     if (h >= H) return;                             // no barrier follows
+#pragma unroll
+    for (int k = 0; k < CPW; ++k) {
+    const int c = cw * CPW + k;
+    if (c >= a.nc) break;
+    const int qhi = min(Q, L - c * Q);
 
     float v[PPL], dA[PPL];
     float carry = 0.f;
 #pragma unroll
     for (int j = 0; j < PPL; ++j) {
         const int q = lane + 64 * j;
-        float d = q < Q ? tile[q][w] : 0.f;
+        float d = q < Q ? tile[k][q][w] : 0.f;
         if (a.bias) d += bias;
         if (a.softplus) d = softplus_f(d);
         d = fminf(fmaxf(d, a.lo), a.hi);
@@ -107,13 +122,14 @@ __global__ void __launch_bounds__(THREADS) k_chunk_cumsum(CumsumArgs a) {
         a.dto[off + q] = v[j];
         if (a.wts) {
             float wv = expf(fminf(total - dA[j], 0.f)) * v[j];
-            if (a.seq && (q >= qhi || se < 0 || sq[j] != se)) wv = 0.f;
+            if (a.seq && (q >= qhi || se[k] < 0 || sq[k][j] != se[k])) wv = 0.f;
             a.wts[off + q] = wv;
         }
     }
     if (a.scl && lane == 0) {
-        const bool keep = !a.seq || se == sprev;
+        const bool keep = !a.seq || se[k] == sprev[k];
         a.scl[((int64_t)bi * H + h) * a.nc + c] = keep ? expf(total) : 0.f;
+    }
     }
 }
 
@@ -136,16 +152,24 @@ int launch_chunk_cumsum_ex(const m2_chunk_cumsum_args& a, const int32_t* seq_idx
     k.nc = (int)((a.seqlen + a.chunk_size - 1) / a.chunk_size);
     k.softplus = a.dt_softplus; k.lo = a.dt_min; k.hi = a.dt_max;
     k.nhb = (int)((a.nheads + HB - 1) / HB);
-    const int64_t nblocks = (int64_t)k.nhb * k.nc * a.batch;
+    // two chunks per workgroup where one per workgroup needs more than one
+    // round of the CUs (two 16-wavefront workgroups on each of MI355X's 256)
+    const int cpw = (int64_t)k.nhb * k.nc * a.batch > 2 * 256 ? 2 : 1;
+    const int64_t nblocks = (int64_t)k.nhb * ((k.nc + cpw - 1) / cpw) * a.batch;
     M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_cumsum: too many blocks");
     k.nblocks = (int)nblocks;
     const dim3 grid((unsigned)nblocks);
     if (a.dt_dtype != M2_F32 && a.dt_dtype != M2_BF16)
         return set_error(M2_ERR_UNSUPPORTED, "chunk_cumsum: dt dtype %d", a.dt_dtype);
     const bool f32 = a.dt_dtype == M2_F32;
-#define M2_CUMSUM_LAUNCH(PPL)                                                \
-    if (f32) k_chunk_cumsum<float, PPL><<<grid, THREADS, 0, s>>>(k);         \
-    else k_chunk_cumsum<bf16, PPL><<<grid, THREADS, 0, s>>>(k);
+#define M2_CUMSUM_LAUNCH(PPL)                                                              \
+    if (cpw == 2) {                                                                        \
+        if (f32) k_chunk_cumsum<float, PPL, 2><<<grid, THREADS, 0, s>>>(k);                \
+        else k_chunk_cumsum<bf16, PPL, 2><<<grid, THREADS, 0, s>>>(k);                     \
+    } else {                                                                               \
+        if (f32) k_chunk_cumsum<float, PPL, 1><<<grid, THREADS, 0, s>>>(k);                \
+        else k_chunk_cumsum<bf16, PPL, 1><<<grid, THREADS, 0, s>>>(k);                     \
+    }
     if (k.Q <= 64) { M2_CUMSUM_LAUNCH(1) }
     else if (k.Q <= 128) { M2_CUMSUM_LAUNCH(2) }
     else { M2_CUMSUM_LAUNCH(4) }

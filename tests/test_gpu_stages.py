@@ -39,6 +39,10 @@ def _inputs(b, L, H, G, P, N, Q, dtype, seed, z=False, init=False):
     (1, 256, 64, 256, "bf16", (0.0, float("inf"))),
     (2, 300, 40, 128, "bf16", (0.001, 0.1)),        # L % Q != 0, clamp
     (1, 4096, 128, 128, "bf16", (0.0, float("inf"))),
+    # more than 512 workgroups of one chunk: two chunks per workgroup, an even
+    # chunk count (c3's) and an odd one whose last workgroup has no second chunk
+    (1, 8192, 256, 128, "bf16", (0.0, float("inf"))),
+    (2, 3900, 160, 128, "f32", (0.001, 0.1)),
 ])
 def test_chunk_cumsum(b, L, H, Q, dtype, limit):
     announce("chunk_cumsum", b, L, H, Q, dtype, limit)
