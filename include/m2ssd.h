@@ -63,7 +63,9 @@ int m2_chunk_cumsum(const m2_chunk_cumsum_args* a, void* stream);
  * chunk_state: states[b,c,h] = sum_q exp(min(dA[Q-1]-dA[q],0)) dt[q] x[q]^T B[q]
  * (P x N per chunk and head; B shared by the heads of a group).  With seq_idx,
  * positions whose sequence differs from the one at the chunk's last valid
- * position (or where that id is negative) are left out.
+ * position (or where that id is negative) are left out.  Sizes: headdim 32 /
+ * 64 / 128, dstate 64 / 128 / 256, chunk_size a multiple of 16 up to 256 (the
+ * Python layer maps every other head dim and dstate onto these).
  * Replaces chunk_state_fwd (reference kernels/chunk_state_fwd.py:424-441,
  * :194-304; naive ops/ssd_naive.py:77-128).
  * ------------------------------------------------------------------------- */
@@ -104,7 +106,8 @@ int m2_state_passing(const m2_state_passing_args* a, void* stream);
 /* ---------------------------------------------------------------------------
  * bmm_chunk: out[b,c,g] = a_c @ b_c^T over each chunk (Q x Q, contraction K),
  * then optionally zeroed above the diagonal (causal) and where seq_idx[i] !=
- * seq_idx[j].
+ * seq_idx[j].  k a multiple of 32 (the Python layer zero-pads others),
+ * chunk_size a multiple of 16 up to 256.
  * Replaces bmm_chunk_fwd (reference kernels/bmm_chunk_fwd.py:381-400,
  * :293-374; naive ops/ssd_naive.py:189-216).
  * ------------------------------------------------------------------------- */
@@ -125,7 +128,9 @@ int m2_bmm_chunk(const m2_bmm_chunk_args* a, void* stream);
  * states are rounded to x's dtype before use.  out_x (optional) receives the
  * output before the z gate.  With seq_idx, rows whose sequence differs from
  * the one at the previous chunk's last position (0 for chunk 0) get no
- * inter-chunk term; cb is used as given (mask it with bmm_chunk).
+ * inter-chunk term; cb is used as given (mask it with bmm_chunk).  Sizes:
+ * headdim 32 / 64 / 128, dstate a multiple of 32, chunk_size a multiple of 16
+ * up to 256 (the Python layer maps other sizes onto these).
  * Replaces chunk_scan_fwd (reference kernels/chunk_scan_fwd.py:579-600,
  * :482-572; naive ops/ssd_naive.py:223-318).
  * ------------------------------------------------------------------------- */
@@ -173,8 +178,12 @@ int m2_chunk_state_varlen(const m2_chunk_state_varlen_args* a, void* stream);
  * the caller's workspace (size from m2_ssd_combined_workspace_size).
  * states_passed is kept in x's dtype; out and the final states are float32.
  * chunk_size is a tiling choice here as in the reference (the outputs are the
- * same function of the inputs for every chunk size): bf16 chunks of 256 run
- * as chunks of 128 when that keeps the whole layer on the fused kernels.
+ * same function of the inputs for every chunk size): any positive chunk size
+ * is accepted; bf16 chunk sizes the fused kernels do not take run as chunks of
+ * 128 when that keeps the whole layer on the fused kernels, fp32 chunks of 256
+ * and chunk sizes other than 64 / 128 / 256 run as chunks of 128.  Head dim
+ * and dstate: the sizes of m2_chunk_state / m2_chunk_scan (the Python layer
+ * maps every other size onto these: zero padding, heads of 64, dstate blocks).
  * Replaces mamba_chunk_scan_combined_fwd (reference kernels/ssd_combined.py:46-203).
  * ------------------------------------------------------------------------- */
 typedef struct {
@@ -226,6 +235,8 @@ int m2_ssd_combined_noalloc(const m2_ssd_combined_args* a, void* stream);
  * out = new @ C + D x; out *= silu(z).
  * new goes to new_state, or back into state when new_state is NULL (or
  * equal to state): the in-place update of a decode loop that owns its state.
+ * Any headdim and dstate (16-byte aligned rows are the fast path: dstate a
+ * multiple of 4 up to 256).
  * Replaces selective_state_update (reference ops/selective_state_update.py:22-123).
  * ------------------------------------------------------------------------- */
 typedef struct {

@@ -93,21 +93,28 @@ int record(void** ev, int i, hipStream_t s) {
 
 // The combined forward returns only y and the final (and varlen) states: the
 // same function of the inputs for every chunk size (the chunked algorithm is
-// exact; only the rounding points at chunk boundaries move).  bf16 chunks of
-// 256 run as chunks of 128 when that puts both halves of the layer on the
-// fused kernels (the fused scan keeps at most 128 positions of a chunk in
-// LDS); fp32 chunks of 256 always run as chunks of 128.
+// exact; only the rounding points at chunk boundaries move).  bf16 chunk
+// sizes the fused kernels do not take (256: the fused scan keeps at most 128
+// positions of a chunk in LDS; 32; ...) run as chunks of 128 when that puts
+// both halves of the layer on the fused kernels; fp32 chunks of 256 always
+// run as chunks of 128; chunk sizes other than 64, 128 and 256 run as chunks
+// of 128 (the tile sizes every kernel of the layer is built and tested for).
+bool layer_fused(const m2_ssd_combined_args& a) {
+    return m2::states_fused_supported(a) &&
+           m2::scan_fused_supported(a.headdim, a.dstate, a.chunk_size);
+}
+
 m2_ssd_combined_args internal_args(const m2_ssd_combined_args& a0) {
     m2_ssd_combined_args a = a0;
-    if (a0.dtype == M2_BF16 && a0.chunk_size == 256) {
+    if (a0.dtype == M2_BF16 && a0.chunk_size != 128 && !layer_fused(a0)) {
         a.chunk_size = 128;
-        if (!m2::states_fused_supported(a) || !m2::scan_fused_supported(a.headdim, a.dstate, 128))
-            a.chunk_size = 256;
+        if (!layer_fused(a)) a.chunk_size = a0.chunk_size;
     }
     // fp32 has no rounding points at chunk boundaries: chunks of 128 give the
     // same result up to fp32 summation order, with twice the workgroups and
     // half the intra-chunk work
     if (a0.dtype == M2_F32 && a0.chunk_size == 256) a.chunk_size = 128;
+    if (a.chunk_size != 64 && a.chunk_size != 128 && a.chunk_size != 256) a.chunk_size = 128;
     return a;
 }
 

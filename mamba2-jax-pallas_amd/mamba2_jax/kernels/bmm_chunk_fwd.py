@@ -13,6 +13,7 @@ import math
 import torch
 
 from .. import _lib as L
+from . import _shapes as S
 from .chunk_state_fwd import _io_dtype, _seq_idx
 
 
@@ -31,6 +32,12 @@ def bmm_chunk_fwd(a, b, chunk_size, seq_idx=None, causal=False, output_dtype=Non
     L.require(out_dtype in (torch.float32, torch.bfloat16),
               f"output_dtype {out_dtype} is not supported (float32 or bfloat16)")
     io = _io_dtype(a, b)
+    if k % 32:
+        # zero columns of the contraction add nothing (the reference pads k to
+        # its tile, kernels/bmm_chunk_fwd.py:209-218); the kernels take k % 32 == 0
+        kp = 32 * math.ceil(k / 32)
+        a, b = S.pad_last(a, kp), S.pad_last(b, kp)
+        k = kp
     a_c, b_c = L.dev_contig(a, io), L.dev_contig(b, io)
     seq = _seq_idx(seq_idx, batch, seqlen)
     out = torch.empty((batch, nc, ngroups, chunk_size, chunk_size), dtype=out_dtype, device=dev)

@@ -2,8 +2,10 @@
 D skip + z gate in one MFMA kernel (libm2ssd.so: m2_chunk_scan).
 
 Drop-in for reference kernels/chunk_scan_fwd.py (chunk_scan_fwd :579-600,
-chunk_scan_fwd_mosaic :482-572).  Tile keyword arguments are accepted and
-ignored.
+chunk_scan_fwd_mosaic :482-572), for every head dim and dstate: the
+reference pads both up to its tiles (:367-390); here sizes the kernels do not
+tile run through the exact padding / head splitting / dstate blocks of
+kernels/_shapes.py.  Tile keyword arguments are accepted and ignored.
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ import math
 import torch
 
 from .. import _lib as L
+from . import _shapes as S
 from .chunk_state_fwd import _io_dtype, _seq_idx
 
 
@@ -26,7 +29,7 @@ def chunk_scan_fwd(cb, x, dt, dA_cumsum, C, states, D=None, z=None, seq_idx=None
     states (batch, nchunks, nheads, headdim, dstate) = the state entering each
     chunk (rounded to x's dtype before use), D (nheads,) or (nheads, headdim).
     """
-    dev = L.device_of(cb, x, dt, dA_cumsum, C, states, D, z, seq_idx)
+    L.device_of(cb, x, dt, dA_cumsum, C, states, D, z, seq_idx)
     L.require(x.dim() == 4, "x must be (batch, seqlen, nheads, headdim)")
     batch, seqlen, nheads, hdim = x.shape
     L.require(C.dim() == 4 and tuple(C.shape[:2]) == (batch, seqlen),
@@ -42,15 +45,48 @@ def chunk_scan_fwd(cb, x, dt, dA_cumsum, C, states, D=None, z=None, seq_idx=None
     L.require(tuple(states.shape) == (batch, nchunks, nheads, hdim, dstate),
               f"states.shape={tuple(states.shape)} != {(batch, nchunks, nheads, hdim, dstate)}")
     L.require(nheads % ngroups == 0, "nheads must be a multiple of ngroups")
-    D_has_hdim = 0
     if D is not None:
-        if D.dim() == 2:
-            L.require(tuple(D.shape) == (nheads, hdim), f"D.shape={tuple(D.shape)}")
-            D_has_hdim = 1
-        else:
-            L.require(tuple(D.shape) == (nheads,), f"D.shape={tuple(D.shape)}")
+        L.require(tuple(D.shape) in ((nheads,), (nheads, hdim)), f"D.shape={tuple(D.shape)}")
     if z is not None:
         L.require(tuple(z.shape) == tuple(x.shape), "z.shape != x.shape")
+    return _chunk_scan(cb, x, dt, dA_cumsum, C, states, D, z, seq_idx)
+
+
+def _chunk_scan(cb, x, dt, dA_cumsum, C, states, D, z, seq_idx, native=None):
+    """chunk_scan_fwd for any head dim / dstate (kernels/_shapes.py);
+    `native` runs the mapped problem (default: the library)."""
+    native = native or _chunk_scan_native
+    P, N = x.shape[-1], C.shape[-1]
+    if N > S.NMAX:
+        # the inter-chunk term sums over dstate: one call per column block,
+        # the outputs before the gate added (CB and D in block 0 only), then
+        # the z gate
+        out_x = None
+        for j, (n0, n1) in enumerate(S.n_blocks(N)):
+            o, _ = _chunk_scan(cb if j == 0 else torch.zeros_like(cb), x, dt, dA_cumsum,
+                               C[..., n0:n1], states[..., n0:n1], D if j == 0 else None, None,
+                               seq_idx, native)
+            out_x = o if out_x is None else out_x.add_(o)
+        if z is None:
+            return out_x, None
+        return S.gate(out_x, z), out_x
+    Pp, k = S.p_plan_stage(P)
+    Np = S.n_pad(N, native=(32,) + S.NATIVE_N)
+    if (Pp, k, Np) == (P, 1, N):
+        return native(cb, x, dt, dA_cumsum, C, states, D, z, seq_idx)
+    st = S.split_heads(S.pad_dim(S.pad_last(states, Np), 3, Pp), 2, k)
+    out, out_x = native(cb, S.split_heads(S.pad_last(x, Pp), 2, k), S.repeat_heads(dt, 1, k),
+                        S.repeat_heads(dA_cumsum, 1, k), S.pad_last(C, Np), st,
+                        S.adapt_D(D, k, Pp), S.split_heads(S.pad_last(z, Pp), 2, k), seq_idx)
+    return S.merge_heads(out, 2, k, P), S.merge_heads(out_x, 2, k, P)
+
+
+def _chunk_scan_native(cb, x, dt, dA_cumsum, C, states, D, z, seq_idx):
+    dev = x.device
+    batch, seqlen, nheads, hdim = x.shape
+    _, _, ngroups, dstate = C.shape
+    chunk_size = int(dt.shape[3])
+    D_has_hdim = int(D is not None and D.dim() == 2)
     io = _io_dtype(x, C, z)
     x_c, C_c, z_c = L.dev_contig(x, io), L.dev_contig(C, io), L.dev_contig(z, io)
     cb_c = L.dev_contig(cb if cb.dtype in (torch.float32, torch.bfloat16) else cb.float())

@@ -1,6 +1,8 @@
 """mamba_chunk_scan_combined_fwd on MI355X: the whole SSD layer forward.
 
-Drop-in for reference kernels/ssd_combined.py:46-203.  One call into
+Drop-in for reference kernels/ssd_combined.py:46-203, for every head dim and
+dstate (sizes the kernels do not tile run through the exact padding / head
+splitting / dstate blocks of kernels/_shapes.py).  One call into
 libm2ssd.so (m2_ssd_combined) enqueues the five stage kernels
 (chunk_cumsum -> chunk_state -> state_passing -> bmm_chunk -> chunk_scan, plus
 chunk_state_varlen when varlen states are requested) on the current stream;
@@ -16,6 +18,7 @@ import math
 import torch
 
 from .. import _lib as L
+from . import _shapes as S
 from .chunk_state_fwd import _io_dtype, _seq_idx
 
 
@@ -56,7 +59,7 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
     recorded before the first and after each of the five stages; None entries
     are skipped.
     """
-    dev = L.device_of(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, cu_seqlens)
+    L.device_of(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, cu_seqlens)
     L.require(x.dim() == 4, "x must be (batch, seqlen, nheads, headdim)")
     batch, seqlen, nheads, headdim = x.shape
     L.require(B.dim() == 4 and tuple(B.shape[:2]) == (batch, seqlen),
@@ -68,13 +71,8 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
     L.require(nheads % ngroups == 0, "nheads must be a multiple of ngroups")
     if dt_bias is not None:
         L.require(tuple(dt_bias.shape) == (nheads,), f"dt_bias.shape={tuple(dt_bias.shape)}")
-    D_has_hdim = 0
     if D is not None:
-        if D.dim() == 2:
-            L.require(tuple(D.shape) == (nheads, headdim), f"D.shape={tuple(D.shape)}")
-            D_has_hdim = 1
-        else:
-            L.require(tuple(D.shape) == (nheads,), f"D.shape={tuple(D.shape)}")
+        L.require(tuple(D.shape) in ((nheads,), (nheads, headdim)), f"D.shape={tuple(D.shape)}")
     if z is not None:
         L.require(tuple(z.shape) == tuple(x.shape), "z.shape != x.shape")
     if initial_states is not None:
@@ -93,11 +91,69 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
     elif return_varlen_states:
         raise L.M2ShapeError("return_varlen_states needs cu_seqlens")
 
+    out, fin, vs = _combined(x, dt, A, B, C, chunk_size, D, z, dt_bias, initial_states, seq_idx,
+                             cu_seqlens, nseq, bool(dt_softplus), dt_limit, return_final_states,
+                             _stage_events)
+    if not return_varlen_states:
+        return (out, fin) if return_final_states else out
+    return (out, fin, vs) if return_final_states else (out, vs)
+
+
+def _combined(x, dt, A, B, C, chunk_size, D, z, dt_bias, init, seq_idx, cu_seqlens, nseq,
+              dt_softplus, dt_limit, want_final, events, native=None):
+    """(out, final or None, varlen or None) for any head dim and dstate: sizes
+    the kernels do not tile are mapped onto ones they do (kernels/_shapes.py).
+    `native` runs the mapped problem (default: the library; the CPU tests
+    pass the oracle to check the mapping)."""
+    native = native or _combined_native
+    N = B.shape[-1]
+    if N > S.NMAX:
+        # column blocks: outputs added, states concatenated; D in block 0 only
+        out = None
+        fins, vss = [], []
+        for j, (n0, n1) in enumerate(S.n_blocks(N)):
+            o, f, v = _combined(x, dt, A, B[..., n0:n1], C[..., n0:n1], chunk_size,
+                                D if j == 0 else None, z, dt_bias,
+                                None if init is None else init[..., n0:n1], seq_idx, cu_seqlens,
+                                nseq, dt_softplus, dt_limit, want_final, None, native)
+            out = o if out is None else out.add_(o)
+            fins.append(f)
+            vss.append(v)
+        fin = torch.cat(fins, dim=-1) if want_final else None
+        vs = torch.cat(vss, dim=-1) if cu_seqlens is not None else None
+        return out, fin, vs
+    P = x.shape[-1]
+    Pp, k = S.p_plan_layer(P)
+    Np = S.n_pad(N)
+    if (Pp, k, Np) == (P, 1, N):
+        return native(x, dt, A, B, C, chunk_size, D, z, dt_bias, init, seq_idx, cu_seqlens,
+                      nseq, dt_softplus, dt_limit, want_final, events)
+    xs = S.split_heads(S.pad_last(x, Pp), 2, k)
+    zs = S.split_heads(S.pad_last(z, Pp), 2, k)
+    inits = None
+    if init is not None:
+        inits = S.split_heads(S.pad_dim(S.pad_last(init, Np), 2, Pp), 1, k)
+    o, f, v = native(xs, S.repeat_heads(dt, 2, k), S.repeat_heads(A, 0, k), S.pad_last(B, Np),
+                     S.pad_last(C, Np), chunk_size, S.adapt_D(D, k, Pp), zs,
+                     S.repeat_heads(dt_bias, 0, k), inits, seq_idx, cu_seqlens, nseq, dt_softplus,
+                     dt_limit, want_final, events)
+    return (S.merge_heads(o, 2, k, P), S.merge_heads(f, 1, k, P, N),
+            S.merge_heads(v, 1, k, P, N))
+
+
+def _combined_native(x, dt, A, B, C, chunk_size, D, z, dt_bias, init, seq_idx, cu_seqlens, nseq,
+                     dt_softplus, dt_limit, want_final, events):
+    """One m2_ssd_combined call (sizes the kernels take)."""
+    dev = x.device
+    batch, seqlen, nheads, headdim = x.shape
+    ngroups, dstate = B.shape[2], B.shape[3]
+    D_has_hdim = int(D is not None and D.dim() == 2)
+    return_final_states = want_final
     io = _io_dtype(x, B, C, z)
     x_c, B_c, C_c, z_c = (L.dev_contig(t, io) for t in (x, B, C, z))
     dt_c = L.dev_contig(dt if dt.dtype in (torch.float32, torch.bfloat16) else dt.float())
     A_c, D_c, bias_c = (L.dev_contig(t, torch.float32) for t in (A, D, dt_bias))
-    init = L.dev_contig(initial_states, torch.float32)
+    init = L.dev_contig(init, torch.float32)
     seq = _seq_idx(seq_idx, batch, seqlen)
     cu = L.dev_contig(cu_seqlens, torch.int32)
 
@@ -106,7 +162,7 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
            if return_final_states else None)
     vs = (torch.empty((nseq, nheads, headdim, dstate), dtype=torch.float32, device=dev)
           if cu is not None else None)
-    ev_keep, ev_ptr = _events_array(_stage_events)
+    ev_keep, ev_ptr = _events_array(events)
     args = L.SsdCombinedArgs(
         x=L.ptr(x_c), dt=L.ptr(dt_c), A=L.ptr(A_c), B=L.ptr(B_c), C=L.ptr(C_c), D=L.ptr(D_c),
         z=L.ptr(z_c), dt_bias=L.ptr(bias_c), initial_states=L.ptr(init), seq_idx=L.ptr(seq),
@@ -114,7 +170,7 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
         batch=batch, seqlen=seqlen, nheads=nheads, headdim=headdim, ngroups=ngroups,
         dstate=dstate, chunk_size=chunk_size, nseq=nseq, dtype=L.dtype_code(x_c, "x"),
         dt_dtype=L.dtype_code(dt_c, "dt"), D_has_hdim=D_has_hdim,
-        dt_softplus=int(bool(dt_softplus)), dt_min=float(dt_limit[0]),
+        dt_softplus=int(dt_softplus), dt_min=float(dt_limit[0]),
         dt_max=float(dt_limit[1]), stage_events=ev_ptr)
     lib = L.load_library()
     import ctypes
@@ -126,6 +182,4 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
     with torch.cuda.device(dev):
         L.call("m2_ssd_combined", args, L.stream_of(dev))
     del ev_keep
-    if not return_varlen_states:
-        return (out, fin) if return_final_states else out
-    return (out, fin, vs) if return_final_states else (out, vs)
+    return out, fin, vs
