@@ -45,16 +45,18 @@ STAGES = ["chunk_cumsum", "chunk_state", "state_passing", "bmm_chunk", "chunk_sc
 
 def internal_chunk(cfg):
     """The chunk size the combined path runs (m2_ssd_combined's internal_args):
-    bf16 chunks of 256 run as chunks of 128 when both fused kernels then apply,
-    fp32 chunks of 256 always."""
-    if cfg.chunk_size == 256:
-        if cfg.dtype == "f32":
-            return 128
-        import dataclasses
-        c = dataclasses.replace(cfg, chunk_size=128)
-        if states_is_fused(c) and scan_is_fused(c):
-            return 128
-    return cfg.chunk_size
+    bf16 chunk sizes the fused kernels do not take run as chunks of 128 when
+    both fused kernels then apply, fp32 chunks of 256 always, and chunk sizes
+    other than 64 / 128 / 256 always."""
+    import dataclasses
+    Q = cfg.chunk_size
+    fused = lambda c: states_is_fused(c) and scan_is_fused(c)
+    if cfg.dtype == "bf16" and Q != 128 and not fused(cfg):
+        if fused(dataclasses.replace(cfg, chunk_size=128)):
+            Q = 128
+    if cfg.dtype == "f32" and Q == 256:
+        Q = 128
+    return Q if Q in (64, 128, 256) else 128
 
 
 def stage_work(cfg, with_init=False, with_z=False):
@@ -133,17 +135,16 @@ def cumsum_in_state(cfg):
             and not states_is_fused(cfg))
 
 
-def states_is_fused(cfg):
+def states_is_fused(cfg, force=None):
     """The combined path runs chunk_state and state_passing as one kernel for
     headdim 64, dstate a multiple of 64 and chunk_size a multiple of 64 up to
     256: always for bf16, for fp32 where the pass has at least 256 workgroups
-    (batch x heads x dstate / 64) or M2_F32_STATES=fused forces it
-    (m2::states_fused_supported)."""
+    (batch x heads x dstate / 64) or the f32_states testing override ("fused" /
+    "staged", given as `force`) forces it (m2::states_fused_supported)."""
     shape = (cfg.headdim == 64 and cfg.dstate % 64 == 0 and cfg.chunk_size % 64 == 0
              and cfg.chunk_size <= 256 and cfg.nheads % cfg.ngroups == 0)
     if cfg.dtype == "bf16":
         return shape
-    force = os.environ.get("M2_F32_STATES")
     if not shape or force == "staged":
         return False
     return force == "fused" or cfg.batch * cfg.nheads * (cfg.dstate // 64) >= 256

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define M2SSD_ABI_VERSION 4
+#define M2SSD_ABI_VERSION 5
 
 /* return codes */
 #define M2_OK               0
@@ -228,6 +228,13 @@ int m2_ssd_combined(const m2_ssd_combined_args* a, void* stream);
  * ------------------------------------------------------------------------- */
 #define M2_NOALLOC_SCRATCH_BYTES (128u << 20)
 int m2_ssd_combined_noalloc(const m2_ssd_combined_args* a, void* stream);
+/* Looks up the static array on the current device (what the first
+ * m2_ssd_combined_noalloc call there does otherwise).  That lookup may load
+ * code onto the device, which a capturing stream must not see: the first
+ * m2_ssd_combined_noalloc call on a device refuses a stream under graph
+ * capture (M2_ERR_INVALID), so a caller that captures calls this once per
+ * device beforehand.  No counterpart in the reference; for the same callers. */
+int m2_ssd_combined_noalloc_prepare(void);
 
 /* ---------------------------------------------------------------------------
  * selective_state_update (one decode token):
@@ -411,6 +418,23 @@ typedef struct {
     m2_causal_conv1d_update_args conv;
 } m2_skinny_gemm_norm_args;
 int m2_skinny_gemm_norm(const m2_skinny_gemm_norm_args* a, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Testing hook, no counterpart in the reference: forces one of the kernel
+ * choices the library otherwise makes from the shape, process-wide, so that a
+ * test can run every path on one shape (production code never calls it; no
+ * environment variable is read).  value 0 restores the automatic choice; a
+ * forced choice the shape cannot take is ignored.  Returns the previous value,
+ * or M2_ERR_INVALID for an unknown knob or value.
+ * ------------------------------------------------------------------------- */
+#define M2_KNOB_STATES_SPLIT  0   /* bf16 fused state pass: 1 a head in 64-column
+                                     halves, 2 head pairs x 64 columns, 3 head
+                                     pairs x 128 columns                       */
+#define M2_KNOB_F32_STATES    1   /* fp32 layer: 1 the fused state pass, 2 the
+                                     staged chunk_state + state_passing        */
+#define M2_KNOB_ONESHOT_HEADS 2   /* one-shot state kernel: 1 one head per
+                                     workgroup                                 */
+int m2_set_dispatch_override(int knob, int value);
 
 /* thread-local message for the last non-zero return code of this thread */
 const char* m2_last_error(void);

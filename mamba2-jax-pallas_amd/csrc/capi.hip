@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 #include "m2_internal.h"
 
 namespace m2 {
@@ -24,10 +26,25 @@ int check_launch(const char* what) {
     return M2_OK;
 }
 
+constexpr int NKNOBS = 3;
+static std::atomic<int> g_knob[NKNOBS];
+
+int dispatch_override(int knob) {
+    return knob >= 0 && knob < NKNOBS ? g_knob[knob].load(std::memory_order_relaxed) : 0;
+}
+
 }  // namespace m2
 
 extern "C" const char* m2_last_error(void) { return m2::g_err; }
 extern "C" int m2_abi_version(void) { return M2SSD_ABI_VERSION; }
+
+extern "C" int m2_set_dispatch_override(int knob, int value) {
+    static const int maxval[m2::NKNOBS] = {3, 2, 1};
+    if (knob < 0 || knob >= m2::NKNOBS || value < 0 || value > maxval[knob])
+        return m2::set_error(M2_ERR_INVALID, "m2_set_dispatch_override: knob %d value %d", knob,
+                             value);
+    return m2::g_knob[knob].exchange(value, std::memory_order_relaxed);
+}
 
 #define M2_ENTRY(name, T, launcher)                                  \
     extern "C" int name(const T* a, void* stream) {                  \
@@ -114,7 +131,8 @@ m2_ssd_combined_args internal_args(const m2_ssd_combined_args& a0) {
     // same result up to fp32 summation order, with twice the workgroups and
     // half the intra-chunk work
     if (a0.dtype == M2_F32 && a0.chunk_size == 256) a.chunk_size = 128;
-    if (a.chunk_size != 64 && a.chunk_size != 128 && a.chunk_size != 256) a.chunk_size = 128;
+    if (a.chunk_size > 0 && a.chunk_size != 64 && a.chunk_size != 128 && a.chunk_size != 256)
+        a.chunk_size = 128;
     return a;
 }
 

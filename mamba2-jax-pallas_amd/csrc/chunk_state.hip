@@ -441,10 +441,14 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
 // the plane LDS in budget; two heads per workgroup when the group's head
 // count is even.  cs: chunk_cumsum folded in (the StateArgs cumsum fields set)
 int launch_chunk_state_f32(const StateArgs& sa, int64_t bhc, hipStream_t s, bool cs = false) {
-    if (sa.P != 64 || sa.N % F32_NB || (sa.Q != 64 && sa.Q != 128)) return M2_ERR_UNSUPPORTED;
+    if (sa.P != 64 || sa.N % F32_NB || (sa.Q != 64 && sa.Q != 128))
+        return m2::set_error(M2_ERR_UNSUPPORTED,
+                             "chunk_state (fp32 planes): headdim 64, dstate %% %d == 0 and chunk 64 "
+                             "/ 128 only (got %d / %d / %d)", F32_NB, sa.P, sa.N, sa.Q);
     const int HP = (sa.H / sa.G) % 2 == 0 ? 2 : 1;
     const size_t shm = cs_f32_lds(sa.Q, HP);
-    if (shm > 160 * 1024) return M2_ERR_UNSUPPORTED;
+    if (shm > 160 * 1024)
+        return m2::set_error(M2_ERR_UNSUPPORTED, "chunk_state (fp32 planes): %zu B of LDS", shm);
     void (*kern)(StateArgs) = nullptr;
 #define M2_CSF_CASE(HPV, QV, CSV) \
     if (HP == HPV && sa.Q == QV && cs == CSV) kern = k_chunk_state_f32<HPV, QV / 32, CSV>;
@@ -457,7 +461,8 @@ int launch_chunk_state_f32(const StateArgs& sa, int64_t bhc, hipStream_t s, bool
         return m2::set_error(M2_ERR_LAUNCH, "chunk_state: cannot reserve %zu B of LDS", shm);
     StateArgs k = sa;
     const int64_t nblocks = bhc / HP * (sa.N / F32_NB);
-    if (nblocks >= (1ll << 31)) return M2_ERR_UNSUPPORTED;
+    if (nblocks >= (1ll << 31))
+        return m2::set_error(M2_ERR_UNSUPPORTED, "chunk_state (fp32 planes): too many blocks");
     k.nblocks = (int)nblocks;
     kern<<<(unsigned)nblocks, THREADS, shm, s>>>(k);
     return m2::check_launch("chunk_state");
@@ -553,7 +558,7 @@ int launch_chunk_state_cumsum(const m2_chunk_cumsum_args& c1, const m2_chunk_sta
     sa.A = c1.A; sa.dt_bias = c1.dt_bias; sa.dt_lo = c1.dt_min; sa.dt_hi = c1.dt_max;
     sa.dA_out = c1.dA_cumsum; sa.dt_out = c1.dt_out;
     const int64_t nblocks = a.batch * sa.nc * a.nheads;
-    if (nblocks >= (1ll << 31)) return M2_ERR_UNSUPPORTED;
+    M2_REQUIRE(nblocks < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_state: too many blocks");
     return launch_chunk_state_f32(sa, nblocks, s, true);
 }
 

@@ -6,6 +6,10 @@
 #include "m2_common.h"
 
 namespace m2 {
+// The value m2_set_dispatch_override last set for a knob (M2_KNOB_*); 0 =
+// the automatic choice.
+int dispatch_override(int knob);
+
 int launch_chunk_cumsum(const m2_chunk_cumsum_args& a, hipStream_t stream);
 // chunk_cumsum that also writes the chunk-state weights wts [b, H, nc, Q] and
 // the carried-state decay scl [b, H, nc] (seq_idx rules applied) when non-NULL

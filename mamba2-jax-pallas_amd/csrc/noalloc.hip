@@ -10,7 +10,10 @@
 // the process ends.  Host code never passes the array's name to a kernel (on
 // the host it is only a stand-in symbol); its device address comes from
 // hipGetSymbolAddress, looked up once per device, with that device current, on
-// the first call there, and kept per device.
+// the first call there (or in m2_ssd_combined_noalloc_prepare), and kept per
+// device.  The lookup may load the code object onto the device, which a stream
+// under graph capture must not see: a first call on a capturing stream is
+// refused, and callers that capture call the prepare function beforehand.
 //
 // Calls on one GPU share its array: two calls that overlap in time on one GPU
 // (different streams, or the same stream from different threads without
@@ -28,8 +31,9 @@ constexpr int MAX_DEVICES = 64;
 std::mutex g_mu;
 void* g_ptr[MAX_DEVICES];          // device address of `scratch` per device, or NULL
 
-// The device address of `scratch` on the current device (looked up once).
-int scratch_of_current_device(void** out) {
+// The device address of `scratch` on the current device (looked up once; not
+// while `capturing`).
+int scratch_of_current_device(void** out, bool capturing) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess)
         return m2::set_error(M2_ERR_LAUNCH, "m2_ssd_combined_noalloc: hipGetDevice failed");
@@ -38,6 +42,11 @@ int scratch_of_current_device(void** out) {
                              MAX_DEVICES);
     std::lock_guard<std::mutex> lock(g_mu);
     if (!g_ptr[dev]) {
+        if (capturing)
+            return m2::set_error(M2_ERR_INVALID,
+                                 "m2_ssd_combined_noalloc: first call on device %d is under stream "
+                                 "capture; call m2_ssd_combined_noalloc_prepare() before capturing",
+                                 dev);
         void* p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p)
@@ -59,8 +68,16 @@ extern "C" int m2_ssd_combined_noalloc(const m2_ssd_combined_args* a, void* stre
                "m2_ssd_combined_noalloc: this problem needs a %zu-byte workspace, more than the "
                "%zu-byte static scratch; call m2_ssd_combined with a workspace instead",
                need, (size_t)M2_NOALLOC_SCRATCH_BYTES);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cap) != hipSuccess)
+        return m2::set_error(M2_ERR_LAUNCH, "m2_ssd_combined_noalloc: hipStreamIsCapturing failed");
     void* ws = nullptr;
-    int rc = scratch_of_current_device(&ws);
+    int rc = scratch_of_current_device(&ws, cap != hipStreamCaptureStatusNone);
     if (rc) return rc;
     return m2::ssd_combined_on(*a, ws, (size_t)M2_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
+}
+
+extern "C" int m2_ssd_combined_noalloc_prepare(void) {
+    void* ws = nullptr;
+    return scratch_of_current_device(&ws, false);
 }

@@ -562,8 +562,8 @@ bool states_fused_supported(const m2_ssd_combined_args& a) {
 // (128 positions) measured with every CU busy at the BASELINE shapes (1.36 us
 // for a head in 64-column halves, 2.6 for a pair of heads x 64 columns, 4.0
 // for a pair x 128 columns), times the rounds of 256 workgroups (one per CU)
-// and the chunks.  M2_STATES_KERNEL (halves / pair64 / pair128) forces a split where
-// the shape allows it (tests).
+// and the chunks.  The M2_KNOB_STATES_SPLIT override (tests) forces a split
+// where the shape allows it.
 enum StatesSplit { SPLIT_HALVES, SPLIT_PAIR64, SPLIT_PAIR128 };
 
 StatesSplit states_split(const m2_ssd_combined_args& a) {
@@ -574,10 +574,11 @@ StatesSplit states_split(const m2_ssd_combined_args& a) {
     const double t_halves = rounds(bh * (a.dstate / 64)) * nc * 1.36;
     const double t_p64 = pair ? rounds(bh / 2 * (a.dstate / 64)) * nc * 2.6 : 1e30;
     const double t_p128 = pair && a.dstate % 128 == 0 ? rounds(bh / 2 * (a.dstate / 128)) * nc * 4.0 : 1e30;
-    if (const char* e = getenv("M2_STATES_KERNEL")) {
-        if (!strcmp(e, "halves")) return SPLIT_HALVES;
-        if (!strcmp(e, "pair64") && t_p64 < 1e30) return SPLIT_PAIR64;
-        if (!strcmp(e, "pair128") && t_p128 < 1e30) return SPLIT_PAIR128;
+    switch (dispatch_override(M2_KNOB_STATES_SPLIT)) {
+        case 1: return SPLIT_HALVES;
+        case 2: if (t_p64 < 1e30) return SPLIT_PAIR64; break;
+        case 3: if (t_p128 < 1e30) return SPLIT_PAIR128; break;
+        default: break;
     }
     if (t_p128 < t_halves && t_p128 <= t_p64) return SPLIT_PAIR128;
     if (t_p64 < t_halves) return SPLIT_PAIR64;

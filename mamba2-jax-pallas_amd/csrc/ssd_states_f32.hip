@@ -336,15 +336,16 @@ namespace m2 {
 
 // fp32 inputs take this pass where it fills the CUs (one workgroup per (batch,
 // head, 64 dstate columns), at least 256 of them); below that the staged
-// kernels spread the same work over more workgroups.  M2_F32_STATES=fused /
-// staged forces either where the shape allows it (tests).
+// kernels spread the same work over more workgroups.  The M2_KNOB_F32_STATES
+// override (tests) forces either where the shape allows it.
 bool states_fused_f32_supported(const m2_ssd_combined_args& a) {
     if (!(a.dtype == M2_F32 && a.headdim == P && a.dstate % NB == 0 && a.chunk_size % KB == 0 &&
           a.chunk_size <= 256 && a.ngroups > 0 && a.nheads % a.ngroups == 0))
         return false;
-    if (const char* e = getenv("M2_F32_STATES")) {
-        if (!strcmp(e, "fused")) return true;
-        if (!strcmp(e, "staged")) return false;
+    switch (dispatch_override(M2_KNOB_F32_STATES)) {
+        case 1: return true;
+        case 2: return false;
+        default: break;
     }
     return a.batch * a.nheads * (a.dstate / NB) >= 256;
 }

@@ -255,10 +255,9 @@ int block_cols(int64_t N) { return N % 128 == 0 ? 128 : 64; }
 
 // heads per workgroup: two (sharing the B rows) when a group's heads pair up
 // and the tiles of two heads leave room for two workgroups per CU (Q <= 128),
-// else one; M2_ONESHOT_HEADS=1 forces one head (tests, A/B timing)
+// else one; the M2_KNOB_ONESHOT_HEADS override forces one head (tests)
 int heads_per_wg(const VarlenArgs& k) {
-    const char* e = getenv("M2_ONESHOT_HEADS");
-    if (e && !strcmp(e, "1")) return 1;
+    if (m2::dispatch_override(M2_KNOB_ONESHOT_HEADS) == 1) return 1;
     return (k.H / k.G) % 2 == 0 && k.Q <= 128 ? 2 : 1;
 }
 

@@ -9,6 +9,7 @@ libamdhip64 already loaded by torch).
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -19,7 +20,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm2ssd.so
 
 M2_F32 = 0
 M2_BF16 = 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 # bytes of the static scratch m2_ssd_combined_noalloc runs in (M2_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 128 << 20
 
@@ -159,7 +160,15 @@ ENTRY_POINTS = {
     "m2_skinny_gemm": SkinnyGemmArgs,
     "m2_skinny_gemm_norm": SkinnyGemmNormArgs,
 }
-OTHER_SYMBOLS = ("m2_ssd_combined_workspace_size", "m2_last_error", "m2_abi_version")
+OTHER_SYMBOLS = ("m2_ssd_combined_workspace_size", "m2_last_error", "m2_abi_version",
+                 "m2_set_dispatch_override", "m2_ssd_combined_noalloc_prepare")
+
+# testing hook m2_set_dispatch_override: knob name -> (M2_KNOB_*, {choice: value})
+KNOBS = {
+    "states_split": (0, {"halves": 1, "pair64": 2, "pair128": 3}),
+    "f32_states": (1, {"fused": 1, "staged": 2}),
+    "oneshot_heads": (2, {"1": 1}),
+}
 
 
 class M2Error(RuntimeError):
@@ -200,6 +209,10 @@ def load_library(path=LIB_PATH):
         lib.m2_last_error.restype = ctypes.c_char_p
         lib.m2_abi_version.argtypes = []
         lib.m2_abi_version.restype = ctypes.c_int
+        lib.m2_set_dispatch_override.argtypes = [ctypes.c_int, ctypes.c_int]
+        lib.m2_set_dispatch_override.restype = ctypes.c_int
+        lib.m2_ssd_combined_noalloc_prepare.argtypes = []
+        lib.m2_ssd_combined_noalloc_prepare.restype = ctypes.c_int
         if lib.m2_abi_version() != ABI_VERSION:
             raise ImportError(f"{path}: ABI version {lib.m2_abi_version()} != {ABI_VERSION}")
         _lib = lib
@@ -212,6 +225,22 @@ def call(name, args, stream):
     rc = getattr(lib, name)(ctypes.byref(args), ctypes.c_void_p(stream))
     if rc != 0:
         raise M2Error(name, rc, lib.m2_last_error().decode(errors="replace"))
+
+
+@contextlib.contextmanager
+def dispatch_override(knob, choice):
+    """Testing hook: force one of the library's shape-based kernel choices
+    (KNOBS) inside the block, process-wide; the automatic choice is restored
+    after it.  A forced choice the shape cannot take is ignored by the library."""
+    lib = load_library()
+    k, values = KNOBS[knob]
+    prev = lib.m2_set_dispatch_override(k, values[choice])
+    if prev < 0:
+        raise M2Error("m2_set_dispatch_override", prev, lib.m2_last_error().decode())
+    try:
+        yield
+    finally:
+        lib.m2_set_dispatch_override(k, prev)
 
 
 # ---------------------------------------------------------------------------

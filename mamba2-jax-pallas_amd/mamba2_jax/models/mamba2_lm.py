@@ -344,16 +344,14 @@ class Mamba2LMHeadModel:
         the head weight, which promotes to a float32 matmul (:213-216,
         :732-736).  A decode-sized batch with bf16 weights runs the skinny GEMM
         on the bf16-rounded activations with float32 accumulation and output;
-        otherwise the matmul is float32 throughout."""
+        otherwise the activations stay float32 and the matmul is float32
+        throughout."""
         w = params["lm_head_weight"]
         src, resid = (res.float(), None) if out is None else (out, res)
-        if res.dim() == 2 and w.dtype == torch.bfloat16 and res.shape[0] <= linear.PREFERRED_ROWS:
+        if res.dim() == 2 and linear.preferred_rows(res.shape[0], res.shape[1], w):
             xn = rms_norm(src, params["norm_f_weight"], out_dtype=w.dtype, residual=resid)
-            if linear.preferred(xn, w):
-                return linear.linear_skinny(xn, w, out_dtype=torch.float32)
-            xn = xn.float()
-        else:
-            xn = rms_norm(src, params["norm_f_weight"], residual=resid)
+            return linear.linear_skinny(xn, w, out_dtype=torch.float32)
+        xn = rms_norm(src, params["norm_f_weight"], residual=resid)
         return xn @ self._prepared(params, head=True).t()
 
     # -- prefill -------------------------------------------------------------

@@ -32,6 +32,13 @@ def preferred(x, w):
     return supported(x, w, PREFERRED_ROWS)
 
 
+def preferred_rows(rows, K, w):
+    """preferred() for bf16 activations of shape (rows, K) not yet computed:
+    lets a caller decide before it rounds them to bf16."""
+    return (w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[1] == K and K % 8 == 0
+            and 1 <= rows <= PREFERRED_ROWS and w.is_cuda)
+
+
 def linear_skinny(x, w, bias=None, out_dtype=torch.bfloat16):
     """x (M, K) bf16, w (N, K) bf16 (the [out, in] layout), bias (N,) -> y (M, N)."""
     dev = L.device_of(x, w, bias)

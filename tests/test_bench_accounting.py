@@ -19,6 +19,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "mamba2-jax-pallas_amd")]
 
 import bench  # noqa: E402
+from mamba2_jax import _lib as L  # noqa: E402
 from mamba2_jax import configs  # noqa: E402
 
 
@@ -30,6 +31,19 @@ def test_internal_chunk_matches_the_library():
     assert bench.internal_chunk(configs.CONFIGS["c2"]) == 128
     wide = dataclasses.replace(configs.CONFIGS["c1"], headdim=128)     # no fused kernels
     assert bench.internal_chunk(wide) == 256
+
+
+@pytest.mark.parametrize("Q,dtype,P", [(32, "bf16", 64), (100, "bf16", 64), (512, "bf16", 64),
+                                       (48, "f32", 64), (32, "bf16", 32), (256, "bf16", 32),
+                                       (64, "f32", 64), (96, "bf16", 32)])
+def test_other_chunk_sizes_match_the_library(Q, dtype, P):
+    """Chunk sizes other than 64 / 128 / 256 run as 128 (and bf16 ones the fused
+    kernels do not take, where 128 puts the layer on them): bench's mirror of
+    that choice agrees with the workspace the library asks for."""
+    cfg = dataclasses.replace(configs.CONFIGS["c2"], seqlen=1000, nheads=16, ngroups=2,
+                              chunk_size=Q, dtype=dtype, headdim=P)
+    c = dataclasses.replace(cfg, chunk_size=bench.internal_chunk(cfg))
+    assert _workspace_bytes(cfg) == _expected_workspace(cfg, bench.states_is_fused(c))
 
 
 def test_c2_fused_stage_bytes():
@@ -134,14 +148,14 @@ def _expected_workspace(cfg, fused):
     ("c0", "f32", "fused", True),
     ("c1", "bf16", None, True),
 ])
-def test_state_pass_choice_matches_the_library(name, dtype, force, fused, monkeypatch):
+def test_state_pass_choice_matches_the_library(name, dtype, force, fused):
     """bench.states_is_fused (which names the stages the bench reports) agrees
     with the library's own choice, read from the workspace it asks for."""
-    if force:
-        monkeypatch.setenv("M2_F32_STATES", force)
-    else:
-        monkeypatch.delenv("M2_F32_STATES", raising=False)
     cfg = dataclasses.replace(configs.CONFIGS[name], dtype=dtype)
     c = dataclasses.replace(cfg, chunk_size=bench.internal_chunk(cfg))
-    assert bench.states_is_fused(c) == fused
-    assert _workspace_bytes(cfg) == _expected_workspace(cfg, fused)
+    assert bench.states_is_fused(c, force=force) == fused
+    if force:
+        with L.dispatch_override("f32_states", force):
+            assert _workspace_bytes(cfg) == _expected_workspace(cfg, fused)
+    else:
+        assert _workspace_bytes(cfg) == _expected_workspace(cfg, fused)

@@ -138,3 +138,19 @@ def test_python_wrappers_reject_cpu_tensors_and_bad_shapes():
     with pytest.raises(ValueError):
         mamba_chunk_scan_combined_fwd(torch.zeros(1, 8, 2, 4), dt, torch.zeros(2),
                                       torch.zeros(1, 8, 1, 4), torch.zeros(1, 8, 1, 4), 4)
+
+
+def test_dispatch_override_hook_without_gpu():
+    """The testing hook m2_set_dispatch_override: unknown knobs and values are
+    refused, the previous value comes back, the context manager restores it."""
+    lib = L.load_library()
+    assert lib.m2_set_dispatch_override(7, 1) == -1
+    assert lib.m2_set_dispatch_override(0, 9) == -1
+    assert lib.m2_set_dispatch_override(0, 2) == 0
+    assert lib.m2_set_dispatch_override(0, 0) == 2
+    with L.dispatch_override("states_split", "pair128"):
+        with L.dispatch_override("f32_states", "staged"):
+            assert lib.m2_set_dispatch_override(1, 2) == 2
+        assert lib.m2_set_dispatch_override(0, 3) == 3
+    assert lib.m2_set_dispatch_override(0, 0) == 0
+    assert lib.m2_set_dispatch_override(1, 0) == 0

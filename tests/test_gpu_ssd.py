@@ -1,7 +1,8 @@
 """Parity of the whole SSD forward (mamba_chunk_scan_combined_fwd) on the GPU.
 
 * against the CPU oracle (float64) at the benchmark shapes: c0, c1 and c2 in
-  full, c3 with fewer heads or tokens (the oracle's memory grows with L*H*Q);
+  full, c3 in full one head group at a time (heads are independent) and with
+  fewer heads or tokens;
 * at the full c1 / c3 sizes through size-independent properties: agreement
   with the naive formulation run on the GPU (c1) and packed == per-sequence
   runs (c3);
@@ -17,6 +18,7 @@ import pytest
 import torch
 
 from gpu_util import TOL, announce, check, dev, host, tdtype
+from mamba2_jax import _lib as L
 from mamba2_jax import configs
 from mamba2_jax.kernels import mamba_chunk_scan_combined_fwd
 from mamba2_jax.modules.mamba2 import _ssd_combined_fwd
@@ -175,6 +177,94 @@ def test_c3_full_packed_equals_per_sequence():
     _within_bf16_ulp(fin[0], vs[-1], "final == last varlen state")
 
 
+@pytest.fixture(scope="module")
+def c3_full_run():
+    """The full c3 forward (L 8192, 256 heads in 8 groups, dstate 256, six
+    packed sequences) on the GPU once, through the C ABI with a workspace of
+    the test's own, so that the states entering each chunk (bf16, the slot after
+    dA_cumsum, dt', the weights and the chunk decay of the fused state pass)
+    can be read back; host copies of everything."""
+    import ctypes
+    cfg = configs.CONFIGS["c3"]
+    d = configs.make_ssd_inputs(cfg)
+    t = {k: (v.contiguous() if v is not None else None) for k, v in _dev_inputs(d, cfg.dtype).items()}
+    b, Lq, H, P = t["x"].shape
+    N, Q, nseq = cfg.dstate, cfg.chunk_size, cfg.nseq
+    nc = -(-Lq // Q)
+    y = torch.empty((b, Lq, H, P), dtype=torch.float32, device="cuda")
+    fin = torch.empty((b, H, P, N), dtype=torch.float32, device="cuda")
+    vs = torch.empty((nseq, H, P, N), dtype=torch.float32, device="cuda")
+    a = L.SsdCombinedArgs(
+        x=L.ptr(t["x"]), dt=L.ptr(t["dt"]), A=L.ptr(t["A"]), B=L.ptr(t["B"]), C=L.ptr(t["C"]),
+        D=L.ptr(t["D"]), dt_bias=L.ptr(t["dt_bias"]), seq_idx=L.ptr(t["seq_idx"]),
+        cu_seqlens=L.ptr(t["cu_seqlens"]), out=L.ptr(y), final_states=L.ptr(fin),
+        varlen_states=L.ptr(vs), batch=b, seqlen=Lq, nheads=H, headdim=P, ngroups=cfg.ngroups,
+        dstate=N, chunk_size=Q, nseq=nseq, dtype=L.M2_BF16, dt_dtype=L.M2_BF16, dt_softplus=1,
+        dt_min=0.0, dt_max=float("inf"))
+    lib = L.load_library()
+    need = lib.m2_ssd_combined_workspace_size(ctypes.byref(a))
+    al = lambda v: (v + 255) // 256 * 256
+    cq = b * H * nc * Q
+    off = 3 * al(4 * cq) + al(4 * b * H * nc)            # dA_cumsum, dt', weights, decay
+    S = b * nc * H * P * N
+    assert need == off + al(2 * S), "workspace layout of the fused bf16 path"
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    a.workspace, a.workspace_bytes = ws.data_ptr(), need
+    L.call("m2_ssd_combined", a, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    passed = ws[off:off + 2 * S].view(torch.bfloat16).view(b, nc, H, P, N)
+    host32 = lambda v: v.detach().float().cpu().numpy()
+    return cfg, d, host32(y), host32(fin), host32(vs), host32(passed)
+
+
+@pytest.mark.parametrize("g", range(configs.CONFIGS["c3"].ngroups))
+def test_c3_full_vs_oracle_by_group(c3_full_run, g):
+    """Full c3 against the oracle, one head group at a time: the heads of a
+    group (with its B / C) are independent of every other head, so the oracle
+    evaluated on group g's 32 heads is exactly the full problem's result for
+    them.  At the plain bf16 bar: outputs, final states and the varlen states;
+    the states entering each chunk (bf16) within one bf16 step of the oracle's
+    (plus fp32 summation order), element by element.  The varlen states add exp(dA) * (the
+    state entering the sequence's last chunk, rounded to bf16) -- a rounding
+    point of the reference (kernels/ssd_combined.py:140,
+    kernels/chunk_state_fwd.py:587-595) where one rounding flip, decided by
+    fp32 summation order, can move a large state by more than the bar -- so
+    they are compared with the oracle's chunk_state_varlen fed the states the
+    GPU rounded (the same rounding decisions on both sides)."""
+    cfg, d, y, fin, vs, passed = c3_full_run
+    announce("c3 full vs oracle, group", g)
+    hpg = cfg.nheads // cfg.ngroups
+    hs = slice(g * hpg, (g + 1) * hpg)
+    dg = dict(d, x=d["x"][:, :, hs], dt=d["dt"][:, :, hs], A=d["A"][hs], D=d["D"][hs],
+              dt_bias=d["dt_bias"][hs], B=d["B"][:, :, g:g + 1], C=d["C"][:, :, g:g + 1])
+    want = O.ssd_combined(io_dtype=cfg.dtype, chunk_size=cfg.chunk_size, dt_softplus=True,
+                          return_final_states=True, return_varlen_states=True, **dg)
+    tol = TOL[cfg.dtype]
+    check(y[:, :, hs], want[0], tol, f"group {g} out")
+    check(fin[:, hs], want[1], tol, f"group {g} final_states")
+    dA, dto = O.chunk_cumsum(dg["dt"], dg["A"], cfg.chunk_size, dg["dt_bias"], True)
+    st = O.chunk_state(dg["B"], dg["x"], dto, dA, seq_idx=d["seq_idx"])
+    b, nc, Hg, P, N = st.shape
+    sp, _ = O.state_passing(st.reshape(b, nc, Hg, P * N), dA[:, :, :, -1],
+                            seq_idx=d["seq_idx"], chunk_size=cfg.chunk_size)
+    # bf16 values rounded from fp32 sums of different order: element by
+    # element equal or one bf16 step apart (2^-7 of the larger magnitude), on
+    # top of the fp32 summation-order difference before the rounding (1e-5 of
+    # the largest state)
+    wp = O.bf16_round(sp).reshape(b, nc, Hg, P, N).astype(np.float64)
+    gp = passed[:, :, hs].astype(np.float64)
+    allow = 2.0 ** -7 * np.maximum(np.abs(gp), np.abs(wp)) + 1e-5 * np.abs(wp).max()
+    excess = np.abs(gp - wp) / allow
+    print(f"  group {g} states entering each chunk: {np.mean(gp != wp):.2e} of them differ, "
+          f"max |diff| / (one bf16 step + 1e-5 max) = {excess.max():.3f} (tol 1)", flush=True)
+    assert excess.max() <= 1.0
+    wv = O.chunk_state_varlen(dg["B"][0], dg["x"][0], dto[0], dA[0], d["cu_seqlens"],
+                              passed[0][:, hs])
+    check(vs[:, hs], wv, tol, f"group {g} varlen_states")
+    e = O.rel_err(vs[:, hs], want[2])
+    print(f"  group {g} varlen_states vs the oracle's own rounding: {e:.3e}", flush=True)
+
+
 def _within_bf16_ulp(got, want, what):
     g, w = host(got), host(want)
     e = float(np.max(np.abs(g - w)) / np.max(np.abs(w)))
@@ -215,7 +305,7 @@ def test_return_arity_and_dispatch():
 
 
 # The fused state pass splits its work one of three ways, chosen from the
-# shape (M2_STATES_KERNEL forces one where the shape allows it): a head in
+# shape (the states_split override forces one where the shape allows it): a head in
 # 64-column halves, a pair of heads x 64 columns, a pair of heads x 128
 # columns.  Each must match the oracle with an initial state, ragged lengths,
 # batch > 1, sequence resets, dstate 64 / 128 / 256.
@@ -230,15 +320,15 @@ _SPLIT_CASES = {
 
 @pytest.mark.parametrize("split", ["halves", "pair64", "pair128"])
 @pytest.mark.parametrize("case", sorted(_SPLIT_CASES))
-def test_state_pass_splits(case, split, monkeypatch):
+def test_state_pass_splits(case, split):
     announce("state-pass split", case, split)
-    monkeypatch.setenv("M2_STATES_KERNEL", split)
     cfg = _SPLIT_CASES[case]
     d = configs.make_ssd_inputs(cfg)
     kw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True)
     t = _dev_inputs(d, cfg.dtype)
     t.pop("cu_seqlens")
-    got = mamba_chunk_scan_combined_fwd(**t, **kw)
+    with L.dispatch_override("states_split", split):
+        got = mamba_chunk_scan_combined_fwd(**t, **kw)
     d = dict(d, cu_seqlens=None)
     want = O.ssd_combined(io_dtype=cfg.dtype, **d, **kw)
     check(got[0], want[0], TOL[cfg.dtype], "out")
@@ -246,12 +336,12 @@ def test_state_pass_splits(case, split, monkeypatch):
 
 
 @pytest.mark.parametrize("split", ["pair64", "pair128"])
-def test_state_pass_pair_splits_varlen(split, monkeypatch):
+def test_state_pass_pair_splits_varlen(split):
     """Packed sequences through the pair splits: outputs, final and varlen states."""
     announce("state-pass pair split, varlen", split)
-    monkeypatch.setenv("M2_STATES_KERNEL", split)
     cfg = dataclasses.replace(configs.CONFIGS["c3"], seqlen=2048, nheads=32, min_seqlen=64)
-    _run_and_check(cfg, varlen=True)
+    with L.dispatch_override("states_split", split):
+        _run_and_check(cfg, varlen=True)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -327,7 +417,7 @@ def test_fp32_cumsum_in_chunk_state(H, G, N, Q, L, packed):
 
 
 # fp32 through the fused state pass (chosen from 256 workgroups up, forced by
-# M2_F32_STATES=fused on these smaller shapes): initial states, batch > 1,
+# the f32_states override on these smaller shapes): initial states, batch > 1,
 # ragged lengths, sequence resets with varlen states, dstate 64 / 256, chunk
 # 64 and 256 (run as 128), z and D per head-dim
 _F32_FUSED_CASES = {
@@ -340,11 +430,11 @@ _F32_FUSED_CASES = {
 
 
 @pytest.mark.parametrize("case", sorted(_F32_FUSED_CASES))
-def test_fp32_fused_state_pass(case, monkeypatch):
+def test_fp32_fused_state_pass(case):
     announce("fp32 fused state pass", case)
-    monkeypatch.setenv("M2_F32_STATES", "fused")
     cfg = _F32_FUSED_CASES[case]
-    _run_and_check(cfg, with_z=True, Dhp=True, varlen=cfg.nseq > 0)
+    with L.dispatch_override("f32_states", "fused"):
+        _run_and_check(cfg, with_z=True, Dhp=True, varlen=cfg.nseq > 0)
 
 
 def test_c2_full_fp32():
@@ -354,11 +444,15 @@ def test_c2_full_fp32():
     _run_and_check(dataclasses.replace(configs.CONFIGS["c2"], dtype="f32"))
 
 
-def test_fp32_fused_state_pass_graph_replays(monkeypatch):
+def test_fp32_fused_state_pass_graph_replays():
     """The fp32 fused state pass inside a captured combined forward: replays
     equal the eager result bit for bit."""
     announce("fp32 fused state pass, graph replays")
-    monkeypatch.setenv("M2_F32_STATES", "fused")
+    with L.dispatch_override("f32_states", "fused"):
+        _fp32_fused_graph_replays()
+
+
+def _fp32_fused_graph_replays():
     cfg = dataclasses.replace(configs.CONFIGS["c0"], seqlen=1000, init_state=True)
     d = configs.make_ssd_inputs(cfg)
     t = _dev_inputs(d, "f32")

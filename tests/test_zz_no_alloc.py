@@ -111,3 +111,36 @@ def test_noalloc_rejects_oversized_problem():
     with pytest.raises(L.M2Error) as e:
         L.call("m2_ssd_combined_noalloc", a, torch.cuda.current_stream().cuda_stream)
     assert e.value.code == -4 and "static scratch" in str(e.value)
+
+
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture():
+    """m2_ssd_combined_noalloc captured in a HIP graph after
+    m2_ssd_combined_noalloc_prepare (the first call on a device looks the
+    scratch up, which a capturing stream must not see): every replay, with an
+    eager noalloc call on other inputs between replays (it overwrites the
+    shared scratch), equals the workspace entry point bit for bit."""
+    announce("noalloc under graph capture")
+    lib = L.load_library()
+    assert lib.m2_ssd_combined_noalloc_prepare() == 0
+    rng = np.random.default_rng(77)
+    t = _inputs(rng, 1, 1000, 16, 2, 64, 128, "bf16", True)
+    (ow, fw), _ = _run_both(t, 128, "bf16")
+    other = _inputs(rng, 1, 700, 8, 1, 64, 64, "bf16", False)
+    out = torch.full_like(ow, float("nan"))
+    fin = torch.full_like(fw, float("nan"))
+    an = _args(dict(t, out=out), 128, L.M2_BF16, fin=fin)
+    ao = _args(other, 128, L.M2_BF16)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        L.call("m2_ssd_combined_noalloc", an, torch.cuda.current_stream().cuda_stream)
+    for r in range(3):
+        L.call("m2_ssd_combined_noalloc", ao, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        out.fill_(float("nan"))
+        fin.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ow), f"replay {r}: outputs differ"
+        assert torch.equal(fin, fw), f"replay {r}: final states differ"
