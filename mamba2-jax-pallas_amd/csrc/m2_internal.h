@@ -62,9 +62,10 @@ struct ScanFusedArgs {
     int hps, nslice;          // heads per workgroup (a slice of the group's), slices
 };
 // the chunk-128 scan kernel (csrc/ssd_scan128.hip) for dstate 32 * ns (ns 2, 4,
-// 8), with the z gate / with CB given; NULL for other sizes; its block size
+// 8), with the z gate / with CB given / with non-temporal output stores (not
+// with CB given); NULL for other sizes; its block size
 typedef void (*ScanKernel)(ScanFusedArgs);
-ScanKernel scan_q128_kernel(int ns, bool hasz, bool cbin);
+ScanKernel scan_q128_kernel(int ns, bool hasz, bool cbin, bool nt);
 constexpr int SCAN_Q128_THREADS = 768;
 
 // fused bmm_chunk + chunk_scan of the combined forward (bf16 inputs)

@@ -58,6 +58,13 @@ constexpr int Q = 128, QT = 8;
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int LDS_BYTES = 160 * 1024;
 
+// a 16-byte output store, non-temporal for NT (a compile-time choice: the
+// compiler merges the two stores of a runtime branch and drops the hint)
+template <bool NT> M2_DEV void store_out(const f32x4& v, float* p) {
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+    else *reinterpret_cast<f32x4*>(p) = v;
+}
+
 template <int V> using IC = std::integral_constant<int, V>;
 
 M2_DEV f32x4 mma16(bf16x4 a, bf16x4 b, f32x4 c) {
@@ -116,7 +123,7 @@ struct Units {
     static constexpr int kt(int u) { return u < NL ? (KH ? 4 + u : u) : u < NOFF ? u - NL : TM; }
 };
 
-template <int NS, bool HASZ, bool CBIN, int PI, int KH>
+template <int NS, bool HASZ, bool CBIN, bool NT, int PI, int KH>
 M2_DEV void compute_path(const ScanFusedArgs& a, char* ring, f32x4 (*xchg)[4][64], float* ftab,
                          char* stg, const int* seqs, int bi, int ci, int g, int h0, int nh,
                          int valid, int seq_prev) {
@@ -423,15 +430,15 @@ M2_DEV void compute_path(const ScanFusedArgs& a, char* ring, f32x4 (*xchg)[4][64
                 *reinterpret_cast<float4*>(stg + w * S::STW + ln * 256 + 16 * c) =
                     make_float4(v[0], v[1], v[2], v[3]);
             } else if (mrow < valid) {
-                *reinterpret_cast<float4*>(a.out + ((tok0 + mrow) * H + h) * P + 16 * pt + 4 * kg) =
-                    make_float4(v[0], v[1], v[2], v[3]);
+                const f32x4 o = {v[0], v[1], v[2], v[3]};
+                store_out<NT>(o, a.out + ((tok0 + mrow) * H + h) * P + 16 * pt + 4 * kg);
             }
         }
     }
     if (S::STAGE) lds_barrier();                              // the last head's outputs staged
 }
 
-template <int NS, bool HASZ, bool CBIN>
+template <int NS, bool HASZ, bool CBIN, bool NT>
 __global__ void __launch_bounds__(THREADS) k_scan_q128(ScanFusedArgs a) {
     typedef Cfg<NS> S;
     constexpr int N = S::N, SCPR = S::SCPR, R = S::R, XB = S::XB, SB = S::SB, SLOT = S::SLOT;
@@ -463,7 +470,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_q128(ScanFusedArgs a) {
     if (w < NWAVES) {
         // one instantiation of the compute path per (pair, half)
 #define M2_Q128_CASE(W) \
-        case W: compute_path<NS, HASZ, CBIN, ((W) & 3), ((W) >> 2)>(a, ring, xchg, ftab, stg, seqs, bi, ci, g, h0, nh, valid, seq_prev); break;
+        case W: compute_path<NS, HASZ, CBIN, NT, ((W) & 3), ((W) >> 2)>(a, ring, xchg, ftab, stg, seqs, bi, ci, g, h0, nh, valid, seq_prev); break;
         switch (w) {
             M2_Q128_CASE(0) M2_Q128_CASE(1) M2_Q128_CASE(2) M2_Q128_CASE(3)
             M2_Q128_CASE(4) M2_Q128_CASE(5) M2_Q128_CASE(6) M2_Q128_CASE(7)
@@ -531,10 +538,10 @@ __global__ void __launch_bounds__(THREADS) k_scan_q128(ScanFusedArgs a) {
             for (int it = 0; it < 4; ++it) {
                 const int o = 1024 * it + 16 * lane;
                 const int row = o / 256, c = ((o % 256) / 16) ^ row;
-                const float4 v = *reinterpret_cast<const float4*>(stg + cw * S::STW + o);
+                const f32x4 v = *reinterpret_cast<const f32x4*>(stg + cw * S::STW + o);
                 const int m = 16 * ct + row;
                 if (m < valid)
-                    *reinterpret_cast<float4*>(a.out + ((tok0 + m) * H + h) * P + 4 * c) = v;
+                    store_out<NT>(v, a.out + ((tok0 + m) * H + h) * P + 4 * c);
             }
         }
     };
@@ -562,10 +569,11 @@ __global__ void __launch_bounds__(THREADS) k_scan_q128(ScanFusedArgs a) {
 
 namespace m2 {
 
-ScanKernel scan_q128_kernel(int ns, bool hasz, bool cbin) {
-#define M2_Q128_PICK(NSV)                                                         \
-    if (ns == NSV) return cbin ? k_scan_q128<NSV, false, true>                    \
-                               : hasz ? k_scan_q128<NSV, true, false> : k_scan_q128<NSV, false, false>;
+ScanKernel scan_q128_kernel(int ns, bool hasz, bool cbin, bool nt) {
+#define M2_Q128_PICK(NSV)                                                                  \
+    if (ns == NSV) return cbin ? k_scan_q128<NSV, false, true, false>                      \
+                         : hasz ? (nt ? k_scan_q128<NSV, true, false, true> : k_scan_q128<NSV, true, false, false>) \
+                                : (nt ? k_scan_q128<NSV, false, false, true> : k_scan_q128<NSV, false, false, false>);
     M2_Q128_PICK(2) M2_Q128_PICK(4) M2_Q128_PICK(8)
 #undef M2_Q128_PICK
     return nullptr;
