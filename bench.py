@@ -59,9 +59,10 @@ def internal_chunk(cfg):
     return Q if Q in (64, 128, 256) else 128
 
 
-def stage_work(cfg, with_init=False, with_z=False):
+def stage_work(cfg, with_init=False, with_z=False, cu_seqlens=None):
     """Algorithmic (compulsory) HBM bytes and flops per launch of each stage, as
-    the combined path runs them (CB and the carried states in the input dtype)."""
+    the combined path runs them (CB and the carried states in the input dtype);
+    with cu_seqlens (packed sequences, batch 1) also the varlen final states."""
     import dataclasses
     cfg = dataclasses.replace(cfg, chunk_size=internal_chunk(cfg))
     s = 2 if cfg.dtype == "bf16" else 4
@@ -107,12 +108,25 @@ def stage_work(cfg, with_init=False, with_z=False):
         w[FUSED_STATES] = (b * L * H * P * s + b * L * G * N * s + 4 * cq + 4 * b * H * nc
                            + s * S + 4 * b * H * P * N + (4 * b * H * P * N if with_init else 0),
                            2 * b * L * H * P * N + 2 * S)
+    if cu_seqlens is not None:
+        # per sequence: x and B rows of its last chunk, that chunk's dA_cumsum /
+        # dt', the state entering it (when the sequence started earlier) and
+        # the fp32 final state out
+        cu = [int(v) for v in cu_seqlens]
+        by = fl = 0
+        for s0, s1 in zip(cu[:-1], cu[1:]):
+            c0 = (s1 - 1) // Q * Q
+            by += (Q * H * P + Q * G * N) * s + 8 * H * Q + 4 * H * P * N
+            by += s * H * P * N if s0 < c0 else 0
+            fl += 2 * 2 * (s1 - max(s0, c0)) * H * P * N
+        w[VARLEN] = (by, fl)
     return w
 
 
 FUSED_STATES = "chunk_state+state_passing"
 FUSED_CUMSUM = "chunk_cumsum+chunk_state"
 FUSED_PASS_BMM = "state_passing+bmm_chunk"
+VARLEN = "chunk_state_varlen"
 
 
 def pass_bmm_fused(cfg):
@@ -525,7 +539,7 @@ def stage_events(cfg, steps):
     icfg = dataclasses.replace(cfg, chunk_size=internal_chunk(cfg))
     fs, fc = states_is_fused(icfg), scan_is_fused(icfg)
     fcs, fpb = cumsum_in_state(icfg), pass_bmm_fused(icfg)
-    keep = [True, not fcs, True, not (fs or fpb), not fc, True]
+    keep = [True, not fcs, True, not (fs or fpb), not fc, True, cfg.nseq > 0]
     evs = [[hev.new() if k else None for k in keep] for _ in range(steps)]
     return hev, evs, keep, fs, fc
 
@@ -541,9 +555,12 @@ def _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc):
         if not keep[j + 1]:
             return 0.0
         return float(np.mean([hev.elapsed_ms(evs[i][a], evs[i][j + 1]) for i in range(steps)]))
-    slot_ms = [slot(j) for j in range(5)]
-    total = float(np.mean([hev.elapsed_ms(evs[i][0], evs[i][5]) for i in range(steps)]))
-    work = stage_work(cfg, with_init=kw["initial_states"] is not None)
+    slot_ms = [slot(j) for j in range(6 if keep[6] else 5)]
+    last = 6 if keep[6] else 5
+    total = float(np.mean([hev.elapsed_ms(evs[i][0], evs[i][last]) for i in range(steps)]))
+    cu = kw.get("cu_seqlens")
+    work = stage_work(cfg, with_init=kw["initial_states"] is not None,
+                      cu_seqlens=None if cu is None or not keep[6] else cu.cpu().tolist())
     slots = dict(zip(STAGES, slot_ms))
     if fs:
         first = {"chunk_cumsum": slots["chunk_cumsum"], FUSED_STATES: slots["chunk_state"]}
@@ -560,6 +577,8 @@ def _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc):
         first.pop("state_passing")
         first[FUSED_PASS_BMM] = second.pop("bmm_chunk")
     stage_ms = {**first, **second}
+    if keep[6]:
+        stage_ms[VARLEN] = slot_ms[5]
     peak_mfma = PEAK_MFMA_TFLOPS[cfg.dtype]
     stages = {}
     for s in stage_ms:

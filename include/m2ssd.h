@@ -207,10 +207,11 @@ typedef struct {
     int32_t dtype, dt_dtype;
     int32_t D_has_hdim, dt_softplus;
     float   dt_min, dt_max;
-    void**         stage_events;    /* optional profiling hook: NULL, or 6
-                                       hipEvent_t recorded before stage 1 and
-                                       after each of the 5 stages; a NULL
-                                       entry is not recorded                */
+    void**         stage_events;    /* optional profiling hook: NULL, or 7
+                                       hipEvent_t recorded before stage 1,
+                                       after each of the 5 stages and after
+                                       the varlen states (when requested); a
+                                       NULL entry is not recorded           */
 } m2_ssd_combined_args;
 size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a);
 int m2_ssd_combined(const m2_ssd_combined_args* a, void* stream);

@@ -270,6 +270,7 @@ int m2::ssd_combined_on(const m2_ssd_combined_args& a0, void* workspace, size_t 
         c6.ngroups = a.ngroups; c6.dstate = a.dstate; c6.nchunks = nc; c6.chunk_size = a.chunk_size;
         c6.dtype = a.dtype; c6.states_dtype = a.dtype;
         if ((rc = m2::launch_chunk_state_varlen(c6, s))) return rc;
+        if ((rc = record(a.stage_events, 6, s))) return rc;
     }
     return M2_OK;
 }

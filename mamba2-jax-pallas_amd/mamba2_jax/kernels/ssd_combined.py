@@ -23,18 +23,18 @@ from .chunk_state_fwd import _io_dtype, _seq_idx
 
 
 def _events_array(events):
-    """Raw hipEvent_t handles of 6 events: torch.cuda.Event objects (created on
+    """Raw hipEvent_t handles of 7 events: torch.cuda.Event objects (created on
     first record), objects with a raw `cuda_event` handle, or None (that point
     is not recorded)."""
     import ctypes
     if events is None:
         return None, None
-    if len(events) != 6:
-        raise ValueError("_stage_events needs 6 events")
+    if len(events) != 7:
+        raise ValueError("_stage_events needs 7 events")
     for e in events:
         if isinstance(e, torch.cuda.Event) and not e.cuda_event:
             e.record()          # forces creation of the underlying event
-    arr = (ctypes.c_void_p * 6)(*[None if e is None else e.cuda_event for e in events])
+    arr = (ctypes.c_void_p * 7)(*[None if e is None else e.cuda_event for e in events])
     return arr, ctypes.cast(arr, ctypes.c_void_p).value
 
 
@@ -55,9 +55,9 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
     dstate) if return_varlen_states -- the reference's arity
     (kernels/ssd_combined.py:194-203).
 
-    ``_stage_events`` (optional, 6 events) is a profiling hook: the events are
-    recorded before the first and after each of the five stages; None entries
-    are skipped.
+    ``_stage_events`` (optional, 7 events) is a profiling hook: the events are
+    recorded before the first and after each of the five stages, and after the
+    varlen states when they are requested; None entries are skipped.
     """
     L.device_of(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, cu_seqlens)
     L.require(x.dim() == 4, "x must be (batch, seqlen, nheads, headdim)")
