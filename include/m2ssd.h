@@ -435,6 +435,10 @@ int m2_skinny_gemm_norm(const m2_skinny_gemm_norm_args* a, void* stream);
                                      staged chunk_state + state_passing        */
 #define M2_KNOB_ONESHOT_HEADS 2   /* one-shot state kernel: 1 one head per
                                      workgroup                                 */
+#define M2_KNOB_F32_SCAN      3   /* fp32 chunk_scan (chunk 128, head dim 64):
+                                     1 one workgroup per (chunk, head); v >= 2
+                                     one per (chunk, group, slice of v - 1 of
+                                     the group's heads)                        */
 int m2_set_dispatch_override(int knob, int value);
 
 /* thread-local message for the last non-zero return code of this thread */

@@ -26,11 +26,26 @@ int check_launch(const char* what) {
     return M2_OK;
 }
 
-constexpr int NKNOBS = 3;
+constexpr int NKNOBS = 4;
 static std::atomic<int> g_knob[NKNOBS];
 
 int dispatch_override(int knob) {
     return knob >= 0 && knob < NKNOBS ? g_knob[knob].load(std::memory_order_relaxed) : 0;
+}
+
+// compute units of the current device, queried once per device (256 on
+// MI355X); 256 where the query fails
+int cu_count() {
+    constexpr int MAXDEV = 64;
+    static std::atomic<int> cache[MAXDEV];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+        n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 
 }  // namespace m2
@@ -39,7 +54,7 @@ extern "C" const char* m2_last_error(void) { return m2::g_err; }
 extern "C" int m2_abi_version(void) { return M2SSD_ABI_VERSION; }
 
 extern "C" int m2_set_dispatch_override(int knob, int value) {
-    static const int maxval[m2::NKNOBS] = {3, 2, 1};
+    static const int maxval[m2::NKNOBS] = {3, 2, 1, 65};
     if (knob < 0 || knob >= m2::NKNOBS || value < 0 || value > maxval[knob])
         return m2::set_error(M2_ERR_INVALID, "m2_set_dispatch_override: knob %d value %d", knob,
                              value);

@@ -598,6 +598,8 @@ int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t s) {
         if (a.cb_dtype == M2_BF16) return launch_typed<bf16, bf16>(sa, s);
     } else if (a.dtype == M2_F32) {
         M2_REQUIRE(a.dstate % 32 == 0, M2_ERR_UNSUPPORTED, "chunk_scan: f32 needs dstate %% 32 == 0");
+        // chunk 128, head dim 64, fp32 CB and states: the group kernel
+        if (scan_f32g_supported(a)) return launch_scan_f32g(a, s);
         // split planes when they fit (head dim 32 / 64): x, C and states fp32
         if (sa.P == 64 && sa.states_same && f32_scan_lds(sa.Q, sa.P, sa.N) <= 160 * 1024) {
             const int rc = a.cb_dtype == M2_F32 ? launch_f32<float>(sa, s)

@@ -9,6 +9,8 @@ namespace m2 {
 // The value m2_set_dispatch_override last set for a knob (M2_KNOB_*); 0 =
 // the automatic choice.
 int dispatch_override(int knob);
+// compute units of the current device (queried once per device)
+int cu_count();
 
 int launch_chunk_cumsum(const m2_chunk_cumsum_args& a, hipStream_t stream);
 // chunk_cumsum that also writes the chunk-state weights wts [b, H, nc, Q] and
@@ -28,6 +30,12 @@ bool state_passing_bmm_supported(const m2_state_passing_args& p, const m2_bmm_ch
 int launch_state_passing_bmm(const m2_state_passing_args& p, const m2_bmm_chunk_args& m,
                              hipStream_t stream);
 int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t stream);
+// chunk_scan for fp32 x / C / CB / states at chunk 128, head dim 64, dstate 64 /
+// 128: one workgroup per (batch, chunk, group, slice of the group's heads)
+// (csrc/scan_f32g.hip)
+bool scan_f32g_supported(const m2_chunk_scan_args& a);
+int launch_scan_f32g(const m2_chunk_scan_args& a, hipStream_t stream);
+int scan_f32g_heads_per_wg(int64_t batch, int64_t nc, int64_t G, int64_t hpg, int64_t N);
 int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t stream);
 int launch_ssu(const m2_ssu_args& a, hipStream_t stream);
 int launch_causal_conv1d(const m2_causal_conv1d_args& a, hipStream_t stream);

@@ -168,6 +168,7 @@ KNOBS = {
     "states_split": (0, {"halves": 1, "pair64": 2, "pair128": 3}),
     "f32_states": (1, {"fused": 1, "staged": 2}),
     "oneshot_heads": (2, {"1": 1}),
+    "f32_scan": (3, {"per_head": 1, **{f"group{n}": n + 1 for n in range(1, 65)}}),
 }
 
 

@@ -154,3 +154,14 @@ def test_dispatch_override_hook_without_gpu():
         assert lib.m2_set_dispatch_override(0, 3) == 3
     assert lib.m2_set_dispatch_override(0, 0) == 0
     assert lib.m2_set_dispatch_override(1, 0) == 0
+    assert lib.m2_set_dispatch_override(3, 66) == -1
+    with L.dispatch_override("f32_scan", "per_head"):
+        assert lib.m2_set_dispatch_override(3, 3) == 1
+    assert lib.m2_set_dispatch_override(3, 0) == 0      # restored on exit
+    with L.dispatch_override("f32_scan", "group16"):
+        assert lib.m2_set_dispatch_override(3, 17) == 17
+    assert lib.m2_set_dispatch_override(3, 0) == 0
+    # the knob numbers of the header are the ones the Python table uses
+    hdr = open(HEADER).read()
+    defs = {n.lower(): int(v) for n, v in re.findall(r"#define M2_KNOB_(\w+)\s+(\d+)", hdr)}
+    assert defs == {k: v[0] for k, v in L.KNOBS.items()}

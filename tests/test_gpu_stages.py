@@ -249,6 +249,59 @@ def test_chunk_scan(cfg, dtype):
         assert out_x is None
 
 
+F32_GROUP = [
+    # (b, L, H, G, N, D per head dim, z, seq_lengths, heads per workgroup: 0 = the
+    # launcher's choice)
+    (2, 300, 8, 2, 128, True, True, None, 3),            # slices of 3 + 1, last chunk 44 rows
+    (1, 512, 24, 1, 128, False, False, None, 2),         # mamba2-130m heads, 12 slices
+    (1, 384, 8, 4, 64, False, True, [[100, 284]], 2),    # dstate 64: three ring slots
+    (2, 256, 16, 2, 128, True, False, [[60, 196], [256]], 8),
+    (1, 130, 4, 1, 64, True, True, None, 4),             # last chunk of 2 positions
+    (1, 512, 16, 2, 128, True, False, None, 0),
+    (1, 4096, 128, 8, 128, False, False, None, 0),       # nemotron-h-8b shape
+]
+
+
+@pytest.mark.parametrize("case", F32_GROUP)
+def test_chunk_scan_f32_group(case):
+    """fp32 chunk_scan at chunk 128, head dim 64 runs the group kernel (one
+    workgroup per (chunk, group, slice of the group's heads)): against the
+    oracle, and against the per-(chunk, head) kernel (the same bf16-triple
+    products, summed in another order)."""
+    from mamba2_jax._lib import dispatch_override
+    b, L, H, G, N, Dhp, hasz, lens, hps = case
+    P, Q = 64, 128
+    announce("chunk_scan fp32 group kernel", case)
+    d = _inputs(b, L, H, G, P, N, Q, "f32", seed=L + H + N, z=hasz)
+    seq = seq_idx_from_lengths(lens) if lens else None
+    wA, wdt = O.chunk_cumsum(d["dt"], d["A"], Q, d["dt_bias"], True)
+    wA, wdt = wA.astype(np.float32), wdt.astype(np.float32)
+    CB = O.bmm_chunk(d["C"], d["B"], Q, seq_idx=seq).astype(np.float32)
+    nc = math.ceil(L / Q)
+    rng = np.random.default_rng(H + N)
+    states = (0.5 * rng.standard_normal((b, nc, H, P, N))).astype(np.float32)
+    D = rng.uniform(0.5, 1.5, (H, P) if Dhp else H).astype(np.float32)
+    args = (dev(CB), dev(d["x"]), dev(wdt), dev(wA), dev(d["C"]), dev(states))
+    kw = dict(D=dev(D), z=dev(d["z"]), seq_idx=dev(seq))
+    with dispatch_override("f32_scan", f"group{hps}" if hps else "per_head"):
+        if hps:
+            out, out_x = chunk_scan_fwd(*args, **kw)
+        else:
+            ref, ref_x = chunk_scan_fwd(*args, **kw)
+    if hps:
+        with dispatch_override("f32_scan", "per_head"):
+            ref, ref_x = chunk_scan_fwd(*args, **kw)
+    else:
+        out, out_x = chunk_scan_fwd(*args, **kw)
+    wo, wox = O.chunk_scan(CB, d["x"], wdt, wA, d["C"], states, D=D, z=d["z"], seq_idx=seq,
+                           round_fn=O.round_fn_for("f32"))
+    check(out, wo, TOL["f32"], "out")
+    check(out, host(ref), 2e-5, "out, group vs per-head kernel")
+    if hasz:
+        check(out_x, wox, TOL["f32"], "out_x")
+        check(out_x, host(ref_x), 2e-5, "out_x, group vs per-head kernel")
+
+
 def test_chunk_scan_bf16_cb_and_states():
     """cb and states given in bf16 (the combined path's internal formats)."""
     b, L, H, P, N, G, Q = 1, 256, 8, 64, 128, 2, 128
