@@ -133,7 +133,7 @@ def pass_bmm_fused(cfg):
     """fp32 inputs whose bmm_chunk takes the tiled kernel (fewer than 128
     (chunk, group) blocks, or chunk / dstate outside 64 / 128): state_passing
     and bmm_chunk run in one launch (m2::state_passing_bmm_supported)."""
-    if cfg.dtype != "f32" or states_is_fused(cfg):
+    if cfg.dtype != "f32" or states_is_fused(cfg) or scan_is_fused(cfg):
         return False
     Q, K = cfg.chunk_size, cfg.dstate
     nblocks = cfg.batch * math.ceil(cfg.seqlen / Q) * cfg.ngroups
@@ -164,9 +164,20 @@ def states_is_fused(cfg, force=None):
     return force == "fused" or cfg.batch * cfg.nheads * (cfg.dstate // 64) >= 256
 
 
-def scan_is_fused(cfg):
+def scan_is_fused(cfg, states_fused=None):
     """The combined path fuses bmm_chunk into chunk_scan for bf16, headdim 64,
-    dstate 64/128/256 and chunk_size 64/128 (m2::scan_fused_supported)."""
+    dstate 64/128/256 and chunk_size 64/128 (m2::scan_fused_supported), and for
+    fp32, headdim 64, dstate 64/128 at chunk 128, where the group scan builds
+    CB itself (layer_scan_builds_cb in csrc/capi.hip); `states_fused` gives the
+    state pass choice where a testing override forces it."""
+    if cfg.dtype == "f32":
+        if states_fused is None:
+            states_fused = states_is_fused(cfg)
+        # except where state_passing carries bmm_chunk in its launch (fewer
+        # than 128 (chunk, group) blocks on the staged path)
+        nblocks = cfg.batch * math.ceil(cfg.seqlen / cfg.chunk_size) * cfg.ngroups
+        return (cfg.headdim == 64 and cfg.dstate in (64, 128) and cfg.chunk_size == 128
+                and cfg.nheads % cfg.ngroups == 0 and (states_fused or nblocks >= 128))
     return (cfg.dtype == "bf16" and cfg.headdim == 64 and cfg.dstate in (64, 128, 256)
             and cfg.chunk_size in (64, 128))
 

@@ -35,7 +35,13 @@ int launch_chunk_scan(const m2_chunk_scan_args& a, hipStream_t stream);
 // (csrc/scan_f32g.hip)
 bool scan_f32g_supported(const m2_chunk_scan_args& a);
 int launch_scan_f32g(const m2_chunk_scan_args& a, hipStream_t stream);
-int scan_f32g_heads_per_wg(int64_t batch, int64_t nc, int64_t G, int64_t hpg, int64_t N);
+// the same kernel in the combined forward, building CB = C B^T itself (no
+// bmm_chunk launch): fp32 inputs at the internal chunk 128, head dim 64,
+// dstate 64 / 128
+bool scan_f32g_layer_supported(const m2_ssd_combined_args& a);
+int launch_scan_f32g_layer(const m2_ssd_combined_args& a, const float* dA, const float* dt_out,
+                           const void* states_passed, hipStream_t stream);
+int scan_f32g_heads_per_wg(int64_t batch, int64_t nc, int64_t G, int64_t hpg, int64_t N, bool cbb);
 int launch_chunk_state_varlen(const m2_chunk_state_varlen_args& a, hipStream_t stream);
 int launch_ssu(const m2_ssu_args& a, hipStream_t stream);
 int launch_causal_conv1d(const m2_causal_conv1d_args& a, hipStream_t stream);

@@ -75,6 +75,7 @@ struct GCfg {
     static constexpr int XI = XB / 1024 / NLOAD, SI = SB / 1024 / NLOAD;
     static constexpr int SRPI = 1024 / SROW;           // state rows per direct load
     static constexpr int SPR = SROW / 16;              // 16-byte pieces per fp32 state row
+    static constexpr int BI = Q * SROW / 1024 / NLOAD; // CBB: direct loads of B rows per load wavefront
     // loads of one load wavefront that may still be in flight when head i
     // must have landed: those of the R - 2 later heads (+ one aux load for the
     // wavefronts that bring dA, dt or D)
@@ -83,6 +84,7 @@ struct GCfg {
     static_assert(XI * 4 * NLOAD == Q && SI * SRPI * NLOAD == P, "rows per load wavefront");
     static_assert(WAITA <= 63, "vmcnt range");
     static_assert(R * SLOT <= LDS_BYTES, "LDS budget");
+    static_assert(Q * SROW <= XB + SB && BI * SRPI * NLOAD == Q, "B rows fit a slot");
 };
 
 // x plane piece layout: byte offset in row r of the 4 bf16 of columns
@@ -115,7 +117,8 @@ M2_DEV float ex2(float v) { return __builtin_amdgcn_exp2f(v); }
 struct GArgs {
     const float* x;
     const float* C;
-    const float* cb;        // [b, nc, G, Q, Q]
+    const float* B;         // [b, L, G, N] (CBB: CB built here)
+    const float* cb;        // [b, nc, G, Q, Q] (given CB)
     const float* states;    // [b, nc, H, P, N]
     const float* dt;        // [b, H, nc, Q]
     const float* dA;        // [b, H, nc, Q]
@@ -128,7 +131,11 @@ struct GArgs {
     int L, H, G, nc, hpg, hps, nslice, nwork;
 };
 
-template <int NS, bool HASZ>
+// CBB: CB = C B^T (seq_idx-masked) is built here from the group's B rows,
+// which pass through the second ring slot (as hi / lo planes laid out like
+// the state rows) before the second head is loaded: the layer then needs no
+// bmm_chunk launch and no CB buffer.
+template <int NS, bool HASZ, bool CBB>
 __global__ void __launch_bounds__(THREADS) k_scan_f32g(GArgs a) {
     typedef GCfg<NS> Cf;
     constexpr int N = Cf::N, SROW = Cf::SROW, XB = Cf::XB, SB = Cf::SB, SLOT = Cf::SLOT;
@@ -223,18 +230,62 @@ __global__ void __launch_bounds__(THREADS) k_scan_f32g(GArgs a) {
             }
         };
         const bool aux = li < 2 || (li == 2 && hasD);
+        if constexpr (CBB) {
+            // the group's B rows 32 li .. 32 li + 31 (clamped like x) into the
+            // second slot beside head 0, both split, then two barriers: B
+            // ready, B consumed (the compute wavefronts' CB tiles are built)
+            issue(0, 0);
+            char* const bb = ring + SLOT;
+            const float* bsrc = a.B + (tok0 * a.G + g) * N;
 #pragma unroll
-        for (int i = 0; i < R - 1; ++i) issue(min(i, nh - 1), i);
+            for (int uu = 0; uu < Cf::BI; ++uu) {
+                const int u = li * Cf::BI + uu;
+                const int r = min(Cf::SRPI * u + lane / Cf::SPR, valid - 1);
+                dma16(bsrc + (int64_t)r * a.G * N + 4 * (lane % Cf::SPR), ring_lds + SLOT + 1024 * u);
+            }
+            wait_vmem<0>();
+            split(0);
+            {
+                float4 bv[Cf::BI];
+#pragma unroll
+                for (int uu = 0; uu < Cf::BI; ++uu)
+                    bv[uu] = *reinterpret_cast<const float4*>(bb + 1024 * (li * Cf::BI + uu) + 16 * lane);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+#pragma unroll
+                for (int uu = 0; uu < Cf::BI; ++uu) {
+                    const int r = Cf::SRPI * (li * Cf::BI + uu) + lane / Cf::SPR, fc = lane % Cf::SPR;
+                    uint32_t h0_, l0_, h1_, l1_;
+                    split2(bv[uu].x, bv[uu].y, h0_, l0_);
+                    split2(bv[uu].z, bv[uu].w, h1_, l1_);
+                    char* const rp = bb + r * SROW + ((fc & 1) << 3);
+                    *reinterpret_cast<u2*>(rp + soff<NS>(r, 0, fc >> 1)) = u2{h0_, h1_};
+                    *reinterpret_cast<u2*>(rp + soff<NS>(r, 1, fc >> 1)) = u2{l0_, l1_};
+                }
+            }
+            lds_barrier();                // B planes and head 0 ready
+            lds_barrier();                // B consumed: slots 1 .. R - 1 free
+#pragma unroll
+            for (int i = 1; i < R; ++i)
+                if (R > 2 || i < nh) issue(min(i, nh - 1), i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < R - 1; ++i) issue(min(i, nh - 1), i);
+        }
         for (int i = 0; i < nh; ++i) {
-            // head i complete (later heads may be in flight)
-            if (aux) wait_vmem<Cf::WAITA>();
-            else wait_vmem<Cf::WAITB>();
-            split(i % R);
+            if (!CBB || i > 0) {
+                // head i complete (later heads may be in flight)
+                if (aux) wait_vmem<Cf::WAITA>();
+                else wait_vmem<Cf::WAITB>();
+                split(i % R);
+            }
             lds_barrier();                // slot i % R ready, slot (i - 1) % R free
             // past the last head the last one is loaded again into the free
             // slot (never read), so that every wait above counts the same
-            // loads; with two slots every wait is for all loads
-            if (R > 2 || i + 1 < nh) issue(min(i + R - 1, nh - 1), (i + R - 1) % R);
+            // loads; with two slots every wait is for all loads (CBB: heads
+            // 1 .. R - 1 went out after the B barriers)
+            if ((!CBB || i > 0) && (R > 2 || i + 1 < nh))
+                issue(min(i + R - 1, nh - 1), (i + R - 1) % R);
         }
         wait_vmem<0>();                   // nothing may land after the workgroup ends
         return;
@@ -271,7 +322,54 @@ __global__ void __launch_bounds__(THREADS) k_scan_f32g(GArgs a) {
     // (j & 3) + 16 (j >> 2) (the positions the transposed x reads give this
     // lane group)
     float cbv[4][8];
-    {
+    if constexpr (CBB) {
+        // CB^T tiles [16 k x 16 m] = B[k, :] C[m, :]^T: A operand B rows from
+        // the planes in slot 1, B operand the C fragments above; the
+        // accumulator (lane = m, 4 consecutive k of a 16-row k tile) is the
+        // W^T layout: k tile 2 ks gives j < 4, k tile 2 ks + 1 gives j >= 4.
+        // seq_idx: CB[m, k] = 0 where the sequences of m and k differ.
+        int sq[4][8];
+        if (a.seq_idx) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int k = 32 * ks + 4 * kg + (j & 3) + 16 * (j >> 2);
+                    sq[ks][j] = ks < nks ? a.seq_idx[tok0 + min(k, valid - 1)] : 0;
+                }
+        }
+        const int sm = a.seq_idx ? a.seq_idx[tok0 + mc] : 0;
+        lds_barrier();                    // B planes ready
+        const char* const bb = ring + SLOT;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            f32x4 t0 = zero4(), t1 = zero4();
+            if (ks < nks) {
+#pragma unroll
+                for (int ns = 0; ns < NS; ++ns) {
+                    const int r0 = 32 * ks + ln, r1 = r0 + 16;
+                    const char* const p0 = bb + r0 * SROW;
+                    const char* const p1 = bb + r1 * SROW;
+                    t0 = mma3(*reinterpret_cast<const bf16x8*>(p0 + soff<NS>(r0, 0, 4 * ns + kg)),
+                              *reinterpret_cast<const bf16x8*>(p0 + soff<NS>(r0, 1, 4 * ns + kg)),
+                              ch[ns], cl[ns], t0);
+                    t1 = mma3(*reinterpret_cast<const bf16x8*>(p1 + soff<NS>(r1, 0, 4 * ns + kg)),
+                              *reinterpret_cast<const bf16x8*>(p1 + soff<NS>(r1, 1, 4 * ns + kg)),
+                              ch[ns], cl[ns], t1);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                cbv[ks][j] = t0[j];
+                cbv[ks][4 + j] = t1[j];
+            }
+            if (a.seq_idx)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (sq[ks][j] != sm) cbv[ks][j] = 0.f;
+        }
+        lds_barrier();                    // B consumed
+    } else {
         const float* cbrow = a.cb + (((int64_t)bi * nc + c) * a.G + g) * (int64_t)Q * Q + (int64_t)m * Q;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -388,28 +486,37 @@ __global__ void __launch_bounds__(THREADS) k_scan_f32g(GArgs a) {
 
 namespace m2 {
 
+static bool shape_ok(int64_t headdim, int64_t chunk, int64_t dstate, int64_t H, int64_t G) {
+    return headdim == P && chunk == Q && (dstate == 64 || dstate == 128) && G > 0 && H % G == 0 &&
+           dispatch_override(M2_KNOB_F32_SCAN) != 1;
+}
+
 bool scan_f32g_supported(const m2_chunk_scan_args& a) {
     return a.dtype == M2_F32 && a.states_dtype == M2_F32 && a.cb_dtype == M2_F32 &&
-           a.headdim == P && a.chunk_size == Q && (a.dstate == 64 || a.dstate == 128) &&
-           a.ngroups > 0 && a.nheads % a.ngroups == 0 &&
-           dispatch_override(M2_KNOB_F32_SCAN) != 1;
+           shape_ok(a.headdim, a.chunk_size, a.dstate, a.nheads, a.ngroups);
+}
+
+bool scan_f32g_layer_supported(const m2_ssd_combined_args& a) {
+    return a.dtype == M2_F32 && shape_ok(a.headdim, a.chunk_size, a.dstate, a.nheads, a.ngroups);
 }
 
 // Heads per workgroup: one workgroup per CU (the ring takes 130-148 KB of
 // LDS), so a launch takes ceil(workgroups / CUs) rounds, each as long as a
-// workgroup's C / CB rows plus its heads' x and state tiles take to arrive
-// (the bytes a CU pulls in: C and the causal half of CB against x + state per
-// head).  The smallest cost over slices of at most 8 heads wins: measured at
-// the nemotron-h-8b shape (16 heads per group), two rounds of 8-head slices
-// take 91 us against 95 for one round of whole groups (every workgroup of a
-// single round starts and stops its loads in step with the others) and 103.5
-// for four rounds of 4; at mamba2-130m (24 heads, 16 chunks) slices of 1 / 2 /
-// 3 / 4 heads take 21.5 / 16.6 / 19.7 / 23.2 us, as the cost predicts.  The
-// M2_KNOB_F32_SCAN override (tests) forces value - 1 heads per workgroup.
-int scan_f32g_heads_per_wg(int64_t batch, int64_t nc, int64_t G, int64_t hpg, int64_t N) {
+// workgroup's C and CB (or B) rows plus its heads' x and state tiles take to
+// arrive (the bytes a CU pulls in: C and the causal half of CB, or B, against
+// x + state per head).  The smallest cost over slices of at most 8 heads
+// wins: measured at the nemotron-h-8b shape (16 heads per group, CB given),
+// two rounds of 8-head slices take 91 us against 95 for one round of whole
+// groups (every workgroup of a single round starts and stops its loads in
+// step with the others) and 103.5 for four rounds of 4; at mamba2-130m (24
+// heads, 16 chunks) slices of 1 / 2 / 3 / 4 heads take 21.5 / 16.6 / 19.7 /
+// 23.2 us, as the cost predicts.  The M2_KNOB_F32_SCAN override (tests)
+// forces value - 1 heads per workgroup.
+int scan_f32g_heads_per_wg(int64_t batch, int64_t nc, int64_t G, int64_t hpg, int64_t N, bool cbb) {
     const int forced = dispatch_override(M2_KNOB_F32_SCAN);
     if (forced >= 2) return (int)(forced - 1 < hpg ? forced - 1 : hpg);
-    const double pro = (double)(Q * N * 4 + Q * Q * 4 * 9 / 16) / (double)(Q * P * 4 + P * N * 4);
+    const double cbytes = cbb ? (double)(Q * N * 4) : (double)(Q * Q * 4 * 9 / 16);
+    const double pro = ((double)(Q * N * 4) + cbytes) / (double)(Q * P * 4 + P * N * 4);
     const int64_t cus = cu_count();
     double best = 1e300;
     int hps = 1;
@@ -423,6 +530,23 @@ int scan_f32g_heads_per_wg(int64_t batch, int64_t nc, int64_t G, int64_t hpg, in
     return hps;
 }
 
+static int launch_common(GArgs& k, int64_t batch, int64_t dstate, bool cbb, hipStream_t s) {
+    k.hps = scan_f32g_heads_per_wg(batch, k.nc, k.G, k.hpg, dstate, cbb);
+    k.nslice = (k.hpg + k.hps - 1) / k.hps;
+    const int64_t nwork = batch * k.nc * k.G * k.nslice;
+    M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_scan: too many workgroups");
+    k.nwork = (int)nwork;
+    void (*kern)(GArgs) = nullptr;
+    const bool z = k.z != nullptr;
+#define M2_F32G(NSV) \
+    kern = cbb ? (z ? k_scan_f32g<NSV, true, true> : k_scan_f32g<NSV, false, true>) \
+               : (z ? k_scan_f32g<NSV, true, false> : k_scan_f32g<NSV, false, false>);
+    if (dstate == 64) { M2_F32G(2) } else { M2_F32G(4) }
+#undef M2_F32G
+    kern<<<(unsigned)k.nwork, THREADS, 0, s>>>(k);
+    return check_launch("chunk_scan (fp32 group kernel)");
+}
+
 int launch_scan_f32g(const m2_chunk_scan_args& a, hipStream_t s) {
     M2_REQUIRE(scan_f32g_supported(a), M2_ERR_UNSUPPORTED,
                "chunk_scan: unsupported shape / dtype for the fp32 group kernel");
@@ -434,16 +558,22 @@ int launch_scan_f32g(const m2_chunk_scan_args& a, hipStream_t s) {
     k.L = (int)a.seqlen; k.H = (int)a.nheads; k.G = (int)a.ngroups;
     k.nc = (int)((a.seqlen + Q - 1) / Q);
     k.hpg = (int)(a.nheads / a.ngroups);
-    k.hps = scan_f32g_heads_per_wg(a.batch, k.nc, a.ngroups, k.hpg, a.dstate);
-    k.nslice = (k.hpg + k.hps - 1) / k.hps;
-    const int64_t nwork = a.batch * k.nc * a.ngroups * k.nslice;
-    M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "chunk_scan: too many workgroups");
-    k.nwork = (int)nwork;
-    void (*kern)(GArgs) = nullptr;
-    if (a.dstate == 64) kern = a.z ? k_scan_f32g<2, true> : k_scan_f32g<2, false>;
-    else kern = a.z ? k_scan_f32g<4, true> : k_scan_f32g<4, false>;
-    kern<<<(unsigned)k.nwork, THREADS, 0, s>>>(k);
-    return check_launch("chunk_scan (fp32 group kernel)");
+    return launch_common(k, a.batch, a.dstate, false, s);
+}
+
+int launch_scan_f32g_layer(const m2_ssd_combined_args& a, const float* dA, const float* dt_out,
+                           const void* states_passed, hipStream_t s) {
+    M2_REQUIRE(scan_f32g_layer_supported(a), M2_ERR_UNSUPPORTED,
+               "ssd_combined: unsupported shape / dtype for the fp32 group scan");
+    GArgs k{};
+    k.x = (const float*)a.x; k.C = (const float*)a.C; k.B = (const float*)a.B;
+    k.states = (const float*)states_passed; k.dt = dt_out; k.dA = dA; k.D = a.D;
+    k.z = (const float*)a.z; k.seq_idx = a.seq_idx; k.out = a.out;
+    k.D_has_hdim = a.D_has_hdim;
+    k.L = (int)a.seqlen; k.H = (int)a.nheads; k.G = (int)a.ngroups;
+    k.nc = (int)((a.seqlen + Q - 1) / Q);
+    k.hpg = (int)(a.nheads / a.ngroups);
+    return launch_common(k, a.batch, a.dstate, true, s);
 }
 
 }  // namespace m2

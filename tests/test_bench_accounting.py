@@ -135,7 +135,7 @@ def _expected_workspace(cfg, fused):
     S = cfg.batch * nc * cfg.nheads * cfg.headdim * cfg.dstate
     tot = 2 * al(4 * cq) + al(S * es)
     tot += al(4 * cq) + al(4 * cfg.batch * cfg.nheads * nc) if fused else al(4 * S)
-    if not bench.scan_is_fused(c):
+    if not bench.scan_is_fused(c, states_fused=fused):
         tot += al(es * cfg.batch * nc * cfg.ngroups * Q * Q)
     return tot
 

@@ -437,6 +437,48 @@ def test_fp32_fused_state_pass(case):
         _run_and_check(cfg, with_z=True, Dhp=True, varlen=cfg.nseq > 0)
 
 
+# fp32 at chunk 128, head dim 64, dstate 64 / 128: the group scan builds CB
+# itself (no bmm_chunk launch) after the fused state pass (forced by the
+# f32_states override on these smaller shapes), and after the staged pass where
+# bmm_chunk would be a launch of its own (>= 128 (chunk, group) blocks).  Each
+# case against the oracle, and against the same layer with bmm_chunk and the
+# per-(chunk, head) scan kernel (the f32_scan override), which computes CB and
+# the products from the same bf16 triples
+_F32_GROUP_CASES = {
+    "packed_z_Dhp": (configs.SSDConfig("f32g", 1, 1200, 8, 2, 64, 128, 128, "f32", nseq=4,
+                                       min_seqlen=100, seed=51),
+                     dict(with_z=True, Dhp=True, varlen=True), "fused"),
+    "b2_init_ragged": (configs.SSDConfig("f32g", 2, 777, 12, 3, 64, 128, 256, "f32", init_state=True,
+                                         seed=52), dict(), "fused"),
+    "n64_z": (configs.SSDConfig("f32g", 4, 640, 16, 2, 64, 64, 128, "f32", seed=53),
+              dict(with_z=True), "fused"),
+    "n64_packed": (configs.SSDConfig("f32g", 1, 900, 6, 1, 64, 64, 128, "f32", nseq=3,
+                                     min_seqlen=64, seed=54), dict(varlen=True, Dhp=True), "fused"),
+    "staged_256_blocks": (configs.SSDConfig("f32g", 2, 4096, 8, 4, 64, 128, 128, "f32", seed=55),
+                          dict(with_z=True), None),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_F32_GROUP_CASES))
+def test_fp32_group_scan_builds_cb(case):
+    announce("fp32 group scan with CB built in", case)
+    cfg, kw, force = _F32_GROUP_CASES[case]
+    states = L.dispatch_override("f32_states", force or "staged")
+    with states:
+        _run_and_check(cfg, **kw)
+    d = configs.make_ssd_inputs(cfg, with_z=kw.get("with_z", False))
+    if kw.get("Dhp"):
+        d["D"] = np.random.default_rng(1).uniform(0.5, 1.5, (cfg.nheads, cfg.headdim)).astype(np.float32)
+    ckw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
+               return_varlen_states=kw.get("varlen", False))
+    with L.dispatch_override("f32_states", force or "staged"):
+        got = mamba_chunk_scan_combined_fwd(**_dev_inputs(d, "f32"), **ckw)
+        with L.dispatch_override("f32_scan", "per_head"):
+            ref = mamba_chunk_scan_combined_fwd(**_dev_inputs(d, "f32"), **ckw)
+    check(got[0], host(ref[0]), 2e-5, "out, group scan vs bmm_chunk + per-head scan")
+    assert torch.equal(got[1], ref[1])          # the state pass is the same kernel
+
+
 def test_c2_full_fp32():
     """The headline shape with fp32 inputs (the reference's published
     conditions), where the fp32 fused state pass runs, against the oracle."""
