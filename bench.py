@@ -262,7 +262,7 @@ def cpu_baseline(cfg, heads, min_seconds=10.0, max_reps=20):
             f"{heads} of {cfg.nheads} heads (whole groups) x {cfg.nheads / heads:g} (linear in heads)")
     return {
         "value": cfg.tokens / t, "unit": "tokens/s", "cores": threads, "kind": "port",
-        "cpu": cpu_model(), "ms_per_layer": t * 1e3,
+        "cpu": cpu_model(), "ms_per_layer": t * 1e3, "sampled": heads != cfg.nheads,
         "sample": (f"oracle NumPy float32 restatement of ssd_naive, {what}, full L={cfg.seqlen}; "
                    f"median of {len(times)} runs; host affinity "
                    f"{len(os.sched_getaffinity(0))} cpus, BLAS threads {threads}"),

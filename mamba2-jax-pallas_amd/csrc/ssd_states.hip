@@ -561,8 +561,8 @@ bool states_fused_supported(const m2_ssd_combined_args& a) {
 // Work split of the pass (see k_ssd_pair): the time of a workgroup's chunk
 // (128 positions) measured with every CU busy at the BASELINE shapes (1.36 us
 // for a head in 64-column halves, 2.6 for a pair of heads x 64 columns, 4.0
-// for a pair x 128 columns), times the rounds of 256 workgroups (one per CU)
-// and the chunks.  The M2_KNOB_STATES_SPLIT override (tests) forces a split
+// for a pair x 128 columns), times the rounds of workgroups over the CUs (one
+// per CU) and the chunks.  The M2_KNOB_STATES_SPLIT override (tests) forces a split
 // where the shape allows it.
 enum StatesSplit { SPLIT_HALVES, SPLIT_PAIR64, SPLIT_PAIR128 };
 
@@ -570,7 +570,8 @@ StatesSplit states_split(const m2_ssd_combined_args& a) {
     const bool pair = (a.nheads / a.ngroups) % 2 == 0 && a.chunk_size % 128 == 0;
     const int64_t nc = (a.seqlen + a.chunk_size - 1) / a.chunk_size;
     const int64_t bh = a.batch * a.nheads;
-    auto rounds = [](int64_t wg) { return (double)((wg + 255) / 256); };
+    const int64_t cus = cu_count();
+    auto rounds = [cus](int64_t wg) { return (double)((wg + cus - 1) / cus); };
     const double t_halves = rounds(bh * (a.dstate / 64)) * nc * 1.36;
     const double t_p64 = pair ? rounds(bh / 2 * (a.dstate / 64)) * nc * 2.6 : 1e30;
     const double t_p128 = pair && a.dstate % 128 == 0 ? rounds(bh / 2 * (a.dstate / 128)) * nc * 4.0 : 1e30;

@@ -259,6 +259,9 @@ F32_GROUP = [
     (1, 130, 4, 1, 64, True, True, None, 4),             # last chunk of 2 positions
     (1, 512, 16, 2, 128, True, False, None, 0),
     (1, 4096, 128, 8, 128, False, False, None, 0),       # nemotron-h-8b shape
+    (1, 50, 4, 4, 128, True, True, None, 1),             # one partial chunk, one head a group
+    (2, 100, 6, 3, 64, False, False, [[30, 70], [100]], 0),
+    (1, 256, 8, 2, 128, True, False, None, 9),           # slice larger than the group
 ]
 
 
