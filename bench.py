@@ -403,16 +403,27 @@ def bench_ops(lm_configs=("130m",)):
     return out
 
 
-def bench_fp32_same_shape(cfg, steps=100, warmup=300):
+def bench_fp32_same_shape(cfg, name="c2", steps=100, warmup=50):
     """The configuration's shape with fp32 inputs (the reference's published
-    numbers are fp32 runs at the nemotron-h-8b shape, README.md:35).  The
-    warmup (~60 ms of layers) brings the GPU to its steady clocks first."""
+    numbers are fp32 runs at the nemotron-h-8b shape, README.md:35): ms per
+    layer, tokens/s, the per-kernel table with its dominant kernel's roofline.
+    The event pass (300 layers) brings the GPU to its steady clocks first."""
     import dataclasses
     c32 = dataclasses.replace(cfg, dtype="f32")
     kw = _layer_inputs(c32)
+    nev = 300
+    finish = stage_table_enqueue(c32, kw, nev, stage_events(c32, nev))
     ms, _ = time_layer(kw, steps, warmup)
+    stages, dom, roof, _, tot_by = finish()
+    traffic = measured_traffic(f"{name}_f32")
+    roof["traffic"] = traffic.get(dom)
+    if traffic:
+        roof["traffic_source"] = traffic.get("source")
+    del kw
     return {"workload": f"{cfg.name} shape, fp32 inputs", "ms_per_layer": ms,
-            "tokens_per_s": c32.tokens / (ms * 1e-3)}
+            "tokens_per_s": c32.tokens / (ms * 1e-3),
+            "layer_hbm_frac": tot_by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "roofline": roof, "stages": stages}
 
 
 def bench_stage_operators(cfg, calls=10, replays=5):
@@ -696,7 +707,7 @@ def main(argv=None):
     # per layer after 5 warm-up steps on an idle GPU, 0.107 ms when busy).
     if args.config == "c2" and own_dtype and not args.no_configs:
         res_extra["configs"] = {c: bench_other_config(c) for c in ("c0", "c1", "c3")}
-        res_extra["fp32_same_shape"] = bench_fp32_same_shape(cfg)
+        res_extra["fp32_same_shape"] = bench_fp32_same_shape(cfg, args.config)
         res_extra["stage_operators"] = bench_stage_operators(cfg)
     if not args.no_decode:
         res_extra["decode"] = bench_decode()

@@ -87,12 +87,14 @@ def test_c0_fp32_stage_bytes_at_chunk_128():
     assert w["chunk_scan"][1] == b * nc * H * P * Q * (Q + 1) + 2 * b * L * H * N * P
 
 
-@pytest.mark.parametrize("name", ["c0", "c1", "c2", "c3"])
+@pytest.mark.parametrize("name", ["c0", "c1", "c2", "c3", "c2_f32"])
 def test_traffic_files_name_the_reported_stages(name):
     path = os.path.join(ROOT, "profiles", f"hbm_traffic_{name}.json")
     with open(path) as f:
         t = json.load(f)
-    cfg = configs.CONFIGS[name]
+    cfg = configs.CONFIGS[name.split("_")[0]]
+    if name.endswith("_f32"):
+        cfg = dataclasses.replace(cfg, dtype="f32")
     stages = set(bench.stage_work(cfg, with_init=cfg.init_state))
     # chunk_state_varlen (c3) runs after the five stage intervals
     measured = {k for k in t if k not in ("config", "unit", "source", "chunk_state_varlen")}
