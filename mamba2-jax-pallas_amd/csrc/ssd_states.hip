@@ -66,7 +66,11 @@ constexpr int CPR = 8;       // 16-byte chunks per 128-byte tile row
 // takes KB/2 positions (KS MFMA K steps of 32).
 template <int KB>
 struct StCfg {
-    static constexpr int DEPTH = KB == 64 ? 6 : 3;   // LDS stage slots: DEPTH - 1 in flight
+    // LDS stage slots, DEPTH - 1 stages in flight.  128-position stages: one
+    // in flight measures faster than two (c2: 42.7-43.6 against 44.6-45.2 us by
+    // events, A/B on one box): fewer loads queued per CU against the same
+    // per-CU intake, and three in flight (an early slot release) is slower again
+    static constexpr int DEPTH = KB == 64 ? 6 : 2;
     static constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
     static constexpr int AUXB = KB * 4 + 256;        // weights, 64 copies of the decay
     static constexpr int SLOT = XB + BB + AUXB;
