@@ -5,8 +5,8 @@
 //   y[m, :] = exp(dA[m]) * C[m, :] h_c^T                            (carried state)
 //           + sum_{k <= m} CB[m, k] exp(dA[m] - dA[k]) dt[k] x[k, :] (intra chunk)
 //           + D x[m, :],   then y *= silu(z[m, :]) when z is given
-// with CB the (seq_idx-masked) fp32 bmm_chunk output and h_c the fp32 state
-// entering chunk c.
+// with CB = C B^T (seq_idx-masked; the fp32 bmm_chunk output, or built here
+// in the combined forward: CBB below) and h_c the fp32 state entering chunk c.
 //
 // The per-(chunk, head) fp32 kernel (chunk_scan.hip) brings the group's C and
 // CB rows into the CU again for every head, ~100 of the ~165 KB it reads per
@@ -44,8 +44,9 @@
 // exp(dA[m]) exp(-dA[k]), which overflows once |dA| inside a chunk exceeds
 // ~88).
 //
-// Follows reference ops/ssd_naive.py:223-318 (math), kernels/chunk_scan_fwd.py
-// :294-322 (seq_idx rule for the carried-state term) and :545-570 (epilogue).
+// Follows reference ops/ssd_naive.py:189-318 (math), kernels/chunk_scan_fwd.py
+// :294-322 (seq_idx rule for the carried-state term) and :545-570 (epilogue),
+// kernels/bmm_chunk_fwd.py:353-372 (seq_idx mask of CB).
 #include <math.h>
 
 #include "m2_internal.h"
