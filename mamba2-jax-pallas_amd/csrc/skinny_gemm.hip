@@ -6,9 +6,9 @@
 // The weights are K-contiguous ([N, K], the layout torch.nn.functional.linear
 // takes), so each lane loads 8 consecutive k of one output column as one
 // 16-byte access, which is exactly a 16x16x32 bf16 MFMA's B-operand fragment.
-// One workgroup per 16 output columns; its 4, 8 or 16 wavefronts (enough for
-// ~2048 over the chip) split K and meet in LDS, so every weight byte is read
-// once; x (a few KB) comes from the cache.
+// One workgroup per 16 output columns (fewer where that leaves CUs idle); its
+// 4, 8 or 16 wavefronts (enough for ~2048 over the chip) split K and meet in
+// LDS, so every weight byte is read once; x (a few KB) comes from the cache.
 // MT = ceil(M / 16) row tiles share each weight fragment.
 //
 // k_skinny_gemm_norm is the same product for a decode step's first rows
@@ -34,6 +34,7 @@ struct GemmArgs {
     int64_t ldx, ldw, ldy;
     int M, N, K;
     int bias_bf16, y_bf16;
+    int cw;                 // output columns per workgroup (<= 16)
 };
 
 // MT 16-row tiles of x, NW wavefronts splitting K
@@ -41,8 +42,9 @@ template <int MT, int NW>
 __global__ void __launch_bounds__(NW * 64) k_skinny_gemm(GemmArgs a) {
     __shared__ f32x4 red[NW - 1][MT][64];
     const int lane = threadIdx.x & 63, w = wave_id();
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * a.cw;
     const int col = lane & 15, kq = (lane >> 4) * 8;   // fragment column / k offset
+    const bool colok = col < a.cw;                     // lanes past cw load and store nothing
     const int nb = min(n0 + col, a.N - 1);             // clamped: tail columns are masked on store
     const bf16* wr = a.w + (int64_t)nb * a.ldw;
     // this wavefront's k range, in steps of 32
@@ -61,7 +63,7 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm(GemmArgs a) {
         for (int u = 0; u < UNROLL; ++u) {
             const int k = (s + u) * 32 + kq;
             const bool ok = s + u < s1 && k < a.K;
-            bf[u] = ok ? *reinterpret_cast<const bf16x8*>(wr + k) : zf;
+            bf[u] = ok && colok ? *reinterpret_cast<const bf16x8*>(wr + k) : zf;
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const int m = 16 * t + col;
@@ -103,7 +105,7 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm(GemmArgs a) {
         }
     // D layout: lane holds column n0 + (lane & 15), rows 16 t + 4 (lane >> 4) + i
     const int n = n0 + col;
-    if (n >= a.N) return;
+    if (!colok || n >= a.N) return;
     float bv = 0.f;
     if (a.bias)
         bv = a.bias_bf16 ? (float)reinterpret_cast<const bf16*>(a.bias)[n]
@@ -136,6 +138,7 @@ struct NormGemmArgs {
     int64_t ldw, ldy, r_rs;
     int M, N, K;
     int bias_bf16, y_bf16;
+    int cw;                 // output columns per workgroup (<= 16)
 };
 
 template <int NW, bool CONV>
@@ -144,8 +147,9 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm_norm(NormGemmArgs a) {
     __shared__ f32x4 red[NW - 1][64];
     __shared__ float part[NW][NORM_MAXM * NORM_MAXG];    // per-wavefront sums of squares
     const int lane = threadIdx.x & 63, w = wave_id();
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * a.cw;
     const int col = lane & 15, kq = (lane >> 4) * 8;
+    const bool colok = col < a.cw;                     // lanes past cw load and store nothing
     const int nb = min(n0 + col, a.N - 1);
     const bf16* wr = a.w + (int64_t)nb * a.ldw;
     const int K = a.K, M = a.M;
@@ -158,7 +162,7 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm_norm(NormGemmArgs a) {
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) {
             const int k = (s + u) * 32 + kq;
-            bf[u] = s + u < s1 && k < K ? *reinterpret_cast<const bf16x8*>(wr + k) : zf;
+            bf[u] = s + u < s1 && k < K && colok ? *reinterpret_cast<const bf16x8*>(wr + k) : zf;
         }
     };
     // the first weight batch is in flight while the rows are normalised
@@ -239,7 +243,7 @@ __global__ void __launch_bounds__(NW * 64) k_skinny_gemm_norm(NormGemmArgs a) {
         for (int i = 0; i < 4; ++i) acc[i] += o[i];
     }
     const int n = n0 + col;
-    if (n >= a.N) return;
+    if (!colok || n >= a.N) return;
     float bv = 0.f;
     if (a.bias)
         bv = a.bias_bf16 ? (float)reinterpret_cast<const bf16*>(a.bias)[n]
@@ -292,6 +296,18 @@ void launch_mt(const GemmArgs& k, int64_t ngroups, hipStream_t s) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Output columns per workgroup: 16 (a full MFMA tile) when that gives at
+// least one workgroup per CU, else as few as spread the columns over every CU
+// (at least 4): the weight stream then comes in through all the CUs instead
+// of a few, e.g. the 2.7b out-projection (N 2560: 160 workgroups of 16
+// columns) as 256 workgroups of 10.  MFMA lanes past cw carry zeros.
+int cols_per_wg(int64_t N) {
+    const int64_t cus = m2::cu_count();
+    if ((N + 15) / 16 >= cus) return 16;
+    const int64_t cw = (N + cus - 1) / cus;
+    return (int)(cw < 4 ? 4 : cw > 16 ? 16 : cw);
+}
+
 }  // namespace
 
 namespace m2 {
@@ -321,7 +337,8 @@ int launch_skinny_gemm(const m2_skinny_gemm_args& a, hipStream_t s) {
     k.ldx = a.ldx; k.ldw = a.ldw; k.ldy = a.ldy;
     k.M = (int)a.M; k.N = (int)a.N; k.K = (int)a.K;
     k.bias_bf16 = a.bias_dtype == M2_BF16; k.y_bf16 = a.y_dtype == M2_BF16;
-    const int64_t ng = (a.N + 15) / 16;
+    k.cw = cols_per_wg(a.N);
+    const int64_t ng = (a.N + k.cw - 1) / k.cw;
     if (a.M <= 16) launch_mt<1>(k, ng, s);
     else if (a.M <= 32) launch_mt<2>(k, ng, s);
     else launch_mt<4>(k, ng, s);
@@ -366,7 +383,8 @@ int launch_skinny_gemm_norm(const m2_skinny_gemm_norm_args& a, hipStream_t s) {
     M2_REQUIRE(a.y_dtype == M2_BF16 || a.y_dtype == M2_F32, M2_ERR_UNSUPPORTED, "%s: y dtype %d",
                who, a.y_dtype);
     k.bias_bf16 = a.bias_dtype == M2_BF16; k.y_bf16 = a.y_dtype == M2_BF16;
-    const int64_t ng = (a.N + 15) / 16;
+    k.cw = cols_per_wg(a.N);
+    const int64_t ng = (a.N + k.cw - 1) / k.cw;
     const int nsteps = (int)((a.K + 31) / 32);
     k.conv_lo = -1;
     if (a.with_conv) {
