@@ -128,7 +128,8 @@ def chunk_cumsum(dt, A, chunk_size, dt_bias=None, dt_softplus=False,
 
 
 # ---------------------------------------------------------------------------
-# seq_idx helpers (kernels/*_fwd.py seq_idx rules)
+# seq_idx helpers (the seq_idx rules of reference kernels/chunk_state_fwd.py:239-269,
+# kernels/state_passing_fwd.py:208-225, kernels/chunk_scan_fwd.py:294-322)
 # ---------------------------------------------------------------------------
 
 def _pad_seq(seq_idx, nc, chunk_size):
