@@ -96,7 +96,13 @@ struct Cfg {
     static constexpr int ring_bytes(int r) { return r * SLOT > SLOT + BT ? r * SLOT : SLOT + BT; }
     static constexpr int STW = 16 * 64 * 4, STG = NWAVES * STW;   // staged output tiles
     static constexpr bool STAGE = ring_bytes(2) + FIXED + STG <= LDS_BYTES;
-    static constexpr int EXTRA = FIXED + (STAGE ? STG : 0);
+    // without room for whole tiles (N 256) each compute wavefront stages its
+    // own tile, 32 columns (128-byte row pieces) at a time, and stores it
+    // itself: whole 128-byte lines per store instead of 64-byte pieces (the
+    // scan at c3: 323 against 332 us)
+    static constexpr int WSTW = 16 * 32 * 4, WSTG = NWAVES * WSTW;
+    static constexpr bool WST = !STAGE && ring_bytes(2) + FIXED + WSTG <= LDS_BYTES;
+    static constexpr int EXTRA = FIXED + (STAGE ? STG : WST ? WSTG : 0);
     static constexpr int R = ring_bytes(4) + EXTRA <= LDS_BYTES ? 4
                            : ring_bytes(3) + EXTRA <= LDS_BYTES ? 3 : 2;
     static constexpr int RING = ring_bytes(R);
@@ -416,7 +422,9 @@ M2_DEV void compute_path(const ScanFusedArgs& a, char* ring, f32x4 (*xchg)[4][64
             }
         }
         // 5. epilogue: silu(z) gate in z's dtype; the tile goes to the staging
-        // area (stored by the data wavefronts) or straight to HBM
+        // area (stored by the data wavefronts), through the wavefront's own
+        // staging rows to HBM, or straight to HBM
+        f32x4 vo[4];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
             float v[4] = {acc[0][pt][0], acc[0][pt][1], acc[0][pt][2], acc[0][pt][3]};
@@ -424,14 +432,39 @@ M2_DEV void compute_path(const ScanFusedArgs& a, char* ring, f32x4 (*xchg)[4][64
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] *= rbf(silu_f((float)zr[pt][i]));
             }
+            vo[pt] = f32x4{v[0], v[1], v[2], v[3]};
             if (S::STAGE) {
                 // row ln, 16-byte chunk 4 pt + kg, XOR-swizzled by the row
                 const int c = (4 * pt + kg) ^ ln;
                 *reinterpret_cast<float4*>(stg + w * S::STW + ln * 256 + 16 * c) =
                     make_float4(v[0], v[1], v[2], v[3]);
-            } else if (mrow < valid) {
-                const f32x4 o = {v[0], v[1], v[2], v[3]};
-                store_out<NT>(o, a.out + ((tok0 + mrow) * H + h) * P + 16 * pt + 4 * kg);
+            } else if (!S::WST && mrow < valid) {
+                store_out<NT>(vo[pt], a.out + ((tok0 + mrow) * H + h) * P + 16 * pt + 4 * kg);
+            }
+        }
+        if constexpr (S::WST) {
+            // half hf (columns 32 hf ..): row ln, 16-byte chunk 4 pl + kg of the
+            // 128-byte row, XOR-swizzled by the row; read back as whole rows
+            char* sw = stg + w * S::WSTW;
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+                for (int pl = 0; pl < 2; ++pl)
+                    *reinterpret_cast<f32x4*>(sw + ln * 128 + 16 * ((4 * pl + kg) ^ (ln & 7))) = vo[2 * hf + pl];
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                f32x4 o[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int r = 8 * q + (lane >> 3);
+                    o[q] = *reinterpret_cast<const f32x4*>(sw + r * 128 + 16 * ((lane & 7) ^ (r & 7)));
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int m = 16 * TM + 8 * q + (lane >> 3);
+                    if (m < valid)
+                        store_out<NT>(o[q], a.out + ((tok0 + m) * H + h) * P + 32 * hf + 4 * (lane & 7));
+                }
             }
         }
     }
@@ -445,7 +478,7 @@ __global__ void __launch_bounds__(THREADS) k_scan_q128(ScanFusedArgs a) {
     __shared__ __align__(16) char ring[S::RING];
     __shared__ __align__(16) f32x4 xchg[4][4][64];
     __shared__ __align__(16) float ftab[NWAVES * 64];
-    __shared__ __align__(16) char stg[S::STAGE ? S::STG : 16];
+    __shared__ __align__(16) char stg[S::STAGE ? S::STG : S::WST ? S::WSTG : 16];
     __shared__ int seqs[Q];
 
     const int L = a.L, H = a.H, G = a.G, nc = a.nc, hpg = a.hpg;

@@ -346,8 +346,11 @@ template <int RB> M2_DEV int rswz(int R) { return RB == 128 ? ((R >> 1) & 3) << 
 // Compute wavefront w owns head (w >> 2) of the pair, head-dim rows
 // 16 (w & 3) .. +15 and all NB columns, and takes every position of a stage
 // (no position halves, so no exchange): each x element is weighted by one
-// wavefront, and the bf16 state entering a chunk is stored straight from the
-// accumulators.
+// wavefront.  The bf16 state entering a chunk leaves through the wavefront's
+// own staging rows in LDS, CW columns at a time, so that every store writes
+// whole CW-column row pieces (128 bytes at NB 128): stored straight from the
+// accumulators, 32-byte pieces of 16 rows per store, the states took 70 of
+// the 257 us of the pass at c3 (1.37x).
 //
 // A slot holds the stage's x rows of both heads [KB x 2 P] (the heads are
 // adjacent in memory: 256 contiguous bytes per row), the B rows [KB x NB],
@@ -364,12 +367,17 @@ struct PairCfg {
     static constexpr int XL = XB / 1024 / NLOAD, BL = BB / 1024 / NLOAD;
     static constexpr int KS = KB / 32;                            // K steps per stage
     static constexpr int NT = NB / 16;                            // column tiles per wavefront
+    // state staging: CW columns per pass, rows of CW + 8 bf16 (16 bytes of pad),
+    // LPR lanes of 16 bytes per row, RPI rows per store
+    static constexpr int CW = NB == 128 ? 64 : 32, SROW = CW + 8;
+    static constexpr int LPR = CW / 8, RPI = 64 / LPR;
     // loads of one load wavefront that may still be in flight when stage s is
     // needed: DEPTH - 2 later stages (+ weights / decay for load wavefronts 0, 1)
     static constexpr int WAIT01 = (DEPTH - 2) * (XL + BL + 1), WAIT23 = (DEPTH - 2) * (XL + BL);
     static_assert(XB % (1024 * NLOAD) == 0 && BB % (1024 * NLOAD) == 0, "even load split");
     static_assert(DEPTH >= 3 && WAIT01 <= 63, "ring depth / vmcnt range");
     static_assert(HP * KB / 4 <= 64, "weights: one 16-byte load per lane");
+    static_assert(DEPTH * SLOT + NWAVES * 16 * SROW * 2 <= 160 * 1024, "LDS budget");
 };
 
 template <int NB, int KB>
@@ -378,6 +386,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
     constexpr int HP = C::HP;
     constexpr int DEPTH = C::DEPTH, XB = C::XB, BB = C::BB, SLOT = C::SLOT, NT = C::NT;
     __shared__ __align__(16) char ring[DEPTH * SLOT];
+    __shared__ __align__(16) bf16 stg[NWAVES][16][C::SROW];   // per compute wavefront
 
     // work = head pair x nblk + column block: the column blocks of a pair and
     // the pairs of a group, which read the same x and B rows, share an XCD
@@ -459,14 +468,31 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
             acc[j] = zero4();
         }
     }
-    // this lane's part of the bf16 state [p][n] (8 bytes per tile) into passed[c]
-    auto store_state = [&](int c) {
-        bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + prow) * N + ncol;
+    // the bf16 state entering chunk c (pk[j]: this lane's 4 columns of tile j)
+    // into passed[c], rows 16 pw .. 16 pw + 15 of head h: per pass the lanes
+    // write their pieces of CW columns into the staging rows and read them
+    // back as 16-byte pieces of whole row segments.  The staging rows are this
+    // wavefront's alone; its LDS operations complete in order, and the waits
+    // keep the compiler from moving the accesses across each other.
+    typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
+    auto store_state = [&](int c, const u2* pk) {
+        constexpr int CW = C::CW, SROW = C::SROW, LPR = C::LPR, RPI = C::RPI;
+        bf16* pp = a.passed + ((((int64_t)bi * nc + c) * H + h) * P + 16 * pw) * N + NB * nb;
+        bf16* sw = &stg[w][0][0];
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-            typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u2;
-            const u2 v = {pk_bf16(acc[j][0], acc[j][1]), pk_bf16(acc[j][2], acc[j][3])};
-            *reinterpret_cast<u2*>(pp + 16 * j) = v;
+        for (int ps = 0; ps < NB / CW; ++ps) {
+#pragma unroll
+            for (int jj = 0; jj < CW / 16; ++jj)
+                *reinterpret_cast<u2*>(sw + ln * SROW + 16 * jj + 4 * kg) = pk[(CW / 16) * ps + jj];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            u32x4 v[16 / RPI];
+#pragma unroll
+            for (int q = 0; q < 16 / RPI; ++q)
+                v[q] = *reinterpret_cast<const u32x4*>(sw + (RPI * q + lane / LPR) * SROW + 8 * (lane % LPR));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int q = 0; q < 16 / RPI; ++q)
+                *reinterpret_cast<u32x4*>(pp + (int64_t)(RPI * q + lane / LPR) * N + CW * ps + 8 * (lane % LPR)) = v[q];
         }
     };
 
@@ -511,10 +537,13 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
                 bb[ks][j] = ds_read_tr(slot + bo1[j] + ks * 32 * C::BROW);
             }
         }
+        u2 pk[NT];                                   // h_c in bf16 (chunk starts)
         if (kb == 0) {
-            // acc = h_c, the state entering chunk c; then h <- scl[c] h
+            // acc = h_c, the state entering chunk c (stored after the stage's
+            // MFMAs are issued); then h <- scl[c] h
             const float sc = aux[HP * KB + hh];
-            store_state(c);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) pk[j] = u2{pk_bf16(acc[j][0], acc[j][1]), pk_bf16(acc[j][2], acc[j][3])};
 #pragma unroll
             for (int j = 0; j < NT; ++j)
 #pragma unroll
@@ -541,6 +570,7 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bf, xl, acc[j], 0, 0, 0);
             }
         }
+        if (kb == 0) store_state(c, pk);
     }
 
     if (a.fin) {
@@ -564,7 +594,7 @@ bool states_fused_supported(const m2_ssd_combined_args& a) {
 
 // Work split of the pass (see k_ssd_pair): the time of a workgroup's chunk
 // (128 positions) measured with every CU busy at the BASELINE shapes (1.36 us
-// for a head in 64-column halves, 2.6 for a pair of heads x 64 columns, 4.0
+// for a head in 64-column halves, 2.2 for a pair of heads x 64 columns, 3.0
 // for a pair x 128 columns), times the rounds of workgroups over the CUs (one
 // per CU) and the chunks.  The M2_KNOB_STATES_SPLIT override (tests) forces a split
 // where the shape allows it.
@@ -577,8 +607,8 @@ StatesSplit states_split(const m2_ssd_combined_args& a) {
     const int64_t cus = cu_count();
     auto rounds = [cus](int64_t wg) { return (double)((wg + cus - 1) / cus); };
     const double t_halves = rounds(bh * (a.dstate / 64)) * nc * 1.36;
-    const double t_p64 = pair ? rounds(bh / 2 * (a.dstate / 64)) * nc * 2.6 : 1e30;
-    const double t_p128 = pair && a.dstate % 128 == 0 ? rounds(bh / 2 * (a.dstate / 128)) * nc * 4.0 : 1e30;
+    const double t_p64 = pair ? rounds(bh / 2 * (a.dstate / 64)) * nc * 2.2 : 1e30;
+    const double t_p128 = pair && a.dstate % 128 == 0 ? rounds(bh / 2 * (a.dstate / 128)) * nc * 3.0 : 1e30;
     switch (dispatch_override(M2_KNOB_STATES_SPLIT)) {
         case 1: return SPLIT_HALVES;
         case 2: if (t_p64 < 1e30) return SPLIT_PAIR64; break;
