@@ -380,7 +380,7 @@ struct PairCfg {
     static_assert(DEPTH * SLOT + NWAVES * 16 * SROW * 2 <= 160 * 1024, "LDS budget");
 };
 
-template <int NB, int KB>
+template <int NB, int KB, bool NTS>
 __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
     typedef PairCfg<NB, KB> C;
     constexpr int HP = C::HP;
@@ -491,8 +491,11 @@ __global__ void __launch_bounds__(THREADS) k_ssd_pair(StatesArgs a) {
                 v[q] = *reinterpret_cast<const u32x4*>(sw + (RPI * q + lane / LPR) * SROW + 8 * (lane % LPR));
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-            for (int q = 0; q < 16 / RPI; ++q)
-                *reinterpret_cast<u32x4*>(pp + (int64_t)(RPI * q + lane / LPR) * N + CW * ps + 8 * (lane % LPR)) = v[q];
+            for (int q = 0; q < 16 / RPI; ++q) {
+                u32x4* dst = reinterpret_cast<u32x4*>(pp + (int64_t)(RPI * q + lane / LPR) * N + CW * ps + 8 * (lane % LPR));
+                if constexpr (NTS) __builtin_nontemporal_store(v[q], dst);
+                else *dst = v[q];
+            }
         }
     };
 
@@ -636,10 +639,25 @@ int launch_states_fused(const m2_ssd_combined_args& a, const float* wts, const f
     const int64_t nwork = a.batch * a.nheads / (sp == SPLIT_HALVES ? 1 : 2) * sa.nblk;
     M2_REQUIRE(nwork < (1ll << 31), M2_ERR_UNSUPPORTED, "ssd_states: too many workgroups");
     sa.nwork = (int)nwork;
-    if (sp == SPLIT_PAIR128) k_ssd_pair<128, 64><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
-    else if (sp == SPLIT_PAIR64) k_ssd_pair<64, 128><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
-    else if (sa.Q % 128 == 0) k_ssd_states<128><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
-    else k_ssd_states<64><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    // The head-pair kernels store states larger than the 256 MB Infinity Cache
+    // (c3: 537 MB) non-temporally: the scan that reads them then starts
+    // without the pass's dirty lines in the cache, and its time drops by more
+    // than the pass's grows (A/B on one box at c3: pass 194 -> 200 us, scan
+    // 326 -> 302 us, layer 0.570 -> 0.554 ms).  Smaller ones (c1: 84 MB) stay
+    // ordinary, as the scan then reads them from the cache (c1 0.110 against
+    // 0.113 ms with non-temporal ones).
+    const bool nts = (double)a.batch * sa.nc * a.nheads * a.headdim * a.dstate * 2 > 256.0 * (1 << 20);
+    if (sp == SPLIT_PAIR128) {
+        if (nts) k_ssd_pair<128, 64, true><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+        else k_ssd_pair<128, 64, false><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    } else if (sp == SPLIT_PAIR64) {
+        if (nts) k_ssd_pair<64, 128, true><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+        else k_ssd_pair<64, 128, false><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    } else if (sa.Q % 128 == 0) {
+        k_ssd_states<128><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    } else {
+        k_ssd_states<64><<<(unsigned)sa.nwork, THREADS, 0, s>>>(sa);
+    }
     return check_launch("ssd_states");
 }
 
