@@ -344,6 +344,27 @@ def test_state_pass_pair_splits_varlen(split):
         _run_and_check(cfg, varlen=True)
 
 
+def test_state_pass_pair_splits_full_c3_nontemporal():
+    """At the full c3 size the states entering each chunk (537 MB) exceed the
+    256 MB Infinity Cache, so both head-pair kernels store them non-temporally
+    through their LDS staging rows.  The two splits sum the same products in
+    the same order, so their outputs, final and varlen states are bit-identical,
+    and the launcher's own choice here (pair x 128 columns) gives the same."""
+    announce("state-pass pair splits, full c3, non-temporal state stores")
+    cfg = configs.CONFIGS["c3"]
+    assert cfg.seqlen * cfg.nheads * cfg.headdim * cfg.dstate * 2 > 256 * 2**20
+    d = configs.make_ssd_inputs(cfg)
+    t = _dev_inputs(d, cfg.dtype)
+    kw = dict(chunk_size=cfg.chunk_size, dt_softplus=True, return_final_states=True,
+              return_varlen_states=True)
+    auto = mamba_chunk_scan_combined_fwd(**t, **kw)
+    for split in ("pair64", "pair128"):
+        with L.dispatch_override("states_split", split):
+            got = mamba_chunk_scan_combined_fwd(**t, **kw)
+        for name, a, b in zip(("out", "final_states", "varlen_states"), got, auto):
+            assert torch.equal(a, b), f"{split} {name}"
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_graph_replays_match_eager(dtype):
     """The combined forward captured in a HIP graph (fp32: the staged kernels,
