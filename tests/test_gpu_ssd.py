@@ -125,6 +125,22 @@ def test_gate_D_per_headdim_and_ragged_length(dtype):
     _run_and_check(cfg, with_z=True, Dhp=True)
 
 
+@pytest.mark.parametrize("case", ["b2_init_ragged", "packed"])
+def test_dstate256_chunk128_gate(case):
+    """bf16, dstate 256, chunk 128, head dim 64: the scan kernel whose compute
+    wavefronts stage and store their own output tiles, here with the z gate
+    applied before the staging, D per head dim, a ragged last chunk (rows past
+    it staged but not stored), an initial state / packed sequences."""
+    announce("dstate 256 chunk 128 with z", case)
+    if case == "b2_init_ragged":
+        cfg = configs.SSDConfig("n256z", 2, 3 * 128 + 45, 8, 2, 64, 256, 128, "bf16",
+                                init_state=True, seed=61)
+    else:
+        cfg = configs.SSDConfig("n256z", 1, 1000, 8, 4, 64, 256, 128, "bf16", nseq=4,
+                                min_seqlen=100, seed=62)
+    _run_and_check(cfg, with_z=True, Dhp=True, varlen=cfg.nseq > 0)
+
+
 def test_headdim_128_dstate_256_chunk_64():
     announce("P=128 N=256 Q=64")
     cfg = configs.SSDConfig("wide", 1, 256, 8, 2, 128, 256, 64, "bf16", seed=22)
