@@ -38,13 +38,10 @@ template <> struct Vec<4> {
         float4 t = *reinterpret_cast<const float4*>(p);
         v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
     }
-    // fp32 states leave non-temporally: at the mamba2-130m shape (fp32, 12.6
-    // MB of passed states read back by the scan) state_passing + bmm_chunk took
-    // 9.5 against 11.3 us and the layer 34.6 against 36.1 us (A/B on one box),
-    // as no dirty state lines remain in L2 for the end of the kernel; the
-    // state_passing operator at the nemotron-h-8b shape (134 MB) is unchanged
-    // (31.7 against 31.8 us)
     M2_DEV void store(float* p) const {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    M2_DEV void store_nt(float* p) const {
         __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4*>(p));
     }
     M2_DEV void store(bf16* p) const {
@@ -73,8 +70,9 @@ struct PassArgs {
     int L, Q, blocks_per_row;
 };
 
-// the walk of block `block` (blockDim.x threads, `scl` nc floats of LDS)
-template <typename TO, int VW, bool ONE_BATCH>
+// the walk of block `block` (blockDim.x threads, `scl` nc floats of LDS);
+// NT (fp32, VW 4, one-batch walk): non-temporal state stores
+template <typename TO, int VW, bool ONE_BATCH, bool NT = false>
 M2_DEV void pass_walk(const PassArgs& p, int block, float* scl) {
     const float* __restrict__ states = p.states;
     const float* __restrict__ dAc = p.dAc;
@@ -136,7 +134,8 @@ M2_DEV void pass_walk(const PassArgs& p, int block, float* scl) {
 #pragma unroll
         for (int c = 0; c < DEPTH; ++c) {
             if (c < nc) {
-                run.store(dst + (int64_t)c * cstride);
+                if constexpr (NT) run.store_nt(dst + (int64_t)c * cstride);
+                else run.store(dst + (int64_t)c * cstride);
                 const float scale = scl[c];
 #pragma unroll
                 for (int j = 0; j < VW; ++j) run.v[j] = fmaf(scale, run.v[j], buf[c].v[j]);
@@ -171,10 +170,10 @@ __global__ void __launch_bounds__(THREADS) k_state_passing(PassArgs p) {
 // launch of 256-thread blocks: blocks below npass walk states, the others
 // compute CB tiles (one launch less on the path, and the CB tiles fill the
 // CUs the walk leaves idle)
-template <int VW, bool ONE_BATCH, int CT>
+template <int VW, bool ONE_BATCH, int CT, bool NT>
 __global__ void __launch_bounds__(THREADS) k_pass_bmm(PassArgs p, m2::BmmTileArgs m, int npass) {
     extern __shared__ float scl[];
-    if ((int)blockIdx.x < npass) pass_walk<float, VW, ONE_BATCH>(p, blockIdx.x, scl);
+    if ((int)blockIdx.x < npass) pass_walk<float, VW, ONE_BATCH, NT>(p, blockIdx.x, scl);
     else m2::bmm_tile<float, float, CT>(m, xcd_remap(blockIdx.x - npass, m.nblocks));
 }
 
@@ -247,13 +246,25 @@ int launch_state_passing_bmm(const m2_state_passing_args& a, const m2_bmm_chunk_
     M2_REQUIRE(mt.nblocks > 0 && npass + mt.nblocks < (1ll << 31), M2_ERR_UNSUPPORTED,
                "state_passing + bmm_chunk: too many blocks");
     const bool one = a.nchunks <= DEPTH;
+    // Small passed states (at most 16 MiB, the fp32 mamba2-130m layer: 12 MiB)
+    // leave non-temporally: there state_passing + bmm_chunk took 9.5 against
+    // 11.3 us and the layer 34.6 against 35.5 us (A/B on one box), no dirty
+    // state lines remaining in L2 for the end of the kernel.  At batch 2 / 4
+    // (24 / 48 MiB) the scan, which reads them next, then lost more than the
+    // walk gained (layer 54.4 against 50.9 us, 89.4 against 84.7).
+    const bool nt = vw == 4 && one &&
+                    (double)a.batch * a.nchunks * a.nheads * a.dim * 4 <= 16.0 * (1 << 20);
     void (*kern)(PassArgs, BmmTileArgs, int) = nullptr;
 #define M2_PB_CASE(VWV, ONEV, CTV) \
-    if (vw == VWV && one == ONEV && ct == CTV) kern = k_pass_bmm<VWV, ONEV, CTV>;
+    if (vw == VWV && one == ONEV && ct == CTV) kern = k_pass_bmm<VWV, ONEV, CTV, false>;
+#define M2_PB_NT(CTV) \
+    if (nt && ct == CTV) kern = k_pass_bmm<4, true, CTV, true>;
 #define M2_PB_CT(VWV, ONEV) M2_PB_CASE(VWV, ONEV, 1) M2_PB_CASE(VWV, ONEV, 2) \
                             M2_PB_CASE(VWV, ONEV, 3) M2_PB_CASE(VWV, ONEV, 4)
     M2_PB_CT(4, true) M2_PB_CT(4, false) M2_PB_CT(1, true) M2_PB_CT(1, false)
+    M2_PB_NT(1) M2_PB_NT(2) M2_PB_NT(3) M2_PB_NT(4)
 #undef M2_PB_CT
+#undef M2_PB_NT
 #undef M2_PB_CASE
     M2_REQUIRE(kern, M2_ERR_UNSUPPORTED, "state_passing + bmm_chunk: chunk_size %lld",
                (long long)m.chunk_size);
