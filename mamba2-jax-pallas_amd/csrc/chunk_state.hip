@@ -256,7 +256,7 @@ M2_DEV bf16x8 tr8(const char* p0, const char* p1) {
     return __builtin_shufflevector(ds_read_tr(p0), ds_read_tr(p1), 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <int HP, int QT, bool CS>
+template <int HP, int QT, bool CS, bool NT>
 __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
     constexpr int P = 64, Q = 32 * QT;
     constexpr int XROW = HP * P * 2, BROW = F32_NB * 2;     // plane row bytes
@@ -431,9 +431,13 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
         const int hh = pr / P, pp = pr % P;
         float* op = a.out + ((((int64_t)bi * nc + c) * H + h0 + hh) * P + pp) * N + nb * F32_NB;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<float4*>(op + 16 * (nt0 + j) + 4 * kg) =
-                make_float4(acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]);
+        for (int j = 0; j < 4; ++j) {
+            float* const dst = op + 16 * (nt0 + j) + 4 * kg;
+            if constexpr (NT)
+                __builtin_nontemporal_store(acc[j][i], reinterpret_cast<f32x4*>(dst));
+            else
+                *reinterpret_cast<float4*>(dst) = make_float4(acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]);
+        }
     }
 }
 
@@ -449,11 +453,22 @@ int launch_chunk_state_f32(const StateArgs& sa, int64_t bhc, hipStream_t s, bool
     const size_t shm = cs_f32_lds(sa.Q, HP);
     if (shm > 160 * 1024)
         return m2::set_error(M2_ERR_UNSUPPORTED, "chunk_state (fp32 planes): %zu B of LDS", shm);
+    // The combined forward's chunk states (cumsum folded in) leave
+    // non-temporally when they are small (at most 16 MiB; the fp32 mamba2-130m
+    // layer: 12 MiB): this kernel 10.6 against 11.6 us, the layer 33.8 against
+    // 34.4 us (A/B on one box), no dirty lines remaining in L2 for the end of
+    // the kernel; at 24 / 48 MiB the state passing that reads them next lost
+    // more than this kernel gained.
+    const bool nt = cs && (double)bhc * sa.P * sa.N * 4 <= 16.0 * (1 << 20);
     void (*kern)(StateArgs) = nullptr;
-#define M2_CSF_CASE(HPV, QV, CSV) \
-    if (HP == HPV && sa.Q == QV && cs == CSV) kern = k_chunk_state_f32<HPV, QV / 32, CSV>;
-    M2_CSF_CASE(2, 64, false) M2_CSF_CASE(2, 128, false) M2_CSF_CASE(1, 64, false) M2_CSF_CASE(1, 128, false)
-    M2_CSF_CASE(2, 64, true) M2_CSF_CASE(2, 128, true) M2_CSF_CASE(1, 64, true) M2_CSF_CASE(1, 128, true)
+#define M2_CSF_CASE(HPV, QV, CSV, NTV) \
+    if (HP == HPV && sa.Q == QV && cs == CSV && nt == NTV) kern = k_chunk_state_f32<HPV, QV / 32, CSV, NTV>;
+    M2_CSF_CASE(2, 64, false, false) M2_CSF_CASE(2, 128, false, false)
+    M2_CSF_CASE(1, 64, false, false) M2_CSF_CASE(1, 128, false, false)
+    M2_CSF_CASE(2, 64, true, false) M2_CSF_CASE(2, 128, true, false)
+    M2_CSF_CASE(1, 64, true, false) M2_CSF_CASE(1, 128, true, false)
+    M2_CSF_CASE(2, 64, true, true) M2_CSF_CASE(2, 128, true, true)
+    M2_CSF_CASE(1, 64, true, true) M2_CSF_CASE(1, 128, true, true)
 #undef M2_CSF_CASE
     if (shm > 65536 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
