@@ -193,6 +193,18 @@ def measured_traffic(config):
         return json.load(f)
 
 
+def attach_traffic(roof, traffic, dom):
+    """roofline.traffic for the dominant stage `dom`, with the file it comes
+    from and, where the file explains measured bytes above the algorithmic
+    ones for that stage, the explanation."""
+    roof["traffic"] = traffic.get(dom)
+    if traffic:
+        roof["traffic_source"] = traffic.get("source")
+        note = traffic.get("above_algorithmic", {}).get(dom)
+        if note:
+            roof["traffic_note"] = note
+
+
 class HipEvents:
     """Raw HIP events for the per-stage timing, created with
     hipEventDisableSystemFence: recording one does not write back and
@@ -415,10 +427,7 @@ def bench_fp32_same_shape(cfg, name="c2", steps=100, warmup=50):
     finish = stage_table_enqueue(c32, kw, nev, stage_events(c32, nev))
     ms, _ = time_layer(kw, steps, warmup)
     stages, dom, roof, _, tot_by = finish()
-    traffic = measured_traffic(f"{name}_f32")
-    roof["traffic"] = traffic.get(dom)
-    if traffic:
-        roof["traffic_source"] = traffic.get("source")
+    attach_traffic(roof, measured_traffic(f"{name}_f32"), dom)
     del kw
     return {"workload": f"{cfg.name} shape, fp32 inputs", "ms_per_layer": ms,
             "tokens_per_s": c32.tokens / (ms * 1e-3),
@@ -621,10 +630,7 @@ def bench_other_config(name, steps=50, warmup=20, cpu=True):
     finish = stage_table_enqueue(cfg, kw, nev, stage_events(cfg, nev))
     ms, _ = time_layer(kw, steps, warmup)
     stages, dom, roof, _, tot_by = finish()
-    traffic = measured_traffic(name)
-    roof["traffic"] = traffic.get(dom)
-    if traffic:
-        roof["traffic_source"] = traffic.get("source")
+    attach_traffic(roof, measured_traffic(name), dom)
     out = {"workload": f"{cfg.name} SSD layer forward ({name})", "dtype": cfg.dtype,
            "batch": cfg.batch, "seq_len": cfg.seqlen, "nheads": cfg.nheads,
            "ngroups": cfg.ngroups, "headdim": cfg.headdim, "dstate": cfg.dstate,
@@ -728,10 +734,7 @@ def main(argv=None):
     ms, wall_ms = time_layer(kw, K, args.warmup)
     stages, dom, roof, stages_ms_total, tot_by = finish()
     # measured traffic is kept for each config at its own dtype
-    traffic = measured_traffic(args.config) if own_dtype else {}
-    roof["traffic"] = traffic.get(dom)
-    if traffic:
-        roof["traffic_source"] = traffic.get("source")
+    attach_traffic(roof, measured_traffic(args.config) if own_dtype else {}, dom)
     res = {
         "metric": METRIC, "value": cfg.tokens / (ms * 1e-3), "unit": "tokens/s",
         "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": ms,

@@ -284,6 +284,7 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
     constexpr int XV = HP * P / 4, XI = Q * XV / THREADS;   // float4 per x row, per thread
     constexpr int BV = F32_NB / 4, BI = Q * BV / THREADS;
     static_assert(Q * XV % THREADS == 0 && Q * BV % THREADS == 0, "even staging split");
+    static_assert(!NT || 2 * Q * (XROW + BROW) >= (THREADS / 64) * 4096, "output staging fits the planes");
     float4 xf[XI], bf[BI];
     {
         const float* xsrc = reinterpret_cast<const float*>(a.x) + (tok0 * H + h0) * P;
@@ -425,18 +426,47 @@ __global__ void __launch_bounds__(THREADS) k_chunk_state_f32(StateArgs a) {
         }
     }
     // lane: p-tile pt0 + i, p = 16 (pt0 + i) + ln over the heads, n = 16 (nt0 + j) + 4 kg .. + 3
+    if constexpr (NT) {
+        // non-temporal stores of whole row pieces (64 columns, 256 bytes): each
+        // wavefront stages the 16 rows of its p-tile in 4 KB of the (no longer
+        // read) plane LDS, 16-byte piece 4 j + kg of row ln XOR-swizzled by the
+        // row, and reads them back 16 lanes per row.  The region is this
+        // wavefront's alone; its LDS operations complete in order, and the
+        // waits keep the compiler from moving the accesses across each other.
+        __syncthreads();
+        char* sw = smem + w * 4096;
 #pragma unroll
-    for (int i = 0; i < PTW; ++i) {
-        const int pr = 16 * (pt0 + i) + ln;
-        const int hh = pr / P, pp = pr % P;
-        float* op = a.out + ((((int64_t)bi * nc + c) * H + h0 + hh) * P + pp) * N + nb * F32_NB;
+        for (int i = 0; i < PTW; ++i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float* const dst = op + 16 * (nt0 + j) + 4 * kg;
-            if constexpr (NT)
-                __builtin_nontemporal_store(acc[j][i], reinterpret_cast<f32x4*>(dst));
-            else
-                *reinterpret_cast<float4*>(dst) = make_float4(acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]);
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<f32x4*>(sw + ln * 256 + 16 * ((4 * j + kg) ^ ln)) = acc[j][i];
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            f32x4 v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = 4 * q + (lane >> 4);
+                v[q] = *reinterpret_cast<const f32x4*>(sw + r * 256 + 16 * ((lane & 15) ^ r));
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int pr = 16 * (pt0 + i) + 4 * q + (lane >> 4);
+                const int hh = pr / P, pp = pr % P;
+                float* const dst = a.out + ((((int64_t)bi * nc + c) * H + h0 + hh) * P + pp) * N +
+                                   nb * F32_NB + 16 * nt0 + 4 * (lane & 15);
+                __builtin_nontemporal_store(v[q], reinterpret_cast<f32x4*>(dst));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < PTW; ++i) {
+            const int pr = 16 * (pt0 + i) + ln;
+            const int hh = pr / P, pp = pr % P;
+            float* op = a.out + ((((int64_t)bi * nc + c) * H + h0 + hh) * P + pp) * N + nb * F32_NB;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                *reinterpret_cast<float4*>(op + 16 * (nt0 + j) + 4 * kg) =
+                    make_float4(acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]);
         }
     }
 }
@@ -454,7 +484,7 @@ int launch_chunk_state_f32(const StateArgs& sa, int64_t bhc, hipStream_t s, bool
     if (shm > 160 * 1024)
         return m2::set_error(M2_ERR_UNSUPPORTED, "chunk_state (fp32 planes): %zu B of LDS", shm);
     // The combined forward's chunk states (cumsum folded in) leave
-    // non-temporally when they are small (at most 16 MiB; the fp32 mamba2-130m
+    // non-temporally, as whole row pieces staged in LDS, when they are small (at most 16 MiB; the fp32 mamba2-130m
     // layer: 12 MiB): this kernel 10.6 against 11.6 us, the layer 33.8 against
     // 34.4 us (A/B on one box), no dirty lines remaining in L2 for the end of
     // the kernel; at 24 / 48 MiB the state passing that reads them next lost

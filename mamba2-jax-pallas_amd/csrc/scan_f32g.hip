@@ -545,6 +545,9 @@ static int launch_common(GArgs& k, int64_t batch, int64_t dstate, bool cbb, hipS
     // 8, rows 24-192 MiB: layer 36.7 -> 35.3, 52.7 -> 50.6, 84.9 -> 84.5,
     // 157.8 -> 152.1 us); where they do not (the nemotron-h-8b shape in fp32:
     // rows of 256 MiB), ordinary ones measure better (0.1886 against 0.1924 ms).
+    // The non-temporal 64-byte row pieces reach HBM unmerged (c0: 18.6 instead
+    // of 12.6 MB written); staging the tiles in LDS so that whole lines leave
+    // measured slower (c0 scan 16.3 -> 16.8 us, batch 8: 76.7 -> 79.5 us).
     const double rows = (double)batch * k.L * k.H * P * 4 + (double)batch * k.nc * k.H * P * dstate * 4;
     const bool nt = rows <= 224.0 * (1 << 20);
     k.hps = scan_f32g_heads_per_wg(batch, k.nc, k.G, k.hpg, dstate, cbb);

@@ -97,13 +97,21 @@ def test_traffic_files_name_the_reported_stages(name):
         cfg = dataclasses.replace(cfg, dtype="f32")
     stages = set(bench.stage_work(cfg, with_init=cfg.init_state))
     # chunk_state_varlen (c3) runs after the five stage intervals
-    measured = {k for k in t if k not in ("config", "unit", "source", "chunk_state_varlen")}
+    measured = {k for k in t if k not in ("config", "unit", "source", "chunk_state_varlen",
+                                          "above_algorithmic")}
     assert measured <= stages, measured - stages
     # the dominant stage of every configuration carries a measurement
     w = bench.stage_work(cfg, with_init=cfg.init_state)
     assert max(w, key=lambda s: w[s][0]) in measured
-    for k in measured:      # within 5 % of the algorithmic bytes
-        assert abs(t[k] - w[k][0]) <= 0.05 * w[k][0], (k, t[k], w[k][0])
+    # within 5 % of the algorithmic bytes, or up to 20 % above them for a stage
+    # whose excess the file explains
+    excess = t.get("above_algorithmic", {})
+    assert set(excess) <= measured and all(isinstance(v, str) and v for v in excess.values())
+    for k in measured:
+        if k in excess:
+            assert w[k][0] <= t[k] <= 1.2 * w[k][0], (k, t[k], w[k][0])
+        else:
+            assert abs(t[k] - w[k][0]) <= 0.05 * w[k][0], (k, t[k], w[k][0])
 
 
 def test_more_than_one_gpu_is_refused():
