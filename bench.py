@@ -624,9 +624,12 @@ def bench_other_config(name, steps=50, warmup=20, cpu=True):
     from mamba2_jax import configs
     cfg = configs.CONFIGS[name]
     kw = _layer_inputs(cfg)
-    # the event pass first (>= 300 steps): it brings the GPU back to its
-    # steady clocks after the host-side input generation
-    nev = max(steps, 300)
+    # the event pass first: it brings the GPU back to its steady clocks after
+    # the host-side input generation, which takes ~30 ms of continuous work;
+    # >= 300 steps and >= 40 ms by a short timing first (a small layer such as
+    # c0's, ~35 us, needs ~1100 steps)
+    est, _ = time_layer(kw, 20, 5)
+    nev = max(steps, 300, int(40.0 / max(est, 1e-3)))
     finish = stage_table_enqueue(cfg, kw, nev, stage_events(cfg, nev))
     ms, _ = time_layer(kw, steps, warmup)
     stages, dom, roof, _, tot_by = finish()
