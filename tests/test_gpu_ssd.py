@@ -102,6 +102,23 @@ def test_c0_full_fp32():
     _run_and_check(configs.CONFIGS["c0"])
 
 
+def test_c0_shape_fp32_batch2():
+    """The c0 shape at batch 2: chunk and passed states of 24 MiB, above the
+    16 MiB up to which they are stored non-temporally (c0 itself: 12 MiB), so
+    the ordinary-store forms of the fp32 chunk_state and state walk run."""
+    announce("c0 shape fp32 batch 2")
+    _run_and_check(dataclasses.replace(configs.CONFIGS["c0"], batch=2))
+
+
+def test_c2_shape_fp32_full():
+    """The nemotron-h-8b shape in fp32 (the reference's published conditions):
+    x and the passed states (256 MiB) exceed what the group scan stores its
+    output non-temporally for, so its ordinary-store form runs, after the
+    fused fp32 state pass."""
+    announce("c2 shape fp32 full")
+    _run_and_check(dataclasses.replace(configs.CONFIGS["c2"], dtype="f32"))
+
+
 def test_c2_full_headline():
     announce("c2 full (nemotron-h-8b, headline)")
     _run_and_check(configs.CONFIGS["c2"])
