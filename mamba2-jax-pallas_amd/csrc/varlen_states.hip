@@ -131,13 +131,17 @@ __global__ void __launch_bounds__(256 * HPW) k_varlen_states(VarlenArgs a) {
     const bf16* xsrc = a.x + (int64_t)h0 * P;
     const bf16* bsrc = a.B + (int64_t)g * N + NB * nb;
     const uint32_t xl = lds_addr(xs);
-    for (int u = w; u < Q * XCPR / 64; u += THREADS / 64) {
+    // only the 32-position K steps that hold [qlo, qhi) (the varlen sequence's
+    // part of the chunk) are loaded and multiplied; their other rows are
+    // loaded as usual and weighted 0
+    const int ks_lo = qlo / 32, ks_hi = (qhi + 31) / 32;
+    for (int u = w + ks_lo * 32 * XCPR / 64; u < ks_hi * 32 * XCPR / 64; u += THREADS / 64) {
         const int gi = 64 * u + lane, r = gi / XCPR;
         const int64_t t = min(t0 + r, tend);
         const int col = ((gi % XCPR) ^ swz<XROW>(r)) * 8;
         dma16(xsrc + t * H * P + col, xl + 1024 * u);
     }
-    for (int u = w; u < Q * BCPR / 64; u += THREADS / 64) {
+    for (int u = w + ks_lo * 32 * BCPR / 64; u < ks_hi * 32 * BCPR / 64; u += THREADS / 64) {
         const int gi = 64 * u + lane, r = gi / BCPR;
         const int64_t t = min(t0 + r, tend);
         const int col = ((gi % BCPR) ^ swz<2 * NB>(r)) * 8;
@@ -199,7 +203,7 @@ __global__ void __launch_bounds__(256 * HPW) k_varlen_states(VarlenArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[j] = zero4();
     // the row swizzle repeats every 8 rows, so step ks is step 0 moved by 32 rows
-    for (int ks = 0; ks < Q / 32; ++ks) {
+    for (int ks = ks_lo; ks < ks_hi; ++ks) {
         const float wl = wq[hh * Q + wpos + 32 * ks];
         const float wv[8] = {row_bcast<0>(wl), row_bcast<1>(wl), row_bcast<2>(wl), row_bcast<3>(wl),
                              row_bcast<4>(wl), row_bcast<5>(wl), row_bcast<6>(wl), row_bcast<7>(wl)};
