@@ -220,12 +220,22 @@ def load_library(path=LIB_PATH):
         return lib
 
 
+_fns = {}
+
+
 def call(name, args, stream):
     """Call entry point `name` with a filled argument struct on `stream`."""
-    lib = load_library()
-    rc = getattr(lib, name)(ctypes.byref(args), ctypes.c_void_p(stream))
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(load_library(), name)
+    rc = fn(ctypes.byref(args), stream)
     if rc != 0:
-        raise M2Error(name, rc, lib.m2_last_error().decode(errors="replace"))
+        raise M2Error(name, rc, load_library().m2_last_error().decode(errors="replace"))
+
+
+# Bumped on every override change: results cached against the library's
+# shape-based choices (the combined forward's workspace size) include it.
+_override_epoch = 0
 
 
 @contextlib.contextmanager
@@ -233,15 +243,22 @@ def dispatch_override(knob, choice):
     """Testing hook: force one of the library's shape-based kernel choices
     (KNOBS) inside the block, process-wide; the automatic choice is restored
     after it.  A forced choice the shape cannot take is ignored by the library."""
+    global _override_epoch
     lib = load_library()
     k, values = KNOBS[knob]
     prev = lib.m2_set_dispatch_override(k, values[choice])
     if prev < 0:
         raise M2Error("m2_set_dispatch_override", prev, lib.m2_last_error().decode())
+    _override_epoch += 1
     try:
         yield
     finally:
         lib.m2_set_dispatch_override(k, prev)
+        _override_epoch += 1
+
+
+def override_epoch():
+    return _override_epoch
 
 
 # ---------------------------------------------------------------------------
@@ -278,22 +295,22 @@ def require(cond, msg):
 
 def device_of(*tensors):
     """The common GPU device of the given tensors (None entries ignored)."""
-    dev = None
+    first, idx = None, -1
     for t in tensors:
         if t is None:
             continue
         if not isinstance(t, torch.Tensor):
             raise TypeError(f"expected a torch.Tensor, got {type(t).__name__}")
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise ValueError(
                 f"tensor on {t.device}: the HIP kernels need GPU tensors (there is no CPU path)")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
-    if dev is None:
+        if first is None:
+            first, idx = t, t.get_device()
+        elif t.get_device() != idx:
+            raise ValueError(f"tensors on different devices: {first.device} and {t.device}")
+    if first is None:
         raise ValueError("no GPU tensor given")
-    return dev
+    return first.device
 
 
 def dev_contig(t, dtype=None):
@@ -313,5 +330,11 @@ def ptr(t):
     return 0 if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device):
+    """The raw handle of `device`'s current stream."""
+    if _raw_stream is not None and device.index is not None:
+        return _raw_stream(device.index)
     return torch.cuda.current_stream(device).cuda_stream
