@@ -289,8 +289,10 @@ def torch_dtype(d):
 
 
 def require(cond, msg):
+    """Raise M2ShapeError(msg) unless cond; msg may be a callable that builds
+    the message (formatted only on failure)."""
     if not cond:
-        raise M2ShapeError(msg)
+        raise M2ShapeError(msg() if callable(msg) else msg)
 
 
 def device_of(*tensors):

@@ -32,8 +32,8 @@ def _io_dtype(*ts):
 def _seq_idx(seq_idx, batch, seqlen):
     if seq_idx is None:
         return None
-    L.require(tuple(seq_idx.shape) == (batch, seqlen),
-              f"seq_idx.shape={tuple(seq_idx.shape)} != ({batch}, {seqlen})")
+    L.require(seq_idx.shape == (batch, seqlen),
+              lambda: f"seq_idx.shape={tuple(seq_idx.shape)} != ({batch}, {seqlen})")
     return L.dev_contig(seq_idx, torch.int32)
 
 

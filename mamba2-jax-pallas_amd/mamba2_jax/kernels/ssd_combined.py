@@ -62,22 +62,23 @@ def mamba_chunk_scan_combined_fwd(x, dt, A, B, C, chunk_size, D=None, z=None, dt
     L.device_of(x, dt, A, B, C, D, z, dt_bias, initial_states, seq_idx, cu_seqlens)
     L.require(x.dim() == 4, "x must be (batch, seqlen, nheads, headdim)")
     batch, seqlen, nheads, headdim = x.shape
-    L.require(B.dim() == 4 and tuple(B.shape[:2]) == (batch, seqlen),
+    L.require(B.dim() == 4 and B.shape[:2] == x.shape[:2],
               "B must be (batch, seqlen, ngroups, dstate)")
     _, _, ngroups, dstate = B.shape
-    L.require(tuple(C.shape) == tuple(B.shape), "C.shape != B.shape")
-    L.require(tuple(dt.shape) == (batch, seqlen, nheads), f"dt.shape={tuple(dt.shape)}")
-    L.require(tuple(A.shape) == (nheads,), f"A.shape={tuple(A.shape)} != ({nheads},)")
+    L.require(C.shape == B.shape, "C.shape != B.shape")
+    L.require(dt.shape == x.shape[:3], lambda: f"dt.shape={tuple(dt.shape)}")
+    L.require(A.shape == (nheads,), lambda: f"A.shape={tuple(A.shape)} != ({nheads},)")
     L.require(nheads % ngroups == 0, "nheads must be a multiple of ngroups")
     if dt_bias is not None:
-        L.require(tuple(dt_bias.shape) == (nheads,), f"dt_bias.shape={tuple(dt_bias.shape)}")
+        L.require(dt_bias.shape == (nheads,), lambda: f"dt_bias.shape={tuple(dt_bias.shape)}")
     if D is not None:
-        L.require(tuple(D.shape) in ((nheads,), (nheads, headdim)), f"D.shape={tuple(D.shape)}")
+        L.require(D.shape == (nheads,) or D.shape == (nheads, headdim),
+                  lambda: f"D.shape={tuple(D.shape)}")
     if z is not None:
-        L.require(tuple(z.shape) == tuple(x.shape), "z.shape != x.shape")
+        L.require(z.shape == x.shape, "z.shape != x.shape")
     if initial_states is not None:
-        L.require(tuple(initial_states.shape) == (batch, nheads, headdim, dstate),
-                  f"initial_states.shape={tuple(initial_states.shape)}")
+        L.require(initial_states.shape == (batch, nheads, headdim, dstate),
+                  lambda: f"initial_states.shape={tuple(initial_states.shape)}")
     chunk_size = int(chunk_size)
     L.require(chunk_size > 0, "chunk_size must be positive")
     if not return_varlen_states:
