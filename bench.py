@@ -564,14 +564,20 @@ def _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc):
     import torch
     torch.cuda.synchronize()
 
-    def slot(j):
-        # interval j: from event j (or the last recorded one before it) to event j + 1
-        a = max(x for x in range(j + 1) if keep[x])
-        if not keep[j + 1]:
+    # the library records the events in stream order `order` (with bf16 and
+    # the fused scan the varlen states run right after state_passing: event 6
+    # comes before events 4 and 5)
+    order = [0, 1, 2, 3, 6, 4, 5] if keep[6] and fc and cfg.dtype == "bf16" else [0, 1, 2, 3, 4, 5, 6]
+    rec = [e for e in order if keep[e]]
+
+    def slot(e):
+        # the interval ending at event e: from the last recorded event before it
+        if not keep[e]:
             return 0.0
-        return float(np.mean([hev.elapsed_ms(evs[i][a], evs[i][j + 1]) for i in range(steps)]))
-    slot_ms = [slot(j) for j in range(6 if keep[6] else 5)]
-    last = 6 if keep[6] else 5
+        a = rec[rec.index(e) - 1]
+        return float(np.mean([hev.elapsed_ms(evs[i][a], evs[i][e]) for i in range(steps)]))
+    slot_ms = [slot(e) for e in range(1, 7 if keep[6] else 6)]
+    last = rec[-1]
     total = float(np.mean([hev.elapsed_ms(evs[i][0], evs[i][last]) for i in range(steps)]))
     cu = kw.get("cu_seqlens")
     work = stage_work(cfg, with_init=kw["initial_states"] is not None,

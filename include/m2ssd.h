@@ -211,7 +211,10 @@ typedef struct {
                                        hipEvent_t recorded before stage 1,
                                        after each of the 5 stages and after
                                        the varlen states (when requested); a
-                                       NULL entry is not recorded           */
+                                       NULL entry is not recorded.  With bf16
+                                       and the fused scan the varlen states
+                                       run after state_passing, so event 6
+                                       is recorded before events 4 and 5    */
 } m2_ssd_combined_args;
 size_t m2_ssd_combined_workspace_size(const m2_ssd_combined_args* a);
 int m2_ssd_combined(const m2_ssd_combined_args* a, void* stream);

@@ -206,6 +206,12 @@ M2_DEV void dma16(const void* g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                  ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
 }
+// the same with a non-temporal hint: rows read once that should not displace
+// cached data
+M2_DEV void dma16nt(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off nt"
+                 ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");
+}
 M2_DEV void dma4(const void* g, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                  ::"s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g) : "memory", "m0");

@@ -74,6 +74,7 @@ struct ScanFusedArgs {
     int D_has_hdim, cb_bf16;
     int L, H, G, nc, hpg, nwork;
     int hps, nslice;          // heads per workgroup (a slice of the group's), slices
+    int ntl;                  // chunk-128 kernel: x / state rows loaded non-temporally
 };
 // the chunk-128 scan kernel (csrc/ssd_scan128.hip) for dstate 32 * ns (ns 2, 4,
 // 8), with the z gate / with CB given / with non-temporal output stores (not

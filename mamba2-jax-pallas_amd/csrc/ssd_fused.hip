@@ -629,6 +629,14 @@ int launch_scan_fused_common(ScanFusedArgs& f, const Sizes& a, bool hz, bool cbi
     // layer, c1 0.135 -> 0.120 ms.  Larger outputs (c3: 537 MB) stream better
     // as ordinary stores (0.637 against 0.645 ms).
     const bool nt = (double)a.batch * a.seqlen * a.nheads * a.headdim * 4 <= 256.0 * (1 << 20);
+    // States entering the chunks beyond the cache (c3: 537 MB of bf16) are
+    // read once here: the chunk-128 kernel loads them and x non-temporally, so
+    // they do not displace what the cache still holds (A/B on one box at c3:
+    // scan 302 -> 262 us; with the varlen states moved before the scan, layer
+    // 0.553 -> 0.525 ms).  At c1 / c2 (states in the cache) the same loads
+    // cost the next call's state pass more than the scan gains (c2 0.092 ->
+    // 0.105 ms).
+    f.ntl = (double)a.batch * nc * a.nheads * a.headdim * a.dstate * 2 > 256.0 * (1 << 20);
     void (*kern)(ScanFusedArgs) = nullptr;
     // chunk 128: the kernel with per-wavefront compile-time unit lists
     // (csrc/ssd_scan128.hip); chunk 64: k_scan_fused

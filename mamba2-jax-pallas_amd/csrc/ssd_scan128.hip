@@ -518,6 +518,8 @@ __global__ void __launch_bounds__(THREADS) k_scan_q128(ScanFusedArgs a) {
     const int li = w - NWAVES;
     const int64_t cq0 = ((int64_t)bi * H * nc + ci) * Q;  // dA / dt row of head 0 (+ h nc Q)
     const int64_t st0 = ((int64_t)bi * nc + ci) * H * P * N;
+    // x and state rows non-temporally where the states exceed the cache
+    const bool ntl = a.ntl;
     auto issue = [&](int j, int k) {
         const int h = h0 + j;
         const uint32_t sb = ring_lds + k * SLOT;
@@ -526,14 +528,17 @@ __global__ void __launch_bounds__(THREADS) k_scan_q128(ScanFusedArgs a) {
             const int u = li * S::XL + uu;
             const int gi = 64 * u + lane, r = gi / 8;
             const int64_t off = (tok0 + min(r, valid - 1)) * H * P + h * P + 8 * ((gi % 8) ^ xswz(r));
-            dma16(a.x + off, sb + 1024 * u);
+            if (ntl) dma16nt(a.x + off, sb + 1024 * u);
+            else dma16(a.x + off, sb + 1024 * u);
         }
         const bf16* sp = a.states + st0 + (int64_t)h * P * N;
 #pragma unroll
         for (int uu = 0; uu < S::SL; ++uu) {
             const int u = li * S::SL + uu;
             const int gi = 64 * u + lane, p = gi / SCPR;
-            dma16(sp + p * N + 8 * ((gi % SCPR) ^ sswz<SCPR>(p)), sb + XB + 1024 * u);
+            const bf16* src = sp + p * N + 8 * ((gi % SCPR) ^ sswz<SCPR>(p));
+            if (ntl) dma16nt(src, sb + XB + 1024 * u);
+            else dma16(src, sb + XB + 1024 * u);
         }
         const int64_t row = cq0 + (int64_t)h * nc * Q;
         if (li == 0 && lane < Q / 2) {
