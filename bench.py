@@ -109,16 +109,17 @@ def stage_work(cfg, with_init=False, with_z=False, cu_seqlens=None):
                            + s * S + 4 * b * H * P * N + (4 * b * H * P * N if with_init else 0),
                            2 * b * L * H * P * N + 2 * S)
     if cu_seqlens is not None:
-        # per sequence: x and B rows of its last chunk, that chunk's dA_cumsum /
-        # dt', the state entering it (when the sequence started earlier) and
-        # the fp32 final state out
+        # per sequence: the x and B rows of its part of its last chunk, their
+        # dA_cumsum / dt', the state entering that chunk (when the sequence
+        # started earlier) and the fp32 final state out
         cu = [int(v) for v in cu_seqlens]
         by = fl = 0
         for s0, s1 in zip(cu[:-1], cu[1:]):
             c0 = (s1 - 1) // Q * Q
-            by += (Q * H * P + Q * G * N) * s + 8 * H * Q + 4 * H * P * N
+            rows = s1 - max(s0, c0)
+            by += (rows * H * P + rows * G * N) * s + 8 * H * rows + 4 * H * P * N
             by += s * H * P * N if s0 < c0 else 0
-            fl += 2 * 2 * (s1 - max(s0, c0)) * H * P * N
+            fl += 2 * 2 * rows * H * P * N
         w[VARLEN] = (by, fl)
     return w
 
