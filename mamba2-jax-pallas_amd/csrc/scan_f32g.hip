@@ -140,7 +140,8 @@ template <bool NT> M2_DEV void store_f4(const f32x4& v, float* p) {
 // CBB: CB = C B^T (seq_idx-masked) is built here from the group's B rows,
 // which pass through the second ring slot (as hi / lo planes laid out like
 // the state rows) before the second head is loaded: the layer then needs no
-// bmm_chunk launch and no CB buffer.  NT: non-temporal output stores.
+// bmm_chunk launch and no CB buffer.  NT: non-temporal output stores; without
+// them, x and the state rows are loaded non-temporally.
 template <int NS, bool HASZ, bool CBB, bool NT>
 __global__ void __launch_bounds__(THREADS) k_scan_f32g(GArgs a) {
     typedef GCfg<NS> Cf;
@@ -179,13 +180,15 @@ __global__ void __launch_bounds__(THREADS) k_scan_f32g(GArgs a) {
             for (int uu = 0; uu < XI; ++uu) {
                 const int u = li * XI + uu;
                 const int r = min(4 * u + (lane >> 4), valid - 1);   // past the end: weight 0
-                dma16(xsrc + (int64_t)r * H * P + 4 * (lane & 15), sb + 1024 * u);
+                if constexpr (!NT) dma16nt(xsrc + (int64_t)r * H * P + 4 * (lane & 15), sb + 1024 * u);
+                else dma16(xsrc + (int64_t)r * H * P + 4 * (lane & 15), sb + 1024 * u);
             }
             const float* ssrc = a.states + (((int64_t)bi * nc + c) * H + h) * (int64_t)P * N;
 #pragma unroll
             for (int uu = 0; uu < SI; ++uu) {
                 const int u = li * SI + uu;
-                dma16(ssrc + (int64_t)(Cf::SRPI * u) * N + 4 * lane, sb + XB + 1024 * u);
+                if constexpr (!NT) dma16nt(ssrc + (int64_t)(Cf::SRPI * u) * N + 4 * lane, sb + XB + 1024 * u);
+                else dma16(ssrc + (int64_t)(Cf::SRPI * u) * N + 4 * lane, sb + XB + 1024 * u);
             }
             const int64_t q0 = (((int64_t)bi * H + h) * nc + c) * Q;
             const uint32_t ab = sb + XB + SB;
@@ -548,6 +551,9 @@ static int launch_common(GArgs& k, int64_t batch, int64_t dstate, bool cbb, hipS
     // The non-temporal 64-byte row pieces reach HBM unmerged (c0: 18.6 instead
     // of 12.6 MB written); staging the tiles in LDS so that whole lines leave
     // measured slower (c0 scan 16.3 -> 16.8 us, batch 8: 76.7 -> 79.5 us).
+    // Where the rows do not fit, the kernel instead loads x and the states
+    // non-temporally (read once here): nemotron-h-8b shape in fp32 0.1920 ->
+    // 0.1886 ms (A/B on one box).
     const double rows = (double)batch * k.L * k.H * P * 4 + (double)batch * k.nc * k.H * P * dstate * 4;
     const bool nt = rows <= 224.0 * (1 << 20);
     k.hps = scan_f32g_heads_per_wg(batch, k.nc, k.G, k.hpg, dstate, cbb);
