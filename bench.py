@@ -624,7 +624,7 @@ def _stage_table_finish(cfg, kw, steps, hev, evs, keep, fs, fc):
     return stages, dom, roof, total, sum(w[0] for w in work.values())
 
 
-def bench_other_config(name, steps=50, warmup=20, cpu=True):
+def bench_other_config(name, steps=200, warmup=20, cpu=True):
     """One more BASELINE configuration measured in the same run: ms per layer,
     tokens/s, the per-kernel table with its dominant kernel's roofline, and a
     sampled CPU baseline."""
