@@ -68,8 +68,8 @@ template <int KB>
 struct StCfg {
     // LDS stage slots, DEPTH - 1 stages in flight.  128-position stages: one
     // in flight measures faster than two (c2: 42.7-43.6 against 44.6-45.2 us by
-    // events, A/B on one box): fewer loads queued per CU against the same
-    // per-CU intake, and three in flight (an early slot release) is slower again
+    // events, A/B on one box), and three in flight (an early slot release) is
+    // slower again; 64-position stages with three or four slots: 50.9-51.7 us
     static constexpr int DEPTH = KB == 64 ? 6 : 2;
     static constexpr int XB = KB * P * 2, BB = KB * NB * 2;   // tile bytes
     static constexpr int AUXB = KB * 4 + 256;        // weights, 64 copies of the decay
@@ -337,12 +337,13 @@ template <int RB> M2_DEV int rswz(int R) { return RB == 128 ? ((R >> 1) & 3) << 
 // ---------------------------------------------------------------------------
 // k_ssd_pair: the same pass with one workgroup per (batch, pair of heads of a
 // group, NB-column dstate block), for shapes with enough such workgroups to
-// fill the CUs.  A CU pulls at most ~16 bytes per clock from L2 / HBM, and
-// the pass is bound by that rate (with the compute wavefronts running, the
-// load wavefronts issue at ~10-14 bytes per clock): two heads share each B
-// row the CU brings in, and 128-column blocks bring x in once per 128
-// columns, so a pair moves 16 (NB 128) or 24 (NB 64) KB into the CU per head,
-// 64 columns and 128 positions, against 32 KB for the kernel above.
+// fill the CUs.  Two heads share each B row the CU brings in, and 128-column
+// blocks bring x in once per 128 columns, so a pair moves 16 (NB 128) or 24
+// (NB 64) KB into the CU per head, 64 columns and 128 positions, against 32 KB
+// for the kernel above, and does twice a head's MFMA work per stage.  At c3
+// the pass is HBM-bound (a build without MFMAs takes the same 218 us: 866 MB
+// at 4.0 TB/s, against ~5-6 TB/s for plain HBM streams); at c1, with 160
+// workgroups on 160 CUs, the MFMA work adds ~18 us to the 34 us of memory.
 // Compute wavefront w owns head (w >> 2) of the pair, head-dim rows
 // 16 (w & 3) .. +15 and all NB columns, and takes every position of a stage
 // (no position halves, so no exchange): each x element is weighted by one
