@@ -343,7 +343,7 @@ template <int RB> M2_DEV int rswz(int R) { return RB == 128 ? ((R >> 1) & 3) << 
 // for the kernel above, and does twice a head's MFMA work per stage.  At c3
 // the pass is HBM-bound (a build without MFMAs takes the same 218 us: 866 MB
 // at 4.0 TB/s, against ~5-6 TB/s for plain HBM streams); at c1, with 160
-// workgroups on 160 CUs, the MFMA work adds ~18 us to the 34 us of memory.
+// workgroups on 160 CUs, the compute alone takes 42.5 us, the memory 34 us.
 // Compute wavefront w owns head (w >> 2) of the pair, head-dim rows
 // 16 (w & 3) .. +15 and all NB columns, and takes every position of a stage
 // (no position halves, so no exchange): each x element is weighted by one
