@@ -70,6 +70,8 @@ NORM_CASES = [
     (4, 64, 40, "bf16", False, 16, True, False),
     (16, 768, 3352, "f32", False, None, True, False),     # 130m pre-norm, batch 16
     (11, 1536, 768, "f32", True, 768, False, True),       # 130m-like gated norm, 2 groups
+    (2, 1536, 768, "bf16", True, None, True, True),       # one group, bf16 rows, gate after
+    (1, 5120, 2560, "f32", True, None, True, False),      # one group, gate after the norm
 ]
 
 
